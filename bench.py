@@ -1,0 +1,388 @@
+#!/usr/bin/env python3
+"""Benchmark of the LLAISYS per-layer ops on one MI355X.
+
+Workload (the shape the metric is quoted on): Qwen2-1.5B layer ops in
+bf16 at 8192 tokens -- embedding gather from [151936, 1536], rms_norm [8192, 1536], fused
+residual add + rms_norm [8192, 1536], rope on q [8192, 12, 128] and k [8192, 2, 128],
+swiglu [8192, 8960] and argmax over [1, 151936].  One step = one launch of each op over one
+buffer set; 4 disjoint buffer sets (about 2.6 GB) rotate so that no step finds its inputs in
+the 256 MB Infinity Cache.  Inputs are synthetic (seeded normal samples, the table
+N(0, 0.02), norm weight N(1, 0.1)) and resident in HBM before timing starts.
+
+value = algorithmic HBM bytes of the step (every input read once, every output written
+once) / step time, in GB/s.  Per-op GB/s, the config-4 28-layer chain (2048-token prefill)
+tokens/s, the roofline of the dominant kernel (swiglu) and the reference CPU ops timed on
+this host are reported in the same JSON line.  Timing uses HIP events recorded on the
+library's own stream (llaisysGetContextStream).
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "achieved HBM GB/s (% of MI355X peak) per op; layer-op tokens/s at Qwen2-1.5B"
+PEAK_GBS = 8000.0  # MI355X HBM3E
+
+T, H, V, NH, NKV, D, I = 8192, 1536, 151936, 12, 2, 128, 8960
+NSETS = 4
+
+
+class HipEvents:
+    """hipEvent timing through the HIP runtime already loaded by libllaisys.so."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+
+    def event(self):
+        ev = ctypes.c_void_p()
+        assert self.hip.hipEventCreate(ctypes.byref(ev)) == 0
+        return ev
+
+    def record(self, ev, stream):
+        assert self.hip.hipEventRecord(ev, ctypes.c_void_p(stream)) == 0
+
+    def elapsed_ms(self, a, b):
+        assert self.hip.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+
+def bf16(rng, shape, scale=1.0, loc=0.0):
+    from llaisys_amd.hostfmt import f32_to_bf16
+    return f32_to_bf16(loc + scale * rng.standard_normal(shape, dtype=np.float32))
+
+
+class Workload:
+    """Device buffers of the config-1 step: 4 rotating sets plus the shared table."""
+
+    def __init__(self, L, seed=1):
+        BF, I64 = L.DataType.BF16, L.DataType.I64
+        dev = dict(device=L.DeviceType.AMD, device_id=0)
+        rng = np.random.default_rng(seed)
+        self.L = L
+        self.table = L.Tensor.from_numpy(bf16(rng, (V, H), 0.02), BF, **dev)
+        self.w = L.Tensor.from_numpy(bf16(rng, (H,), 0.1, 1.0), BF, **dev)
+        self.pos = L.Tensor.from_numpy(np.arange(T, dtype=np.int64), **dev)
+        host = {
+            "x": bf16(rng, (T, H)), "r": bf16(rng, (T, H)),
+            "q": bf16(rng, (T, NH, D)), "k": bf16(rng, (T, NKV, D)),
+            "gate": bf16(rng, (T, I)), "up": bf16(rng, (T, I)),
+            "logits": bf16(rng, (1, V)),
+        }
+        api = L.RuntimeAPI(L.DeviceType.AMD)
+        self.sets = []
+        for s in range(NSETS):
+            b = {"ids": L.Tensor.from_numpy(rng.integers(0, V, size=T).astype(np.int64), **dev)}
+            for name, arr in host.items():
+                if s == 0:
+                    b[name] = L.Tensor.from_numpy(arr, BF, **dev)
+                else:  # same values, distinct addresses
+                    b[name] = L.Tensor(arr.shape, BF, **dev)
+                    api.memcpy_sync(b[name].data_ptr(), self.sets[0][name].data_ptr(), arr.nbytes,
+                                    L.MemcpyKind.D2D)
+            for name, shape in (("emb", (T, H)), ("y_rms", (T, H)), ("y", (T, H)), ("h", (T, H)),
+                                ("q_out", (T, NH, D)), ("k_out", (T, NKV, D)), ("act", (T, I))):
+                b[name] = L.Tensor(shape, BF, **dev)
+            b["idx"] = L.Tensor((1,), I64, **dev)
+            b["val"] = L.Tensor((1,), BF, **dev)
+            self.sets.append(b)
+
+    def ops(self):
+        """(name, algorithmic bytes per launch, launch(set)) of one step."""
+        O = self.L.Ops
+        tok = T * H * 2
+        return [
+            ("embedding", T * 8 + 2 * tok, lambda b: O.embedding(b["emb"], b["ids"], self.table)),
+            ("rms_norm", 2 * tok + H * 2, lambda b: O.rms_norm(b["y_rms"], b["x"], self.w, 1e-6)),
+            ("add_rms_norm", 4 * tok + H * 2,
+             lambda b: O.add_rms_norm(b["y"], b["h"], b["x"], b["r"], self.w, 1e-6)),
+            ("rope_q", 2 * T * NH * D * 2 + T * 8, lambda b: O.rope(b["q_out"], b["q"], self.pos, 1e4)),
+            ("rope_k", 2 * T * NKV * D * 2 + T * 8, lambda b: O.rope(b["k_out"], b["k"], self.pos, 1e4)),
+            ("swiglu", 3 * T * I * 2, lambda b: O.swiglu(b["act"], b["gate"], b["up"])),
+            ("argmax", V * 2 + 8 + 2, lambda b: O.argmax(b["idx"], b["val"], b["logits"])),
+        ]
+
+
+class Chain:
+    """Config 4: 28 Qwen2-1.5B layers of the per-layer ops at 2048 tokens, then the final
+    norm and argmax over [2048, 151936] logits.  Random activations stand in for the
+    GEMM / attention outputs; every layer has its own buffers."""
+
+    TOK, LAYERS, MAXSEQ = 2048, 28, 2048
+
+    def __init__(self, L, seed=4):
+        BF, I8, F32 = L.DataType.BF16, L.DataType.I8, L.DataType.F32
+        dev = dict(device=L.DeviceType.AMD, device_id=0)
+        rng = np.random.default_rng(seed)
+        t = self.TOK
+        api = L.RuntimeAPI(L.DeviceType.AMD)
+        self.L = L
+        self.pos = L.Tensor.from_numpy(np.arange(t, dtype=np.int64), **dev)
+        proto = {"attn": bf16(rng, (t, H)), "mlp": bf16(rng, (t, H)), "q": bf16(rng, (t, NH, D)),
+                 "k": bf16(rng, (t, NKV, D)), "v": bf16(rng, (t, NKV, D)),
+                 "gate": bf16(rng, (t, I)), "up": bf16(rng, (t, I))}
+        first = {k: L.Tensor.from_numpy(a, BF, **dev) for k, a in proto.items()}
+        self.layers = []
+        for layer in range(self.LAYERS):
+            b = {}
+            for k, a in proto.items():
+                if layer == 0:
+                    b[k] = first[k]
+                else:
+                    b[k] = L.Tensor(a.shape, BF, **dev)
+                    api.memcpy_sync(b[k].data_ptr(), first[k].data_ptr(), a.nbytes, L.MemcpyKind.D2D)
+            b["w1"] = L.Tensor.from_numpy(bf16(rng, (H,), 0.1, 1.0), BF, **dev)
+            b["w2"] = L.Tensor.from_numpy(bf16(rng, (H,), 0.1, 1.0), BF, **dev)
+            for k, shape in (("n1", (t, H)), ("n2", (t, H)), ("q_out", (t, NH, D)),
+                             ("k_out", (t, NKV, D)), ("act", (t, I))):
+                b[k] = L.Tensor(shape, BF, **dev)
+            for k in ("kc", "vc"):
+                b[k] = L.Tensor((self.MAXSEQ, NKV, D), I8, **dev)
+                b[k + "s"] = L.Tensor((self.MAXSEQ, NKV), F32, **dev)
+            self.layers.append(b)
+        self.resid = L.Tensor.from_numpy(bf16(rng, (t, H)), BF, **dev)
+        self.wf = L.Tensor.from_numpy(bf16(rng, (H,), 0.1, 1.0), BF, **dev)
+        self.final = L.Tensor((t, H), BF, **dev)
+        self.logits = L.Tensor.from_numpy(bf16(rng, (t, V)), BF, **dev)
+        self.tok_idx = L.Tensor((t,), L.DataType.I64, **dev)
+        self.tok_val = L.Tensor((t,), BF, **dev)
+
+    def bytes(self):
+        t, e = self.TOK, 2
+        norm = 4 * t * H * e + H * e
+        rope = 2 * t * (NH + NKV) * D * e + 2 * t * 8
+        kv = 2 * (t * NKV * D * e + t * NKV * D + t * NKV * 4)
+        swi = 3 * t * I * e
+        layer = 2 * norm + rope + kv + swi
+        return self.LAYERS * layer + (2 * t * H * e + H * e) + (t * V * e + t * 8 + t * e)
+
+    def run(self):
+        O = self.L.Ops
+        for b in self.layers:
+            O.add_rms_norm(b["n1"], self.resid, b["attn"], self.resid, b["w1"], 1e-6)
+            O.rope(b["q_out"], b["q"], self.pos, 1e6)
+            O.rope(b["k_out"], b["k"], self.pos, 1e6)
+            O.kv_append_int8(b["kc"], b["kcs"], b["k_out"], 0)
+            O.kv_append_int8(b["vc"], b["vcs"], b["v"], 0)
+            O.add_rms_norm(b["n2"], self.resid, b["mlp"], self.resid, b["w2"], 1e-6)
+            O.swiglu(b["act"], b["gate"], b["up"])
+        O.rms_norm(self.final, self.resid, self.wf, 1e-6)
+        O.argmax_rows(self.tok_idx, self.tok_val, self.logits)
+
+
+def cpu_baseline(seconds):
+    """Reference CPU ops (oracle/_ref, else the oracle port) on a row sample of config 1,
+    single thread pinned to one core; GB/s with the same bytes formula as the GPU."""
+    import oracle
+    rng = np.random.default_rng(7)
+    rows, srows, stok = 512, 128, 512
+    x, r = bf16(rng, (rows, H)), bf16(rng, (rows, H))
+    w = bf16(rng, (H,), 0.1, 1.0)
+    q, k = bf16(rng, (stok, NH, D)), bf16(rng, (stok, NKV, D))
+    pos = np.arange(stok, dtype=np.int64)
+    g, u = bf16(rng, (srows, I)), bf16(rng, (srows, I))
+    table = bf16(rng, (V, H), 0.02)
+    ids = rng.integers(0, V, size=T).astype(np.int64)
+    logits = bf16(rng, (1, V))
+    tok = rows * H * 2
+    work_bytes = ((T * 8 + 2 * T * H * 2) + (2 * tok + H * 2) + (4 * tok + H * 2)
+                  + (2 * stok * (NH + NKV) * D * 2 + 2 * stok * 8) + 3 * srows * I * 2 + (V * 2 + 10))
+    sample = (f"config-1 ops on a sample: embedding 8192 ids, rms_norm and add+rms_norm "
+              f"{rows} rows, rope q+k {stok} tokens, swiglu {srows} rows, argmax [1,{V}]")
+    ref = oracle.reference_library()
+    if ref is not None:
+        import llaisys_amd as L
+        from llaisys_amd.libllaisys import bind
+        bind(ref)
+        C, BF = L.DeviceType.CPU, L.DataType.BF16
+
+        def ht(a, dt=BF):
+            return L.Tensor.from_numpy(a, dt, device=C, lib=ref)
+
+        hx, hr, hw, hq, hk, hp = ht(x), ht(r), ht(w), ht(q), ht(k), ht(pos, L.DataType.I64)
+        hg, hu, htab, hid, hl = ht(g), ht(u), ht(table), ht(ids, L.DataType.I64), ht(logits)
+        o1, o2, o3 = (L.Tensor((rows, H), BF, C, lib=ref) for _ in range(3))
+        oq, ok = L.Tensor(q.shape, BF, C, lib=ref), L.Tensor(k.shape, BF, C, lib=ref)
+        og, oe = L.Tensor(g.shape, BF, C, lib=ref), L.Tensor((T, H), BF, C, lib=ref)
+        oi, ov = L.Tensor((1,), L.DataType.I64, C, lib=ref), L.Tensor((1,), BF, C, lib=ref)
+        f = ctypes.c_float
+
+        def step():
+            ref.llaisysEmbedding(oe.lib_tensor(), hid.lib_tensor(), htab.lib_tensor())
+            ref.llaisysRmsNorm(o1.lib_tensor(), hx.lib_tensor(), hw.lib_tensor(), f(1e-6))
+            ref.llaisysAdd(o2.lib_tensor(), hx.lib_tensor(), hr.lib_tensor())
+            ref.llaisysRmsNorm(o3.lib_tensor(), o2.lib_tensor(), hw.lib_tensor(), f(1e-6))
+            ref.llaisysROPE(oq.lib_tensor(), hq.lib_tensor(), hp.lib_tensor(), f(1e4))
+            ref.llaisysROPE(ok.lib_tensor(), hk.lib_tensor(), hp.lib_tensor(), f(1e4))
+            ref.llaisysSwiGLU(og.lib_tensor(), hg.lib_tensor(), hu.lib_tensor())
+            ref.llaisysArgmax(oi.lib_tensor(), ov.lib_tensor(), hl.lib_tensor())
+        kind = "reference"
+    else:
+        def step():
+            oracle.embedding(ids, table)
+            oracle.rms_norm(x, w, 1e-6)
+            oracle.add_rms_norm(x, r, w, 1e-6)
+            oracle.rope(q, pos, 1e4)
+            oracle.rope(k, pos, 1e4)
+            oracle.swiglu(g, u)
+            oracle.argmax(logits)
+        kind = "port"
+    saved = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {min(saved)})
+    try:
+        step()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            step()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+    finally:
+        os.sched_setaffinity(0, saved)
+    return {"value": round(work_bytes * n / el / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": sample + f"; {n} reps in {el:.1f} s", "cpu_model": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def traffic_of(kernel):
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, read from
+    profiles/traffic.txt ('<kernel> <fetch_bytes> <write_bytes>'), or None."""
+    path = ROOT / "profiles" / "traffic.txt"
+    if not path.is_file():
+        return None
+    for line in path.read_text().splitlines():
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == kernel:
+            return int(float(parts[1]) + float(parts[2]))
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-chain", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the per-layer "
+              "ops shard by rows with no exchange; see the sharding notes)", file=sys.stderr)
+        sys.exit(2)
+
+    import llaisys_amd as L
+    assert L.RuntimeAPI(L.DeviceType.AMD).get_device_count() >= 1, "no AMD GPU"
+    hip = HipEvents()
+    stream = L.context_stream(L.DeviceType.AMD, 0)
+    api = L.RuntimeAPI(L.DeviceType.AMD)
+    print("bench: building config-1 buffers", file=sys.stderr, flush=True)
+    wl = Workload(L)
+    ops = wl.ops()
+    step_bytes = sum(b for _, b, _ in ops)
+
+    def step(i):
+        s = wl.sets[i % NSETS]
+        for _, _, fn in ops:
+            fn(s)
+
+    for i in range(args.warmup):
+        step(i)
+    api.device_synchronize()
+    e0, e1 = hip.event(), hip.event()
+    t0 = time.perf_counter()
+    hip.record(e0, stream)
+    for i in range(args.steps):
+        step(i)
+    hip.record(e1, stream)
+    api.device_synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = hip.elapsed_ms(e0, e1) / args.steps
+    assert L.take_device_error() == 0
+
+    per_op = {}
+    reps = max(args.steps, 20)
+    for name, nbytes, fn in ops:
+        for i in range(3):
+            fn(wl.sets[i % NSETS])
+        hip.record(e0, stream)
+        for i in range(reps):
+            fn(wl.sets[i % NSETS])
+        hip.record(e1, stream)
+        us = hip.elapsed_ms(e0, e1) / reps * 1e3
+        gbs = nbytes / (us * 1e-6) / 1e9
+        per_op[name] = {"us": round(us, 3), "bytes": nbytes, "GB_s": round(gbs, 1),
+                        "frac_peak": round(gbs / PEAK_GBS, 4)}
+    print("bench: per-op " + json.dumps(per_op), file=sys.stderr, flush=True)
+
+    chain = None
+    if not args.no_chain:
+        del wl
+        print("bench: building config-4 chain buffers", file=sys.stderr, flush=True)
+        ch = Chain(L)
+        for _ in range(2):
+            ch.run()
+        hip.record(e0, stream)
+        nrep = 10
+        for _ in range(nrep):
+            ch.run()
+        hip.record(e1, stream)
+        ms = hip.elapsed_ms(e0, e1) / nrep
+        cb = ch.bytes()
+        chain = {"workload": "config 4: 28 Qwen2-1.5B layers, 2048-token prefill, bf16, INT8 KV "
+                             "append, final rms_norm + argmax over [2048, 151936]",
+                 "ms": round(ms, 4), "tokens_per_s": round(Chain.TOK / (ms * 1e-3)),
+                 "bytes": cb, "GB_s": round(cb / (ms * 1e-3) / 1e9, 1),
+                 "frac_peak": round(cb / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)}
+        assert L.take_device_error() == 0
+        del ch
+
+    dom = per_op["swiglu"]
+    roof = {"kernel": "swiglu binaryVec<BF16> [8192, 8960]", "bound": "hbm",
+            "achieved": dom["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
+            "frac": round(dom["GB_s"] / PEAK_GBS, 4), "traffic": traffic_of("swiglu")}
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded normal activations, N(0,0.02) table), resident in HBM",
+        "config": {"workload": "config 1: Qwen2-1.5B layer ops, bf16, 8192 tokens (embedding, "
+                               "rms_norm, add+rms_norm, rope q+k, swiglu, argmax [1,151936])",
+                   "tokens": T, "hidden": H, "intermediate": I, "vocab": V,
+                   "buffer_sets": NSETS, "parallelism": "single GPU"},
+        "frac_peak": round(value / PEAK_GBS, 4),
+        "tokens_per_s": round(T / (ms_step * 1e-3)),
+        "wall_s_timed": round(wall, 3),
+        "per_op": per_op, "chain": chain, "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

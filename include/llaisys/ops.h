@@ -1,0 +1,79 @@
+/*
+ * LLAISYS C ABI -- operators.
+ *
+ * The nine reference entry points keep their exact signatures (include/llaisys/ops.h:7-15;
+ * shims src/llaisys/ops.cc:19-45).  All take pre-allocated tensors, return void and report
+ * argument errors by printing to stderr and throwing, as the reference does
+ * (src/utils/check.hpp:7-88).  On LLAISYS_DEVICE_AMD every op is one or two asynchronous
+ * HIP kernel launches on the context stream (llaisysGetContextStream).
+ *
+ * Scope of this library: the bandwidth-bound per-layer ops.  llaisysLinear,
+ * llaisysRearrange and llaisysSelfAttention are exported so that the reference's ctypes
+ * loader binds, and raise "Unimplemented function" (the reference's own rearrange is a
+ * stub, src/ops/rearrange/op.cpp:4-6).  Ops on CPU tensors raise "Unsupported device":
+ * this library has no CPU compute path.
+ */
+#ifndef LLAISYS_OPS_H
+#define LLAISYS_OPS_H
+
+#include "tensor.h"
+
+__C {
+    /* reference ops.h:7 -- c = a + b (half types add in f32 and round, add_cpu.cpp:7-17) */
+    __export void llaisysAdd(llaisysTensor_t c, llaisysTensor_t a, llaisysTensor_t b);
+    /* reference ops.h:8 -- flat argmax over all elements of vals; first maximum wins
+     * (argmax_cpu.cpp:9-28); max_idx I32/I64, max_val dtype == vals dtype */
+    __export void llaisysArgmax(llaisysTensor_t max_idx, llaisysTensor_t max_val,
+                                llaisysTensor_t vals);
+    /* reference ops.h:9 -- out[i,:] = weight[index[i],:]; index I32/I64 */
+    __export void llaisysEmbedding(llaisysTensor_t out, llaisysTensor_t index,
+                                   llaisysTensor_t weight);
+    /* reference ops.h:10 -- out of scope here: raises "Unimplemented function" */
+    __export void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight,
+                                llaisysTensor_t bias);
+    /* reference ops.h:11 -- out of scope here: raises "Unimplemented function" */
+    __export void llaisysRearrange(llaisysTensor_t out, llaisysTensor_t in);
+    /* reference ops.h:12 -- per last-dim row: y = x * w / sqrt(mean(x^2) + eps) */
+    __export void llaisysRmsNorm(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight,
+                                 float eps);
+    /* reference ops.h:13 -- rotate-half RoPE on [seq, n_heads, head_dim], pos_ids I64 */
+    __export void llaisysROPE(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t pos_ids,
+                              float theta);
+    /* reference ops.h:14 -- out of scope here: raises "Unimplemented function" */
+    __export void llaisysSelfAttention(llaisysTensor_t attn_val, llaisysTensor_t q,
+                                       llaisysTensor_t k, llaisysTensor_t v, float scale);
+    /* reference ops.h:15 -- out = up * gate / (1 + exp(-gate)) */
+    __export void llaisysSwiGLU(llaisysTensor_t out, llaisysTensor_t gate, llaisysTensor_t up);
+
+    /* ---- additive entry points (no reference kernel; same conventions) ---------------- */
+
+    /* Fused residual add + rms_norm, replacing the reference decoder's llaisysAdd followed
+     * by llaisysRmsNorm (src/models/qwen2/layer.hpp:60-71):
+     *   residual_out = T(in + residual);  out = rms_norm(residual_out, weight, eps).
+     * residual_out may be the same tensor as residual (in-place residual stream). */
+    __export void llaisysAddRmsNorm(llaisysTensor_t out, llaisysTensor_t residual_out,
+                                    llaisysTensor_t in, llaisysTensor_t residual,
+                                    llaisysTensor_t weight, float eps);
+    /* Row-wise argmax: the reference argmax (argmax_cpu.cpp:9-28) applied to each row of
+     * vals [rows, cols]; max_idx [rows] I32/I64, max_val [rows] with the dtype of vals. */
+    __export void llaisysArgmaxRows(llaisysTensor_t max_idx, llaisysTensor_t max_val,
+                                    llaisysTensor_t vals);
+    /* Symmetric INT8 absmax quantization per last-dim row of in [..., cols]
+     * (F32/BF16/F16): scale[r] = max|x| / 127 (F32, shape in.shape[:-1]),
+     * q = clamp(round_half_even(x / scale), -127, 127) (I8, shape of in); an all-zero row
+     * gives scale 0 and codes 0; a NaN quotient gives code 0. */
+    __export void llaisysQuantizeInt8(llaisysTensor_t q, llaisysTensor_t scale,
+                                      llaisysTensor_t in);
+    /* out = T(float(q) * scale[row]) for q [..., cols] I8 and scale [...] F32. */
+    __export void llaisysDequantizeInt8(llaisysTensor_t out, llaisysTensor_t q,
+                                        llaisysTensor_t scale);
+    /* INT8 KV-cache append, replacing the f32 row copy of the reference decoder's cache
+     * update (src/models/qwen2/attention.hpp:108-123): quantizes kv [n_tok, n_kvh, head_dim]
+     * per (token, head) row with the rule of llaisysQuantizeInt8 and writes the codes to
+     * cache_q [max_seq, n_kvh, head_dim] (I8) rows pos .. pos+n_tok-1 and the scales to
+     * cache_scale [max_seq, n_kvh] (F32).  Requires pos + n_tok <= max_seq. */
+    __export void llaisysKVAppendInt8(llaisysTensor_t cache_q, llaisysTensor_t cache_scale,
+                                      llaisysTensor_t kv, size_t pos);
+}
+
+#endif /* LLAISYS_OPS_H */

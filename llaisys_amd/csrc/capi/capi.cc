@@ -1,0 +1,154 @@
+// extern "C" entry points of libllaisys.so.
+//
+// Same shape as the reference shims (src/llaisys/ops.cc:17-46, tensor.cc:6-119,
+// runtime.cc:11-19): unwrap the handle, call C++, no try/catch -- an error prints and
+// throws, which through ctypes ends the process, as with the reference library.
+#include "llaisys/models/qwen2.h"
+#include "llaisys/ops.h"
+#include "llaisys/runtime.h"
+#include "llaisys/tensor.h"
+
+#include "../core/core.hpp"
+#include "../device/runtime_api.hpp"
+#include "../ops/ops.hpp"
+#include "../tensor/tensor.hpp"
+#include "../utils/check.hpp"
+
+#include <algorithm>
+#include <vector>
+
+struct LlaisysTensor {
+    llaisys::tensor_t tensor;
+};
+
+namespace {
+llaisysTensor_t wrap(llaisys::tensor_t t) { return new LlaisysTensor{std::move(t)}; }
+} // namespace
+
+__C {
+    // ---- runtime (reference src/llaisys/runtime.cc:11-19) ------------------------------
+    void llaisysSetContextRuntime(llaisysDeviceType_t type, int id) {
+        llaisys::core::context().setDevice(type, id);
+    }
+
+    const LlaisysRuntimeAPI *llaisysGetRuntimeAPI(llaisysDeviceType_t type) {
+        return llaisys::device::getRuntimeAPI(type);
+    }
+
+    llaisysStream_t llaisysGetContextStream(llaisysDeviceType_t type, int id) {
+        auto &ctx = llaisys::core::context();
+        ctx.setDevice(type, id);
+        return ctx.runtime().stream();
+    }
+
+    int llaisysTakeDeviceError(llaisysDeviceType_t type, int id) {
+        if (type != LLAISYS_DEVICE_AMD) return 0;
+        auto &ctx = llaisys::core::context();
+        ctx.setDevice(type, id);
+        return llaisys::device::amd::takeError(ctx.runtime().stream());
+    }
+
+    // ---- tensors (reference src/llaisys/tensor.cc:7-118) -------------------------------
+    llaisysTensor_t tensorCreate(size_t * shape, size_t ndim, llaisysDataType_t dtype,
+                                 llaisysDeviceType_t device_type, int device_id) {
+        std::vector<size_t> dims(shape, shape + ndim);
+        return wrap(llaisys::Tensor::create(dims, dtype, device_type, device_id));
+    }
+
+    void tensorDestroy(llaisysTensor_t t) { delete t; }
+
+    void *tensorGetData(llaisysTensor_t t) { return t->tensor->data(); }
+
+    size_t tensorGetNdim(llaisysTensor_t t) { return t->tensor->ndim(); }
+
+    void tensorGetShape(llaisysTensor_t t, size_t * shape) {
+        std::copy(t->tensor->shape().begin(), t->tensor->shape().end(), shape);
+    }
+
+    void tensorGetStrides(llaisysTensor_t t, ptrdiff_t * strides) {
+        std::copy(t->tensor->strides().begin(), t->tensor->strides().end(), strides);
+    }
+
+    llaisysDataType_t tensorGetDataType(llaisysTensor_t t) { return t->tensor->dtype(); }
+
+    llaisysDeviceType_t tensorGetDeviceType(llaisysTensor_t t) { return t->tensor->deviceType(); }
+
+    int tensorGetDeviceId(llaisysTensor_t t) { return t->tensor->deviceId(); }
+
+    void tensorDebug(llaisysTensor_t t) { t->tensor->debug(); }
+
+    uint8_t tensorIsContiguous(llaisysTensor_t t) { return uint8_t(t->tensor->isContiguous()); }
+
+    void tensorLoad(llaisysTensor_t t, const void *data) { t->tensor->load(data); }
+
+    llaisysTensor_t tensorView(llaisysTensor_t t, size_t * shape, size_t ndim) {
+        return wrap(t->tensor->view(std::vector<size_t>(shape, shape + ndim)));
+    }
+
+    llaisysTensor_t tensorPermute(llaisysTensor_t t, size_t * order) {
+        return wrap(t->tensor->permute(std::vector<size_t>(order, order + t->tensor->ndim())));
+    }
+
+    llaisysTensor_t tensorSlice(llaisysTensor_t t, size_t dim, size_t start, size_t end) {
+        return wrap(t->tensor->slice(dim, start, end));
+    }
+
+    // ---- ops (reference src/llaisys/ops.cc:19-45) --------------------------------------
+    void llaisysAdd(llaisysTensor_t c, llaisysTensor_t a, llaisysTensor_t b) {
+        llaisys::ops::add(c->tensor, a->tensor, b->tensor);
+    }
+    void llaisysArgmax(llaisysTensor_t max_idx, llaisysTensor_t max_val, llaisysTensor_t vals) {
+        llaisys::ops::argmax(max_idx->tensor, max_val->tensor, vals->tensor);
+    }
+    void llaisysEmbedding(llaisysTensor_t out, llaisysTensor_t index, llaisysTensor_t weight) {
+        llaisys::ops::embedding(out->tensor, index->tensor, weight->tensor);
+    }
+    void llaisysLinear(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t, llaisysTensor_t) {
+        TO_BE_IMPLEMENTED();
+    }
+    void llaisysRearrange(llaisysTensor_t, llaisysTensor_t) { TO_BE_IMPLEMENTED(); }
+    void llaisysRmsNorm(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, float eps) {
+        llaisys::ops::rmsNorm(out->tensor, in->tensor, weight->tensor, eps);
+    }
+    void llaisysROPE(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t pos_ids, float theta) {
+        llaisys::ops::rope(out->tensor, in->tensor, pos_ids->tensor, theta);
+    }
+    void llaisysSelfAttention(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t, llaisysTensor_t,
+                              float) {
+        TO_BE_IMPLEMENTED();
+    }
+    void llaisysSwiGLU(llaisysTensor_t out, llaisysTensor_t gate, llaisysTensor_t up) {
+        llaisys::ops::swiglu(out->tensor, gate->tensor, up->tensor);
+    }
+    void llaisysAddRmsNorm(llaisysTensor_t out, llaisysTensor_t residual_out, llaisysTensor_t in,
+                           llaisysTensor_t residual, llaisysTensor_t weight, float eps) {
+        llaisys::ops::addRmsNorm(out->tensor, residual_out->tensor, in->tensor, residual->tensor,
+                                 weight->tensor, eps);
+    }
+    void llaisysArgmaxRows(llaisysTensor_t max_idx, llaisysTensor_t max_val, llaisysTensor_t vals) {
+        llaisys::ops::argmaxRows(max_idx->tensor, max_val->tensor, vals->tensor);
+    }
+    void llaisysQuantizeInt8(llaisysTensor_t q, llaisysTensor_t scale, llaisysTensor_t in) {
+        llaisys::ops::quantizeInt8(q->tensor, scale->tensor, in->tensor);
+    }
+    void llaisysDequantizeInt8(llaisysTensor_t out, llaisysTensor_t q, llaisysTensor_t scale) {
+        llaisys::ops::dequantizeInt8(out->tensor, q->tensor, scale->tensor);
+    }
+    void llaisysKVAppendInt8(llaisysTensor_t cache_q, llaisysTensor_t cache_scale,
+                             llaisysTensor_t kv, size_t pos) {
+        llaisys::ops::kvAppendInt8(cache_q->tensor, cache_scale->tensor, kv->tensor, pos);
+    }
+
+    // ---- model API: out of scope, exported so the reference ctypes loader binds --------
+    struct LlaisysQwen2Model *llaisysQwen2ModelCreate(const struct LlaisysQwen2Meta *,
+                                                      llaisysDeviceType_t, int *, int) {
+        TO_BE_IMPLEMENTED();
+    }
+    void llaisysQwen2ModelDestroy(struct LlaisysQwen2Model *) { TO_BE_IMPLEMENTED(); }
+    struct LlaisysQwen2Weights *llaisysQwen2ModelWeights(struct LlaisysQwen2Model *) {
+        TO_BE_IMPLEMENTED();
+    }
+    int64_t llaisysQwen2ModelInfer(struct LlaisysQwen2Model *, int64_t *, size_t) {
+        TO_BE_IMPLEMENTED();
+    }
+}

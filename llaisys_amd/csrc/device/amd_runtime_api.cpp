@@ -1,0 +1,174 @@
+// The AMD (HIP) device table: one MI355X GPU per device id.
+//
+// Plays the role of the reference's (stubbed) NVIDIA table,
+// src/device/nvidia/nvidia_runtime_api.cu:9-74, on HIP.  Streams are created with the
+// default priority.  Host allocations are pinned (hipHostMalloc) so that tensorLoad and
+// D2H copies run at full PCIe rate.
+#include "runtime_api.hpp"
+
+#include "../utils/check.hpp"
+
+#include <hip/hip_runtime_api.h>
+
+#include <mutex>
+#include <vector>
+
+namespace llaisys::device::amd {
+
+void check(int status, const char *what) {
+    if (status != hipSuccess) {
+        const char *msg = hipGetErrorString(static_cast<hipError_t>(status));
+        LLAISYS_FAIL(std::runtime_error, "HIP " << what << ": " << msg, msg);
+    }
+}
+
+namespace {
+
+hipMemcpyKind toHip(llaisysMemcpyKind_t k) {
+    switch (k) {
+    case LLAISYS_MEMCPY_H2H: return hipMemcpyHostToHost;
+    case LLAISYS_MEMCPY_H2D: return hipMemcpyHostToDevice;
+    case LLAISYS_MEMCPY_D2H: return hipMemcpyDeviceToHost;
+    case LLAISYS_MEMCPY_D2D: return hipMemcpyDeviceToDevice;
+    }
+    return hipMemcpyDefault;
+}
+
+int count() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError(); // no driver / no GPU: report none, leave no sticky error
+        return 0;
+    }
+    return n;
+}
+
+void setDevice(int id) { check(hipSetDevice(id), "hipSetDevice"); }
+
+void sync() {
+    check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    raiseIfError(nullptr);
+}
+
+llaisysStream_t createStream() {
+    hipStream_t s = nullptr;
+    check(hipStreamCreate(&s), "hipStreamCreate");
+    return s;
+}
+
+// Teardown paths ignore errors: at process exit the HIP runtime may already be gone.
+void destroyStream(llaisysStream_t s) {
+    if (s) (void)hipStreamDestroy(static_cast<hipStream_t>(s));
+}
+
+void streamSync(llaisysStream_t s) {
+    check(hipStreamSynchronize(static_cast<hipStream_t>(s)), "hipStreamSynchronize");
+    raiseIfError(s);
+}
+
+void *mallocDevice(size_t n) {
+    void *p = nullptr;
+    check(hipMalloc(&p, n ? n : 1), "hipMalloc");
+    return p;
+}
+
+void freeDevice(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+void *mallocHost(size_t n) {
+    void *p = nullptr;
+    check(hipHostMalloc(&p, n ? n : 1, hipHostMallocDefault), "hipHostMalloc");
+    return p;
+}
+
+void freeHost(void *p) {
+    if (p) (void)hipHostFree(p);
+}
+
+void copy(void *dst, const void *src, size_t n, llaisysMemcpyKind_t k) {
+    if (n) check(hipMemcpy(dst, src, n, toHip(k)), "hipMemcpy");
+}
+
+void copyAsync(void *dst, const void *src, size_t n, llaisysMemcpyKind_t k, llaisysStream_t s) {
+    if (n)
+        check(hipMemcpyAsync(dst, src, n, toHip(k), static_cast<hipStream_t>(s)),
+              "hipMemcpyAsync");
+}
+
+const LlaisysRuntimeAPI kTable = {&count,         &setDevice,  &sync,         &createStream,
+                                  &destroyStream, &streamSync, &mallocDevice, &freeDevice,
+                                  &mallocHost,    &freeHost,   &copy,         &copyAsync};
+
+constexpr int kMaxDevices = 64;
+std::mutex g_mu;
+int *g_err[kMaxDevices] = {};
+// Workspaces are per thread: every thread has its own Context and hence its own stream
+// per device, and stream order is what makes reuse of a workspace safe.
+thread_local void *g_ws[kMaxDevices] = {};
+thread_local size_t g_ws_size[kMaxDevices] = {};
+
+int currentDevice() {
+    int d = 0;
+    check(hipGetDevice(&d), "hipGetDevice");
+    CHECK_ARGUMENT(d >= 0 && d < kMaxDevices, "device id out of range");
+    return d;
+}
+
+} // namespace
+
+const LlaisysRuntimeAPI *getRuntimeAPI() { return &kTable; }
+
+int *errorWord(int dev) {
+    CHECK_ARGUMENT(dev >= 0 && dev < kMaxDevices, "device id out of range");
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_err[dev]) {
+        void *p = nullptr;
+        check(hipMalloc(&p, sizeof(int)), "hipMalloc(error word)");
+        check(hipMemset(p, 0, sizeof(int)), "hipMemset(error word)");
+        g_err[dev] = static_cast<int *>(p);
+    }
+    return g_err[dev];
+}
+
+int takeError(llaisysStream_t s) {
+    const int dev = currentDevice();
+    int *w = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        w = g_err[dev];
+    }
+    if (!w) return 0; // no kernel that reports errors ran on this device yet
+    check(hipStreamSynchronize(static_cast<hipStream_t>(s)), "hipStreamSynchronize");
+    int code = 0;
+    check(hipMemcpy(&code, w, sizeof(int), hipMemcpyDeviceToHost), "hipMemcpy(error word)");
+    if (code) check(hipMemset(w, 0, sizeof(int)), "hipMemset(error word)");
+    return code;
+}
+
+void raiseIfError(llaisysStream_t s) {
+    const int code = takeError(s);
+    if (code == 1) ASSERT(false, "Embedding index out of bound");
+    if (code != 0) LLAISYS_FAIL(std::runtime_error, "device error code " << code, "device error");
+}
+
+void *workspace(int dev, size_t bytes) {
+    CHECK_ARGUMENT(dev >= 0 && dev < kMaxDevices, "device id out of range");
+    if (g_ws_size[dev] < bytes) {
+        // Stream order makes reuse safe; a grow must wait for kernels still reading it.
+        if (g_ws[dev]) {
+            check(hipDeviceSynchronize(), "hipDeviceSynchronize(workspace)");
+            check(hipFree(g_ws[dev]), "hipFree(workspace)");
+        }
+        size_t n = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+        void *p = nullptr;
+        check(hipMalloc(&p, n), "hipMalloc(workspace)");
+        // Kernels that keep a completion counter in the workspace expect it zeroed once.
+        check(hipMemset(p, 0, n), "hipMemset(workspace)");
+        g_ws[dev] = p;
+        g_ws_size[dev] = n;
+    }
+    return g_ws[dev];
+}
+
+} // namespace llaisys::device::amd

@@ -1,0 +1,227 @@
+// Argmax for gfx950: flat (the reference op) and per row (logits [rows, vocab]).
+//
+// Semantics: reference src/ops/argmax/cpu/argmax_cpu.cpp:14-27 -- seed with element 0,
+// replace only on a strictly greater f32 value.  Equivalently: the lowest index whose
+// value is the maximum over the non-NaN elements; index 0 when element 0 is NaN or when no
+// element is greater than -inf.  max_val is T(f32 value of that element).
+//
+// Design: HBM-bound reduction.  Each lane scans its own 16-byte vectors in ascending
+// order (the max of a vector is found with compares first; the index is searched only
+// when that max beats the lane's best, which is rare on real logits), then (value, index)
+// pairs are merged across the wavefront with butterflies and across wavefronts through
+// LDS, ties going to the lower index.  Rows: one 256-thread block per row.  Flat: the
+// vector is cut into segments, one block each; every block stores its partial, and the
+// last block to finish (a device-scope counter) merges them, all in one launch.
+#include "common.hpp"
+#include "launch.hpp"
+#include "rowplan.hpp"
+
+#include <climits>
+
+namespace llaisys::kernels {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kU = 4;
+constexpr int64_t kNone = INT64_MAX;
+
+struct Best {
+    float v;
+    int64_t i;
+};
+
+__device__ __forceinline__ void take(Best &b, float v, int64_t i) {
+    if (v > b.v || (v == b.v && i < b.i)) {
+        b.v = v;
+        b.i = i;
+    }
+}
+
+// Merge of the whole block; the result is valid in thread 0.
+__device__ Best blockMerge(Best b) {
+    __shared__ float sv[kBlock / kWave];
+    __shared__ int64_t si[kBlock / kWave];
+#pragma unroll
+    for (int m = kWave / 2; m > 0; m >>= 1) {
+        const float ov = __shfl_xor(b.v, m, kWave);
+        const int64_t oi = __shfl_xor(b.i, m, kWave);
+        take(b, ov, oi);
+    }
+    const int wave = threadIdx.x / kWave;
+    if (threadIdx.x % kWave == 0) {
+        sv[wave] = b.v;
+        si[wave] = b.i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < kBlock / kWave; ++w) take(b, sv[w], si[w]);
+    return b;
+}
+
+// Scan of [begin, end) by the block; thread-local order is ascending.
+template <typename T>
+__device__ Best scan(const void *vals, size_t begin, size_t end, bool vec) {
+    using F = Fmt<T>;
+    constexpr int N = F::kVec;
+    Best b{-INFINITY, kNone};
+    size_t tail = begin;
+    if (vec) {
+        const size_t nv = (end - begin) / N;
+        tail = begin + nv * N;
+        for (size_t k = threadIdx.x; k < nv; k += kBlock * kU) {
+            uint4 r[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                if (k + u * kBlock < nv) r[u] = load16<T>(vals, begin + (k + u * kBlock) * N);
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
+                if (k + u * kBlock < nv) {
+                    float f[N];
+                    F::unpack(r[u], f);
+                    float m = -INFINITY;
+#pragma unroll
+                    for (int e = 0; e < N; ++e) m = f[e] > m ? f[e] : m;
+                    if (m > b.v) {
+                        int first = N - 1;
+#pragma unroll
+                        for (int e = N - 1; e >= 0; --e) first = f[e] == m ? e : first;
+                        b.v = m;
+                        b.i = int64_t(begin + (k + u * kBlock) * N + first);
+                    }
+                }
+            }
+        }
+    }
+    for (size_t j = tail + threadIdx.x; j < end; j += kBlock) {
+        const float x = F::get(vals, j);
+        if (x > b.v) {
+            b.v = x;
+            b.i = int64_t(j);
+        }
+    }
+    return b;
+}
+
+// Writes the final answer for the element range starting at `first` (thread 0 only).
+template <typename T>
+__device__ void finish(Best b, const void *vals, size_t first, void *idx, bool i64, void *val,
+                       size_t slot) {
+    using F = Fmt<T>;
+    const float x0 = F::get(vals, first);
+    int64_t k = (b.i == kNone || x0 != x0) ? 0 : b.i - int64_t(first);
+    if (i64)
+        static_cast<int64_t *>(idx)[slot] = k;
+    else
+        static_cast<int32_t *>(idx)[slot] = int32_t(k);
+    F::put(val, slot, F::get(vals, first + size_t(k)));
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kBlock)
+    argmaxRowsKernel(void *idx, bool i64, void *val, const void *__restrict__ vals, size_t cols,
+                     bool vec) {
+    const size_t first = size_t(blockIdx.x) * cols;
+    Best b = blockMerge(scan<T>(vals, first, first + cols, vec));
+    if (threadIdx.x == 0) finish<T>(b, vals, first, idx, i64, val, blockIdx.x);
+}
+
+struct Partial {
+    uint32_t vbits;
+    uint32_t pad;
+    int64_t i;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(kBlock)
+    argmaxFlatKernel(void *idx, bool i64, void *val, const void *__restrict__ vals, size_t n,
+                     size_t seg, bool vec, unsigned *counter, Partial *part) {
+    __shared__ bool last;
+    const size_t begin = size_t(blockIdx.x) * seg;
+    const size_t end = begin + seg < n ? begin + seg : n;
+    Best b = blockMerge(scan<T>(vals, begin, end, vec));
+    if (threadIdx.x == 0) {
+        part[blockIdx.x].vbits = __float_as_uint(b.v);
+        part[blockIdx.x].i = b.i;
+        __threadfence();
+        last = atomicAdd(counter, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    Best m{-INFINITY, kNone};
+    for (unsigned p = threadIdx.x; p < gridDim.x; p += kBlock) {
+        // Device-scope loads: other blocks' partials must not come from a stale L1 line.
+        const uint32_t vb = __hip_atomic_load(&part[p].vbits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int64_t pi = __hip_atomic_load(&part[p].i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        take(m, __uint_as_float(vb), pi);
+    }
+    m = blockMerge(m);
+    if (threadIdx.x == 0) {
+        finish<T>(m, vals, 0, idx, i64, val, 0);
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+constexpr size_t kCounterBytes = 256;
+
+template <typename T>
+size_t segmentOf() {
+    return size_t(kBlock) * kU * Fmt<T>::kVec;
+}
+
+size_t segmentFor(llaisysDataType_t dt) {
+    switch (dt) {
+    case LLAISYS_DTYPE_F32: return segmentOf<F32>();
+    default: return segmentOf<BF16>();
+    }
+}
+
+template <typename T>
+void launchRows(void *idx, bool i64, void *val, const void *vals, size_t rows, size_t cols,
+                hipStream_t s) {
+    if (rows == 0 || cols == 0) return;
+    const bool vec = aligned16(vals) && (cols * Fmt<T>::kBytes) % 16 == 0;
+    argmaxRowsKernel<T><<<unsigned(rows), kBlock, 0, s>>>(idx, i64, val, vals, cols, vec);
+}
+
+template <typename T>
+void launchFlat(void *idx, bool i64, void *val, const void *vals, size_t n, void *ws,
+                hipStream_t s) {
+    if (n == 0) return;
+    const size_t seg = segmentOf<T>();
+    const unsigned blocks = unsigned((n + seg - 1) / seg);
+    auto *counter = static_cast<unsigned *>(ws);
+    auto *part = reinterpret_cast<Partial *>(static_cast<char *>(ws) + kCounterBytes);
+    argmaxFlatKernel<T><<<blocks, kBlock, 0, s>>>(idx, i64, val, vals, n, seg, aligned16(vals),
+                                                  counter, part);
+}
+
+} // namespace
+
+size_t argmaxWorkspaceBytes(size_t n, llaisysDataType_t dt) {
+    const size_t seg = segmentFor(dt);
+    return kCounterBytes + ((n + seg - 1) / seg) * sizeof(Partial);
+}
+
+void argmaxRows(void *idx, bool i64, void *val, const void *vals, size_t rows, size_t cols,
+                llaisysDataType_t dt, hipStream_t s) {
+    switch (dt) {
+    case LLAISYS_DTYPE_F32: return launchRows<F32>(idx, i64, val, vals, rows, cols, s);
+    case LLAISYS_DTYPE_BF16: return launchRows<BF16>(idx, i64, val, vals, rows, cols, s);
+    case LLAISYS_DTYPE_F16: return launchRows<F16>(idx, i64, val, vals, rows, cols, s);
+    default: return;
+    }
+}
+
+void argmax(void *idx, bool i64, void *val, const void *vals, size_t n, llaisysDataType_t dt,
+            void *ws, hipStream_t s) {
+    switch (dt) {
+    case LLAISYS_DTYPE_F32: return launchFlat<F32>(idx, i64, val, vals, n, ws, s);
+    case LLAISYS_DTYPE_BF16: return launchFlat<BF16>(idx, i64, val, vals, n, ws, s);
+    case LLAISYS_DTYPE_F16: return launchFlat<F16>(idx, i64, val, vals, n, ws, s);
+    default: return;
+    }
+}
+
+} // namespace llaisys::kernels

@@ -1,0 +1,178 @@
+// Streaming element-wise kernels for gfx950: swiglu, add, INT8 dequantize.
+//
+// swiglu follows src/ops/swiglu/cpu/swiglu_cpu.cpp:15-20: out = T(u * (g / (1 + expf(-g))))
+// in f32 with an IEEE division.  add follows src/ops/add/cpu/add_cpu.cpp:9-16.  dequantize
+// is out = T(float(q) * scale[row]).
+//
+// Design: pure HBM streaming.  Each lane moves U 16-byte vectors per input (all loads
+// issued before any math so U * 16 B per input are in flight per lane); vector k of a
+// block is blockIdx * 256 * U + k * 256 + lane, so every wavefront access is one
+// contiguous 1 KB segment.  A scalar kernel handles lengths / addresses that are not
+// multiples of 16 bytes.
+#include "common.hpp"
+#include "launch.hpp"
+#include "rowplan.hpp"
+
+#include <algorithm>
+
+namespace llaisys::kernels {
+
+namespace {
+
+constexpr int kU = 4;
+
+struct SwigluOp {
+    __device__ static float apply(float g, float u) { return u * (g / (1.0f + expf(-g))); }
+};
+struct AddOp {
+    __device__ static float apply(float a, float b) { return a + b; }
+};
+
+template <typename T, typename Op>
+__global__ void __launch_bounds__(256)
+    binaryVec(void *__restrict__ out, const void *__restrict__ a, const void *__restrict__ b,
+              size_t nvec) {
+    using F = Fmt<T>;
+    constexpr int N = F::kVec;
+    const size_t first = size_t(blockIdx.x) * 256 * kU + threadIdx.x;
+    uint4 ra[kU], rb[kU];
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+        const size_t i = first + size_t(k) * 256;
+        if (i < nvec) {
+            ra[k] = load16<T>(a, i * N);
+            rb[k] = load16<T>(b, i * N);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+        const size_t i = first + size_t(k) * 256;
+        if (i < nvec) {
+            float x[N], y[N];
+            F::unpack(ra[k], x);
+            F::unpack(rb[k], y);
+#pragma unroll
+            for (int e = 0; e < N; ++e) x[e] = Op::apply(x[e], y[e]);
+            store16<T>(out, i * N, F::pack(x));
+        }
+    }
+}
+
+template <typename T, typename Op>
+__global__ void __launch_bounds__(256)
+    binaryScalar(void *out, const void *a, const void *b, size_t n) {
+    using F = Fmt<T>;
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256)
+        F::put(out, i, Op::apply(F::get(a, i), F::get(b, i)));
+}
+
+template <typename T, typename Op>
+void launchBinary(void *out, const void *a, const void *b, size_t n, hipStream_t s) {
+    if (n == 0) return;
+    constexpr int N = Fmt<T>::kVec;
+    if (n % N == 0 && aligned16(out) && aligned16(a) && aligned16(b)) {
+        const size_t nvec = n / N;
+        binaryVec<T, Op><<<blocksFor(nvec, 256 * kU), 256, 0, s>>>(out, a, b, nvec);
+        return;
+    }
+    const unsigned grid = unsigned(std::min<size_t>(blocksFor(n, 256), 1u << 20));
+    binaryScalar<T, Op><<<grid, 256, 0, s>>>(out, a, b, n);
+}
+
+template <typename Op>
+void dispatchBinary(void *out, const void *a, const void *b, size_t n, llaisysDataType_t dt,
+                    hipStream_t s) {
+    switch (dt) {
+    case LLAISYS_DTYPE_F32: return launchBinary<F32, Op>(out, a, b, n, s);
+    case LLAISYS_DTYPE_BF16: return launchBinary<BF16, Op>(out, a, b, n, s);
+    case LLAISYS_DTYPE_F16: return launchBinary<F16, Op>(out, a, b, n, s);
+    default: return;
+    }
+}
+
+// ---- INT8 dequantize --------------------------------------------------------------------
+
+// N codes (one output vector) per lane: 8 bytes of codes for 16-bit outputs, 4 for f32.
+template <int N>
+__device__ __forceinline__ void loadCodes(const int8_t *q, size_t i, float *f) {
+    if constexpr (N == 8) {
+        const uint2 r = *reinterpret_cast<const uint2 *>(q + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            f[e] = float(int8_t(r.x >> (8 * e)));
+            f[4 + e] = float(int8_t(r.y >> (8 * e)));
+        }
+    } else {
+        const uint32_t r = *reinterpret_cast<const uint32_t *>(q + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[e] = float(int8_t(r >> (8 * e)));
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+    dequantVec(void *__restrict__ out, const int8_t *__restrict__ q,
+               const float *__restrict__ scale, size_t nvec, size_t vec_per_row) {
+    using F = Fmt<T>;
+    constexpr int N = F::kVec;
+    const size_t first = size_t(blockIdx.x) * 256 * kU + threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < kU; ++k) {
+        const size_t i = first + size_t(k) * 256;
+        if (i < nvec) {
+            float f[N];
+            loadCodes<N>(q, i * N, f);
+            const float sc = scale[i / vec_per_row];
+#pragma unroll
+            for (int e = 0; e < N; ++e) f[e] = f[e] * sc;
+            store16<T>(out, i * N, F::pack(f));
+        }
+    }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256)
+    dequantScalar(void *out, const int8_t *q, const float *scale, size_t n, size_t cols) {
+    using F = Fmt<T>;
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256)
+        F::put(out, i, float(q[i]) * scale[i / cols]);
+}
+
+template <typename T>
+void launchDequant(void *out, const int8_t *q, const float *scale, size_t rows, size_t cols,
+                   hipStream_t s) {
+    const size_t n = rows * cols;
+    if (n == 0) return;
+    constexpr int N = Fmt<T>::kVec;
+    const size_t code_align = reinterpret_cast<uintptr_t>(q) % N;
+    if (cols % N == 0 && aligned16(out) && code_align == 0) {
+        const size_t nvec = n / N;
+        dequantVec<T><<<blocksFor(nvec, 256 * kU), 256, 0, s>>>(out, q, scale, nvec, cols / N);
+        return;
+    }
+    const unsigned grid = unsigned(std::min<size_t>(blocksFor(n, 256), 1u << 20));
+    dequantScalar<T><<<grid, 256, 0, s>>>(out, q, scale, n, cols);
+}
+
+} // namespace
+
+void swiglu(void *out, const void *gate, const void *up, size_t n, llaisysDataType_t dt,
+            hipStream_t s) {
+    dispatchBinary<SwigluOp>(out, gate, up, n, dt, s);
+}
+
+void add(void *c, const void *a, const void *b, size_t n, llaisysDataType_t dt, hipStream_t s) {
+    dispatchBinary<AddOp>(c, a, b, n, dt, s);
+}
+
+void dequantizeInt8(void *out, const int8_t *q, const float *scale, size_t rows, size_t cols,
+                    llaisysDataType_t dt, hipStream_t s) {
+    switch (dt) {
+    case LLAISYS_DTYPE_F32: return launchDequant<F32>(out, q, scale, rows, cols, s);
+    case LLAISYS_DTYPE_BF16: return launchDequant<BF16>(out, q, scale, rows, cols, s);
+    case LLAISYS_DTYPE_F16: return launchDequant<F16>(out, q, scale, rows, cols, s);
+    default: return;
+    }
+}
+
+} // namespace llaisys::kernels

@@ -1,0 +1,59 @@
+// Host-side launchers of the gfx950 kernels: plain pointers, sizes and a stream.
+//
+// Callers (the op dispatchers) have already validated shapes, dtypes and devices; the
+// launchers choose the kernel variant (vectorised 16-byte path when sizes and addresses
+// allow, scalar path otherwise) and enqueue it asynchronously on `stream`.
+#pragma once
+
+#include "llaisys.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace llaisys::kernels {
+
+// y = rms_norm(x) per row of `cols`; when `residual` is non-null the input is first
+// h = round(x + residual), h is stored to `residual_out` and normalised instead.
+void rmsNorm(void *out, void *residual_out, const void *in, const void *residual,
+             const void *weight, size_t rows, size_t cols, float eps, llaisysDataType_t dt,
+             hipStream_t stream);
+
+// Rotate-half RoPE on [seq, n_heads, head_dim] with int64 positions.
+void rope(void *out, const void *in, const int64_t *pos, size_t seq, size_t n_heads,
+          size_t head_dim, float theta, llaisysDataType_t dt, hipStream_t stream);
+
+// out = up * gate / (1 + exp(-gate)) over n elements.
+void swiglu(void *out, const void *gate, const void *up, size_t n, llaisysDataType_t dt,
+            hipStream_t stream);
+
+// c = a + b over n elements (half types: f32 add, then round).
+void add(void *c, const void *a, const void *b, size_t n, llaisysDataType_t dt,
+         hipStream_t stream);
+
+// out[i, :] = weight[index[i], :] for rows of `row_bytes`; an id outside [0, vocab)
+// leaves its row untouched and ORs 1 into *err.
+void embedding(void *out, const void *index, bool index_i64, size_t n_index, const void *weight,
+               size_t vocab, size_t row_bytes, int *err, hipStream_t stream);
+
+// Per-row argmax of vals [rows, cols]; idx is I32 or I64, val has the dtype of vals.
+void argmaxRows(void *idx, bool idx_i64, void *val, const void *vals, size_t rows, size_t cols,
+                llaisysDataType_t dt, hipStream_t stream);
+
+// Flat argmax over n elements; `workspace` (>= argmaxWorkspaceBytes(n)) holds the
+// per-block partials and a completion counter that must be zero before the first call
+// (the kernel leaves it zero again).
+size_t argmaxWorkspaceBytes(size_t n, llaisysDataType_t dt);
+void argmax(void *idx, bool idx_i64, void *val, const void *vals, size_t n,
+            llaisysDataType_t dt, void *workspace, hipStream_t stream);
+
+// INT8 symmetric absmax quantization per row of `cols` elements.
+void quantizeInt8(int8_t *q, float *scale, const void *in, size_t rows, size_t cols,
+                  llaisysDataType_t dt, hipStream_t stream);
+
+// out = T(float(q) * scale[row]).
+void dequantizeInt8(void *out, const int8_t *q, const float *scale, size_t rows, size_t cols,
+                    llaisysDataType_t dt, hipStream_t stream);
+
+} // namespace llaisys::kernels

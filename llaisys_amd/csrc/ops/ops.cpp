@@ -1,0 +1,246 @@
+// Operator dispatchers.
+//
+// Each op runs the checks of the reference dispatcher it replaces (cited per op), then
+// makes the tensors' device current and launches the gfx950 kernel on that device's
+// context stream.  Where the reference leaves an output size unchecked (rms_norm, swiglu
+// dtypes, embedding output, argmax outputs) a check is added here: on a GPU an undersized
+// output would be an out-of-bounds write, not a CPU heap overrun.  Only the AMD device
+// computes; CPU tensors raise "Unsupported device" (the reference CPU kernels are the
+// test oracle, not a fallback of this library).
+#include "ops.hpp"
+
+#include "../device/runtime_api.hpp"
+#include "../kernels/launch.hpp"
+#include "../utils/check.hpp"
+#include "../utils/types.hpp"
+
+namespace llaisys::ops {
+
+namespace {
+
+bool isFloat(llaisysDataType_t dt) {
+    return dt == LLAISYS_DTYPE_F32 || dt == LLAISYS_DTYPE_BF16 || dt == LLAISYS_DTYPE_F16;
+}
+
+void requireFloat(llaisysDataType_t dt) {
+    if (!isFloat(dt)) EXCEPTION_UNSUPPORTED_DATATYPE(dt);
+}
+
+// Makes the device of `t` current and returns its stream; only the AMD device computes.
+hipStream_t streamFor(const tensor_t &t) {
+    if (t->deviceType() != LLAISYS_DEVICE_AMD) EXCEPTION_UNSUPPORTED_DEVICE;
+    auto &ctx = core::context();
+    ctx.setDevice(t->deviceType(), t->deviceId());
+    return static_cast<hipStream_t>(ctx.runtime().stream());
+}
+
+// Reports a failed launch (bad configuration, no code object for this GPU) at the call.
+void launched(const char *op) { device::amd::check(hipGetLastError(), op); }
+
+size_t lastDim(const tensor_t &t) {
+    ASSERT(t->ndim() >= 1, "tensor must have at least one dimension");
+    return t->shape().back();
+}
+
+} // namespace
+
+// reference src/ops/add/op.cpp:11-38
+void add(tensor_t c, tensor_t a, tensor_t b) {
+    CHECK_SAME_DEVICE(c, a, b);
+    CHECK_SAME_SHAPE(c->shape(), a->shape(), b->shape());
+    CHECK_SAME_DTYPE(c->dtype(), a->dtype(), b->dtype());
+    ASSERT(c->isContiguous() && a->isContiguous() && b->isContiguous(),
+           "Add: all tensors must be contiguous.");
+    requireFloat(c->dtype());
+    auto s = streamFor(c);
+    kernels::add(c->data(), a->data(), b->data(), c->numel(), c->dtype(), s);
+    launched("add");
+}
+
+// reference src/ops/argmax/op.cpp:13-40 (flat over every element of vals)
+void argmax(tensor_t max_idx, tensor_t max_val, tensor_t vals) {
+    CHECK_SAME_DEVICE(max_idx, max_val, vals);
+    CHECK_SAME_DTYPE(max_val->dtype(), vals->dtype());
+    ASSERT(max_idx->isContiguous() && max_val->isContiguous() && vals->isContiguous(),
+           "Argmax: input tensor must be contiguous.");
+    ASSERT(max_idx->dtype() == LLAISYS_DTYPE_I32 || max_idx->dtype() == LLAISYS_DTYPE_I64,
+           "Argmax: max_idx must be INT32 or INT64");
+    requireFloat(vals->dtype());
+    ASSERT(max_idx->numel() >= 1 && max_val->numel() >= 1, "Argmax: outputs must hold one element");
+    auto s = streamFor(vals);
+    const size_t n = vals->numel();
+    if (n == 0) return;
+    void *ws = device::amd::workspace(vals->deviceId(), kernels::argmaxWorkspaceBytes(n, vals->dtype()));
+    kernels::argmax(max_idx->data(), max_idx->dtype() == LLAISYS_DTYPE_I64, max_val->data(),
+                    vals->data(), n, vals->dtype(), ws, s);
+    launched("argmax");
+}
+
+// Row-wise variant: the reference argmax applied to each row of vals [rows, cols].
+void argmaxRows(tensor_t max_idx, tensor_t max_val, tensor_t vals) {
+    CHECK_SAME_DEVICE(max_idx, max_val, vals);
+    CHECK_SAME_DTYPE(max_val->dtype(), vals->dtype());
+    ASSERT(max_idx->isContiguous() && max_val->isContiguous() && vals->isContiguous(),
+           "ArgmaxRows: tensors must be contiguous.");
+    ASSERT(max_idx->dtype() == LLAISYS_DTYPE_I32 || max_idx->dtype() == LLAISYS_DTYPE_I64,
+           "ArgmaxRows: max_idx must be INT32 or INT64");
+    requireFloat(vals->dtype());
+    ASSERT(vals->ndim() == 2, "ArgmaxRows: vals must be 2-D [rows, cols]");
+    const size_t rows = vals->shape()[0], cols = vals->shape()[1];
+    ASSERT(max_idx->numel() == rows && max_val->numel() == rows,
+           "ArgmaxRows: outputs must hold one element per row");
+    auto s = streamFor(vals);
+    kernels::argmaxRows(max_idx->data(), max_idx->dtype() == LLAISYS_DTYPE_I64, max_val->data(),
+                        vals->data(), rows, cols, vals->dtype(), s);
+    launched("argmaxRows");
+}
+
+// reference src/ops/embedding/op.cpp:15-46
+void embedding(tensor_t out, tensor_t index, tensor_t weight) {
+    CHECK_SAME_DEVICE(out, index, weight);
+    ASSERT(out->isContiguous() && index->isContiguous() && weight->isContiguous(),
+           "Embedding inputs must be contiguous");
+    CHECK_SAME_DTYPE(out->dtype(), weight->dtype());
+    ASSERT(index->dtype() == LLAISYS_DTYPE_I32 || index->dtype() == LLAISYS_DTYPE_I64,
+           "Embedding parameter index data type must be INT32 or INT64");
+    ASSERT(weight->ndim() == 2, "Embedding weight must be 2-D [vocab, dim]");
+    const size_t n = index->numel();
+    const size_t vocab = weight->shape()[0], dim = weight->shape()[1];
+    ASSERT(out->numel() == n * dim, "Embedding output must hold index.numel() rows of dim");
+    auto s = streamFor(weight);
+    int *err = device::amd::errorWord(weight->deviceId());
+    kernels::embedding(out->data(), index->data(), index->dtype() == LLAISYS_DTYPE_I64, n,
+                       weight->data(), vocab, dim * weight->elementSize(), err, s);
+    launched("embedding");
+}
+
+// reference src/ops/rms_norm/op.cpp:9-42
+void rmsNorm(tensor_t out, tensor_t in, tensor_t weight, float eps) {
+    CHECK_SAME_DEVICE(out, in, weight);
+    const size_t cols = lastDim(in);
+    ASSERT(weight->ndim() == 1, "RMSNorm weight must be 1D");
+    ASSERT(weight->shape()[0] == cols, "RMSNorm weight shape mismatch");
+    CHECK_SAME_DTYPE(out->dtype(), in->dtype(), weight->dtype());
+    ASSERT(out->isContiguous() && in->isContiguous() && weight->isContiguous(),
+           "RMSNorm input must be contiguous");
+    CHECK_SAME_SHAPE(out->shape(), in->shape());
+    requireFloat(in->dtype());
+    auto s = streamFor(in);
+    kernels::rmsNorm(out->data(), nullptr, in->data(), nullptr, weight->data(),
+                     cols ? in->numel() / cols : 0, cols, eps, in->dtype(), s);
+    launched("rmsNorm");
+}
+
+// Fused residual add + rms_norm (reference call pattern src/models/qwen2/layer.hpp:60-71:
+// ops::add then RMSNorm; checks of both dispatchers).
+void addRmsNorm(tensor_t out, tensor_t residual_out, tensor_t in, tensor_t residual,
+                tensor_t weight, float eps) {
+    CHECK_SAME_DEVICE(out, residual_out, in, residual, weight);
+    const size_t cols = lastDim(in);
+    ASSERT(weight->ndim() == 1, "RMSNorm weight must be 1D");
+    ASSERT(weight->shape()[0] == cols, "RMSNorm weight shape mismatch");
+    CHECK_SAME_DTYPE(out->dtype(), residual_out->dtype(), in->dtype(), residual->dtype(),
+                     weight->dtype());
+    CHECK_SAME_SHAPE(out->shape(), residual_out->shape(), in->shape(), residual->shape());
+    ASSERT(out->isContiguous() && residual_out->isContiguous() && in->isContiguous() &&
+               residual->isContiguous() && weight->isContiguous(),
+           "AddRmsNorm: all tensors must be contiguous");
+    requireFloat(in->dtype());
+    auto s = streamFor(in);
+    kernels::rmsNorm(out->data(), residual_out->data(), in->data(), residual->data(),
+                     weight->data(), cols ? in->numel() / cols : 0, cols, eps, in->dtype(), s);
+    launched("rmsNorm");
+}
+
+// reference src/ops/rope/op.cpp:8-51
+void rope(tensor_t out, tensor_t in, tensor_t pos_ids, float theta) {
+    CHECK_SAME_DEVICE(out, in, pos_ids);
+    ASSERT(in->isContiguous() && out->isContiguous() && pos_ids->isContiguous(),
+           "RoPE paremeter must be contiguous");
+    ASSERT(in->ndim() == 3, "input shape must be 3");
+    CHECK_SAME_SHAPE(in->shape(), out->shape());
+    const size_t seq = in->shape()[0], nh = in->shape()[1], d = in->shape()[2];
+    ASSERT(pos_ids->numel() == seq, "pos_ids length must match Seq_Len");
+    ASSERT(d % 2 == 0, "Head dimension must be even for RoPE");
+    CHECK_SAME_DTYPE(in->dtype(), out->dtype());
+    ASSERT(pos_ids->dtype() == LLAISYS_DTYPE_I64, "token id data type must be INT64");
+    requireFloat(in->dtype());
+    auto s = streamFor(in);
+    kernels::rope(out->data(), in->data(), reinterpret_cast<const int64_t *>(pos_ids->data()),
+                  seq, nh, d, theta, in->dtype(), s);
+    launched("rope");
+}
+
+// reference src/ops/swiglu/op.cpp:7-38
+void swiglu(tensor_t out, tensor_t gate, tensor_t up) {
+    CHECK_SAME_DEVICE(out, gate, up);
+    ASSERT(out->isContiguous() && gate->isContiguous() && up->isContiguous(), "must be contiguous");
+    CHECK_SAME_SHAPE(out->shape(), gate->shape(), up->shape());
+    ASSERT(out->ndim() == 2, "ensure 2D");
+    CHECK_SAME_DTYPE(out->dtype(), gate->dtype(), up->dtype());
+    requireFloat(out->dtype());
+    auto s = streamFor(gate);
+    kernels::swiglu(out->data(), gate->data(), up->data(), gate->numel(), out->dtype(), s);
+    launched("swiglu");
+}
+
+namespace {
+void checkQuantPair(const tensor_t &codes, const tensor_t &scale, const tensor_t &values,
+                    const char *op) {
+    CHECK_SAME_DEVICE(codes, scale, values);
+    ASSERT(codes->isContiguous() && scale->isContiguous() && values->isContiguous(),
+           op << ": tensors must be contiguous");
+    ASSERT(codes->dtype() == LLAISYS_DTYPE_I8, op << ": codes must be INT8");
+    ASSERT(scale->dtype() == LLAISYS_DTYPE_F32, op << ": scales must be F32");
+    requireFloat(values->dtype());
+    CHECK_SAME_SHAPE(codes->shape(), values->shape());
+    const size_t cols = lastDim(values);
+    ASSERT(scale->numel() * cols == values->numel(), op << ": one scale per last-dim row");
+}
+} // namespace
+
+void quantizeInt8(tensor_t q, tensor_t scale, tensor_t in) {
+    checkQuantPair(q, scale, in, "QuantizeInt8");
+    auto s = streamFor(in);
+    const size_t cols = lastDim(in);
+    kernels::quantizeInt8(reinterpret_cast<int8_t *>(q->data()),
+                          reinterpret_cast<float *>(scale->data()), in->data(),
+                          cols ? in->numel() / cols : 0, cols, in->dtype(), s);
+    launched("quantizeInt8");
+}
+
+void dequantizeInt8(tensor_t out, tensor_t q, tensor_t scale) {
+    checkQuantPair(q, scale, out, "DequantizeInt8");
+    auto s = streamFor(out);
+    const size_t cols = lastDim(out);
+    kernels::dequantizeInt8(out->data(), reinterpret_cast<const int8_t *>(q->data()),
+                            reinterpret_cast<const float *>(scale->data()),
+                            cols ? out->numel() / cols : 0, cols, out->dtype(), s);
+    launched("dequantizeInt8");
+}
+
+// Replaces the f32 cache-row copy of src/models/qwen2/attention.hpp:108-123.
+void kvAppendInt8(tensor_t cache_q, tensor_t cache_scale, tensor_t kv, size_t pos) {
+    CHECK_SAME_DEVICE(cache_q, cache_scale, kv);
+    ASSERT(cache_q->isContiguous() && cache_scale->isContiguous() && kv->isContiguous(),
+           "KVAppendInt8: tensors must be contiguous");
+    ASSERT(cache_q->dtype() == LLAISYS_DTYPE_I8, "KVAppendInt8: cache codes must be INT8");
+    ASSERT(cache_scale->dtype() == LLAISYS_DTYPE_F32, "KVAppendInt8: cache scales must be F32");
+    requireFloat(kv->dtype());
+    ASSERT(cache_q->ndim() == 3 && kv->ndim() == 3 && cache_scale->ndim() == 2,
+           "KVAppendInt8: cache [max_seq, n_kvh, d], scales [max_seq, n_kvh], kv [n_tok, n_kvh, d]");
+    const size_t max_seq = cache_q->shape()[0], nkvh = cache_q->shape()[1], d = cache_q->shape()[2];
+    const size_t ntok = kv->shape()[0];
+    ASSERT(kv->shape()[1] == nkvh && kv->shape()[2] == d, "KVAppendInt8: kv head shape mismatch");
+    ASSERT(cache_scale->shape()[0] == max_seq && cache_scale->shape()[1] == nkvh,
+           "KVAppendInt8: scale cache shape mismatch");
+    ASSERT(pos <= max_seq && ntok <= max_seq - pos, "KVAppendInt8: append past the cache end");
+    auto s = streamFor(kv);
+    const size_t r0 = pos * nkvh;
+    kernels::quantizeInt8(reinterpret_cast<int8_t *>(cache_q->data()) + r0 * d,
+                          reinterpret_cast<float *>(cache_scale->data()) + r0, kv->data(),
+                          ntok * nkvh, d, kv->dtype(), s);
+    launched("quantizeInt8");
+}
+
+} // namespace llaisys::ops

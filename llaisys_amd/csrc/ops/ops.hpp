@@ -1,0 +1,21 @@
+// Operator dispatchers: argument checks, device selection, kernel launch.
+#pragma once
+
+#include "../tensor/tensor.hpp"
+
+namespace llaisys::ops {
+
+void add(tensor_t c, tensor_t a, tensor_t b);
+void argmax(tensor_t max_idx, tensor_t max_val, tensor_t vals);
+void argmaxRows(tensor_t max_idx, tensor_t max_val, tensor_t vals);
+void embedding(tensor_t out, tensor_t index, tensor_t weight);
+void rmsNorm(tensor_t out, tensor_t in, tensor_t weight, float eps);
+void addRmsNorm(tensor_t out, tensor_t residual_out, tensor_t in, tensor_t residual,
+                tensor_t weight, float eps);
+void rope(tensor_t out, tensor_t in, tensor_t pos_ids, float theta);
+void swiglu(tensor_t out, tensor_t gate, tensor_t up);
+void quantizeInt8(tensor_t q, tensor_t scale, tensor_t in);
+void dequantizeInt8(tensor_t out, tensor_t q, tensor_t scale);
+void kvAppendInt8(tensor_t cache_q, tensor_t cache_scale, tensor_t kv, size_t pos);
+
+} // namespace llaisys::ops

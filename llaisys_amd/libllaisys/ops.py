@@ -1,0 +1,43 @@
+"""ctypes signatures of the op entry points (include/llaisys/ops.h).
+
+The nine reference entry points have the argtypes of the reference's
+python/llaisys/libllaisys/ops.py:4-36; the additive ones are bound when present, so the
+same loader also binds the reference library (used to write golden vectors).
+"""
+from ctypes import c_float, c_size_t
+
+from .tensor import llaisysTensor_t
+
+T = llaisysTensor_t
+
+REFERENCE_OPS = {
+    "llaisysAdd": [T, T, T],
+    "llaisysArgmax": [T, T, T],
+    "llaisysEmbedding": [T, T, T],
+    "llaisysLinear": [T, T, T, T],
+    "llaisysRearrange": [T, T],
+    "llaisysRmsNorm": [T, T, T, c_float],
+    "llaisysROPE": [T, T, T, c_float],
+    "llaisysSelfAttention": [T, T, T, T, c_float],
+    "llaisysSwiGLU": [T, T, T],
+}
+
+ADDED_OPS = {
+    "llaisysAddRmsNorm": [T, T, T, T, T, c_float],
+    "llaisysArgmaxRows": [T, T, T],
+    "llaisysQuantizeInt8": [T, T, T],
+    "llaisysDequantizeInt8": [T, T, T],
+    "llaisysKVAppendInt8": [T, T, T, c_size_t],
+}
+
+
+def load_ops(lib):
+    for name, args in REFERENCE_OPS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = None
+    for name, args in ADDED_OPS.items():
+        if hasattr(lib, name):
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = None

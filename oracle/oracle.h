@@ -1,0 +1,52 @@
+/*
+ * CPU oracle for the LLAISYS per-layer ops -- TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference's CPU arithmetic (cited per function in
+ * oracle.c).  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * may load it, and only as the checker / timed CPU baseline.  The product library
+ * (llaisys_amd, libllaisys.so) never links, loads or calls it.
+ *
+ * Data-type codes are the llaisysDataType_t values: F16 = 12, F32 = 13, BF16 = 19,
+ * I32 = 5, I64 = 6.  All buffers are contiguous host memory.
+ */
+#ifndef LLAISYS_ORACLE_H
+#define LLAISYS_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define ORC_F16 12
+#define ORC_F32 13
+#define ORC_BF16 19
+#define ORC_I32 5
+#define ORC_I64 6
+
+uint16_t orc_f32_to_bf16(float v);
+float orc_bf16_to_f32(uint16_t v);
+uint16_t orc_f32_to_f16(float v);
+float orc_f16_to_f32(uint16_t v);
+
+void orc_add(void *c, const void *a, const void *b, size_t n, int dtype);
+void orc_rms_norm(void *out, const void *in, const void *w, size_t rows, size_t cols,
+                  float eps, int dtype);
+void orc_add_rms_norm(void *out, void *residual_out, const void *in, const void *residual,
+                      const void *w, size_t rows, size_t cols, float eps, int dtype);
+void orc_rope(void *out, const void *in, const int64_t *pos_ids, size_t seq_len,
+              size_t n_heads, size_t head_dim, float theta, int dtype);
+void orc_swiglu(void *out, const void *gate, const void *up, size_t n, int dtype);
+/* Returns 0, or -1 (after copying the rows before it) at the first id outside [0, vocab). */
+int orc_embedding(void *out, const void *index, int index_dtype, size_t n_index,
+                  const void *weight, size_t vocab, size_t dim, int dtype);
+void orc_argmax(void *max_idx, int idx_dtype, void *max_val, const void *vals, size_t n,
+                int dtype);
+void orc_argmax_rows(void *max_idx, int idx_dtype, void *max_val, const void *vals,
+                     size_t rows, size_t cols, int dtype);
+void orc_quantize_int8(int8_t *q, float *scale, const void *in, size_t rows, size_t cols,
+                       int dtype);
+void orc_dequantize_int8(void *out, const int8_t *q, const float *scale, size_t rows,
+                         size_t cols, int dtype);
+/* Returns -1 if pos + n_tok > max_seq (nothing written), else 0. */
+int orc_kv_append_int8(int8_t *cache_q, float *cache_scale, size_t max_seq, const void *kv,
+                       size_t n_tok, size_t n_kvh, size_t head_dim, size_t pos, int dtype);
+
+#endif

@@ -1,0 +1,400 @@
+"""Parity of the gfx950 kernels with the CPU oracle and the reference golden vectors.
+
+Every test calls the ops through the C ABI (llaisys_amd.Ops -> libllaisys.so) on device
+AMD:0 and compares with oracle/ (itself pinned to the reference, tests/test_oracle.py)
+under the rules of tests/numerics.py: integer work bit-exact, f32 1e-5 relative, bf16 and
+f16 within 2 ulps.  Shapes: the reference tests' own, the BASELINE configs (full size where
+the single-thread oracle finishes in seconds) and edge cases that take the scalar kernels
+(ragged rows, unaligned slices) or the boundary paths (empty, NaN / tie / -inf, out-of-range
+ids, appends at the cache end).
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+import llaisys_amd as L
+import oracle
+from llaisys_amd.hostfmt import bf16_to_f32, f32_to_bf16
+from numerics import assert_close, assert_exact
+
+pytestmark = pytest.mark.gpu
+
+AMD = dict(device=L.DeviceType.AMD, device_id=0)
+DTS = {"f32": L.DataType.F32, "bf16": L.DataType.BF16, "f16": L.DataType.F16}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu_present():
+    n = L.RuntimeAPI(L.DeviceType.AMD).get_device_count()
+    assert n >= 1, "no AMD GPU visible: the gpu tests need the HIP path"
+
+
+def sample(rng, shape, dt, scale=1.0, loc=0.0):
+    x = (loc + scale * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+    return {"f32": x, "bf16": f32_to_bf16(x), "f16": x.astype(np.float16)}[dt]
+
+
+def seed_of(*args):
+    """Deterministic per-case seed (str hashes are salted per process)."""
+    return zlib.crc32(repr(args).encode())
+
+
+def dev(a, dt=None):
+    return L.Tensor.from_numpy(a, dt, **AMD)
+
+
+def empty(shape, dt):
+    return L.Tensor(shape, dt, **AMD)
+
+
+def no_device_error():
+    assert L.take_device_error() == 0
+
+
+# ---- reference golden vectors -------------------------------------------------------
+
+def test_golden_vectors_on_gpu(golden):
+    checked = 0
+    for (op, dt, case), c in golden.items():
+        what = f"{op}/{dt}/{case}"
+        if op == "rms_norm":
+            y = empty(c["x"].shape, DTS[dt])
+            L.Ops.rms_norm(y, dev(c["x"], DTS[dt]), dev(c["w"], DTS[dt]), float(c["eps"]))
+            assert_close(y.numpy(), c["y"], what)
+        elif op == "add":
+            out = empty(c["a"].shape, DTS[dt])
+            L.Ops.add(out, dev(c["a"], DTS[dt]), dev(c["b"], DTS[dt]))
+            assert_exact(out.numpy(), c["c"], what)  # one rounding of an exact f32 sum
+        elif op == "rope":
+            y = empty(c["x"].shape, DTS[dt])
+            L.Ops.rope(y, dev(c["x"], DTS[dt]), dev(c["pos"]), float(c["theta"]))
+            assert_close(y.numpy(), c["y"], what)
+        elif op == "swiglu":
+            y = empty(c["gate"].shape, DTS[dt])
+            L.Ops.swiglu(y, dev(c["gate"], DTS[dt]), dev(c["up"], DTS[dt]))
+            assert_close(y.numpy(), c["y"], what)
+        elif op == "embedding":
+            out = empty(c["out"].shape, DTS[dt])
+            L.Ops.embedding(out, dev(c["idx"]), dev(c["w"], DTS[dt]))
+            assert_exact(out.numpy(), c["out"], what)
+        elif op == "argmax":
+            i, v = empty((1,), L.DataType.I64), empty((1,), DTS[dt])
+            L.Ops.argmax(i, v, dev(c["vals"], DTS[dt]))
+            assert_exact(i.numpy(), c["idx"], what)
+            assert_exact(v.numpy(), c["val"], what)
+        else:
+            continue
+        checked += 1
+    assert checked == len(golden)
+    no_device_error()
+
+
+# ---- rms_norm and the fused residual variant -----------------------------------------
+
+RMS_SHAPES = [
+    ((1, 4), 1e-5), ((512, 4096), 1e-5),        # reference test shapes
+    ((128, 1536), 1e-6),                        # config 0 (f32) / Qwen2 hidden
+    ((8192, 1536), 1e-6),                       # config 1
+    ((64, 8960), 1e-6),                         # 1024-lane rows
+    ((33, 1000), 1e-5), ((5, 20000), 1e-5),     # ragged / wider than the register plan
+    ((3, 8), 1e-5), ((2, 100000), 1e-6),        # tiny, huge rows (scalar kernel)
+]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape,eps", RMS_SHAPES)
+def test_rms_norm(dt, shape, eps):
+    rng = np.random.default_rng(seed_of(shape, dt))
+    x, w = sample(rng, shape, dt), sample(rng, shape[-1:], dt, 0.1, 1.0)
+    y = empty(shape, DTS[dt])
+    L.Ops.rms_norm(y, dev(x, DTS[dt]), dev(w, DTS[dt]), eps)
+    assert_close(y.numpy(), oracle.rms_norm(x, w, eps), f"rms_norm {dt} {shape}")
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", [(8192, 1536), (2048, 1536), (7, 4096), (9, 1000), (1, 12)])
+def test_add_rms_norm(dt, shape):
+    rng = np.random.default_rng(11)
+    x, r = sample(rng, shape, dt), sample(rng, shape, dt)
+    w = sample(rng, shape[-1:], dt, 0.1, 1.0)
+    y, h = empty(shape, DTS[dt]), empty(shape, DTS[dt])
+    L.Ops.add_rms_norm(y, h, dev(x, DTS[dt]), dev(r, DTS[dt]), dev(w, DTS[dt]), 1e-6)
+    ey, eh = oracle.add_rms_norm(x, r, w, 1e-6)
+    assert_exact(h.numpy(), eh, "residual")  # the residual stream is bit-exact
+    assert_close(y.numpy(), ey, "normed")
+
+
+def test_add_rms_norm_in_place_residual():
+    rng = np.random.default_rng(12)
+    x, r = sample(rng, (256, 1536), "bf16"), sample(rng, (256, 1536), "bf16")
+    w = sample(rng, (1536,), "bf16", 0.1, 1.0)
+    tr = dev(r, L.DataType.BF16)
+    y = empty((256, 1536), L.DataType.BF16)
+    L.Ops.add_rms_norm(y, tr, dev(x, L.DataType.BF16), tr, dev(w, L.DataType.BF16), 1e-6)
+    ey, eh = oracle.add_rms_norm(x, r, w, 1e-6)
+    assert_exact(tr.numpy(), eh)
+    assert_close(y.numpy(), ey)
+
+
+def test_rms_norm_unaligned_slice_takes_the_scalar_path():
+    rng = np.random.default_rng(13)
+    x = sample(rng, (9, 1536), "bf16")
+    w = sample(rng, (1536,), "bf16", 0.1, 1.0)
+    big = dev(np.concatenate([np.zeros(3, np.uint16), x.reshape(-1)]), L.DataType.BF16)
+    xs = big.slice(0, 3, 3 + x.size).view(9, 1536)  # 6-byte offset: not 16-byte aligned
+    y = empty((9, 1536), L.DataType.BF16)
+    L.Ops.rms_norm(y, xs, dev(w, L.DataType.BF16), 1e-6)
+    assert_close(y.numpy(), oracle.rms_norm(x, w, 1e-6))
+
+
+# ---- rope ------------------------------------------------------------------------------
+
+ROPE = [
+    ((2, 1, 4), 0, 1e4),            # reference test
+    ((512, 4, 4096), 512, 1e4),     # reference test (head_dim 4096: scalar kernel)
+    ((128, 12, 128), 0, 1e4),       # config 0 q
+    ((128, 2, 128), 0, 1e4),        # config 0 k
+    ((8192, 12, 128), 0, 1e4),      # config 1 q
+    ((8192, 2, 128), 0, 1e4),       # config 1 k
+    ((64, 32, 128), 16320, 5e5),    # config 2 heads, late positions
+    ((7, 3, 6), 3, 1e4),            # odd half-dim
+    ((5, 4, 64), 100000, 1e6),
+]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape,p0,theta", ROPE)
+def test_rope(dt, shape, p0, theta):
+    if shape == (512, 4, 4096) and dt != "bf16":
+        pytest.skip("one dtype is enough for the 8M-element reference shape")
+    rng = np.random.default_rng(seed_of(shape, dt))
+    x = sample(rng, shape, dt)
+    pos = np.arange(p0, p0 + shape[0], dtype=np.int64)
+    y = empty(shape, DTS[dt])
+    L.Ops.rope(y, dev(x, DTS[dt]), dev(pos), theta)
+    assert_close(y.numpy(), oracle.rope(x, pos, theta), f"rope {dt} {shape}")
+
+
+def test_rope_shuffled_positions():
+    rng = np.random.default_rng(14)
+    x = sample(rng, (300, 2, 128), "bf16")
+    pos = rng.integers(0, 32768, size=300).astype(np.int64)
+    y = empty(x.shape, L.DataType.BF16)
+    L.Ops.rope(y, dev(x, L.DataType.BF16), dev(pos), 1e4)
+    assert_close(y.numpy(), oracle.rope(x, pos, 1e4))
+
+
+# ---- swiglu / add ------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape,gs", [((2, 3), 1.0), ((512, 4096), 1.0), ((128, 8960), 1.0),
+                                      ((8192, 8960), 1.0), ((33, 1001), 6.0)])
+def test_swiglu(dt, shape, gs):
+    if shape == (8192, 8960) and dt == "f16":
+        pytest.skip("covered in f32 and bf16")
+    rng = np.random.default_rng(seed_of(shape, dt))
+    g, u = sample(rng, shape, dt, gs), sample(rng, shape, dt)
+    y = empty(shape, DTS[dt])
+    L.Ops.swiglu(y, dev(g, DTS[dt]), dev(u, DTS[dt]))
+    assert_close(y.numpy(), oracle.swiglu(g, u), f"swiglu {dt} {shape}")
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", [(2, 3), (512, 4096), (13, 1001)])
+def test_add(dt, shape):
+    rng = np.random.default_rng(5)
+    a, b = sample(rng, shape, dt), sample(rng, shape, dt)
+    c = empty(shape, DTS[dt])
+    L.Ops.add(c, dev(a, DTS[dt]), dev(b, DTS[dt]))
+    assert_exact(c.numpy(), oracle.add(a, b))
+
+
+# ---- embedding ---------------------------------------------------------------------------
+
+_TABLES = {}
+
+
+def table(vocab, dim, dt):
+    """Embedding tables are built once per shape (the Qwen2 table is 233M elements)."""
+    key = (vocab, dim, dt)
+    if key not in _TABLES:
+        _TABLES.clear()
+        w = sample(np.random.default_rng(vocab + dim), (vocab, dim), dt, 0.02)
+        _TABLES[key] = (w, dev(w, DTS[dt]))
+    return _TABLES[key]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("vocab,dim", [(151936, 1536), (512, 4096), (1000, 3), (300, 1001)])
+@pytest.mark.parametrize("n", [1, 50, 128, 8192])
+@pytest.mark.parametrize("idt", [np.int32, np.int64])
+def test_embedding(dt, vocab, dim, n, idt):
+    rng = np.random.default_rng(vocab + dim + n)
+    w, tw = table(vocab, dim, dt)
+    idx = rng.integers(0, vocab, size=n).astype(idt)
+    idx[: min(n, 3)] = [0, vocab - 1, 0][: min(n, 3)]
+    out = empty((n, dim), DTS[dt])
+    L.Ops.embedding(out, dev(idx), tw)
+    exp, st = oracle.embedding(idx, w)
+    assert st == 0
+    assert_exact(out.numpy(), exp)
+    no_device_error()
+
+
+def test_embedding_out_of_range_sets_the_device_error():
+    w = sample(np.random.default_rng(0), (64, 256), "bf16")
+    idx = np.array([3, 64, -1, 5], np.int64)
+    out = dev(np.zeros((4, 256), np.uint16), L.DataType.BF16)
+    L.Ops.embedding(out, dev(idx), dev(w, L.DataType.BF16))
+    assert L.take_device_error() == 1
+    got = out.numpy()
+    assert np.array_equal(got[0], w[3]) and np.array_equal(got[3], w[5])
+    assert not got[1].any() and not got[2].any()  # out-of-range rows untouched
+    assert L.take_device_error() == 0  # the error word was cleared
+
+
+# ---- argmax ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("n", [1, 4, 4096, 151936, 8193, 3_000_001])
+@pytest.mark.parametrize("idt", [L.DataType.I64, L.DataType.I32])
+def test_argmax_flat(dt, n, idt):
+    rng = np.random.default_rng(n)
+    v = sample(rng, (n,), dt)
+    i, m = empty((1,), idt), empty((1,), DTS[dt])
+    L.Ops.argmax(i, m, dev(v, DTS[dt]))
+    ei, ev = oracle.argmax(v, np.int64 if idt == L.DataType.I64 else np.int32)
+    assert i.numpy()[0] == ei
+    assert_exact(m.numpy(), np.array([ev]))
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_argmax_ties_nans_and_infs(dt):
+    rng = np.random.default_rng(3)
+    n = 151936
+    base = sample(rng, (n,), dt)
+    hi = sample(rng, (1,), dt, 0, 9.0)[0]
+    nan = sample(rng, (1,), dt, 0, np.nan)[0]
+    ninf = sample(rng, (1,), dt, 0, -np.inf)[0]
+    cases = []
+    t = base.copy(); t[[90000, 4097, 150000, 4096 + 8 * 256]] = hi; cases.append(t)  # ties across blocks
+    t = base.copy(); t[[1, 5000, 151935]] = nan; cases.append(t)                     # NaN never wins
+    t = base.copy(); t[0] = nan; cases.append(t)                                      # NaN at 0 wins
+    cases.append(np.full(n, ninf, dtype=base.dtype))                                 # all -inf -> 0
+    t = np.full(n, ninf, dtype=base.dtype); t[77777] = nan; cases.append(t)
+    t = np.full(n, hi, dtype=base.dtype); cases.append(t)                            # all equal -> 0
+    for k, v in enumerate(cases):
+        i, m = empty((1,), L.DataType.I64), empty((1,), DTS[dt])
+        L.Ops.argmax(i, m, dev(v, DTS[dt]))
+        ei, ev = oracle.argmax(v)
+        assert i.numpy()[0] == ei, (dt, k)
+        assert_exact(m.numpy(), np.array([ev]), f"{dt} case {k}")
+        # the row variant agrees on the same data
+        ri, rm = empty((2,), L.DataType.I64), empty((2,), DTS[dt])
+        L.Ops.argmax_rows(ri, rm, dev(np.stack([v, v[::-1]]), DTS[dt]))
+        eri, erm = oracle.argmax_rows(np.stack([v, v[::-1]]))
+        assert np.array_equal(ri.numpy(), eri)
+        assert_exact(rm.numpy(), erm)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("rows,cols", [(2048, 151936), (3, 1001), (64, 7), (1, 151936)])
+def test_argmax_rows(dt, rows, cols):
+    rng = np.random.default_rng(rows * cols)
+    v = sample(rng, (rows, cols), dt)
+    v[1 % rows, 10 % cols] = v[1 % rows].max()  # a tie in row 1
+    i, m = empty((rows,), L.DataType.I32), empty((rows,), DTS[dt])
+    L.Ops.argmax_rows(i, m, dev(v, DTS[dt]))
+    ei, ev = oracle.argmax_rows(v, np.int32)
+    assert_exact(i.numpy(), ei)
+    assert_exact(m.numpy(), ev)
+
+
+# ---- INT8 quantization -------------------------------------------------------------------
+
+def with_outliers(rng, shape, dt, scale):
+    x = (scale * rng.standard_normal(shape)).astype(np.float32)
+    x[rng.random(shape) < 0.01] *= 20
+    return {"f32": x, "bf16": f32_to_bf16(x), "f16": x.astype(np.float16)}[dt]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("shape", [(8960, 1536), (1536, 8960), (4096, 128), (5, 1001), (3, 20000), (7, 8)])
+def test_quantize_dequantize(dt, shape):
+    rng = np.random.default_rng(shape[0])
+    x = with_outliers(rng, shape, dt, 0.02)
+    x[0] = 0  # an all-zero row
+    q, s = empty(shape, L.DataType.I8), empty(shape[:-1], L.DataType.F32)
+    tx = dev(x, DTS[dt])
+    L.Ops.quantize_int8(q, s, tx)
+    eq, es = oracle.quantize_int8(x)
+    assert_exact(q.numpy(), eq, "codes")
+    assert_exact(s.numpy(), es, "scales")
+    out = empty(shape, DTS[dt])
+    L.Ops.dequantize_int8(out, q, s)
+    assert_exact(out.numpy(), oracle.dequantize_int8(eq, es, x.dtype), "dequant")
+
+
+def test_quantize_exact_ties_on_gpu():
+    # scale = 2^-4 exactly; quotients k + 0.5 must round half to even, bit-exact
+    s = np.float32(2.0 ** -4)
+    odd = np.arange(-253, 254, 2)
+    row = np.concatenate([[127 * s], odd.astype(np.float32) * s / 2, np.zeros(512 - 255, np.float32)])
+    x = np.tile(row.astype(np.float32), (4, 1))
+    x[2, 7] = np.nan
+    q, sc = empty(x.shape, L.DataType.I8), empty((4,), L.DataType.F32)
+    L.Ops.quantize_int8(q, sc, dev(x))
+    eq, es = oracle.quantize_int8(x)
+    assert_exact(q.numpy(), eq)
+    assert_exact(sc.numpy(), es)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_kv_append(dt):
+    rng = np.random.default_rng(21)
+    max_seq, nkvh, d = 32768, 2, 128
+    cq = dev(np.full((max_seq, nkvh, d), 7, np.int8))
+    cs = dev(np.full((max_seq, nkvh), -1.0, np.float32))
+    host_q = np.full((max_seq, nkvh, d), 7, np.int8)
+    host_s = np.full((max_seq, nkvh), -1.0, np.float32)
+    for pos, ntok in ((0, 2048), (2048, 1), (5000, 27768), (32767, 1)):
+        kv = with_outliers(rng, (ntok, nkvh, d), dt, 1.0)
+        L.Ops.kv_append_int8(cq, cs, dev(kv, DTS[dt]), pos)
+        assert oracle.kv_append_int8(host_q, host_s, kv, pos) == 0
+    assert_exact(cq.numpy(), host_q)
+    assert_exact(cs.numpy(), host_s)
+    # dequantized read of the whole cache
+    out = empty((max_seq, nkvh, d), DTS[dt])
+    L.Ops.dequantize_int8(out, cq, cs)
+    assert_exact(out.numpy(), oracle.dequantize_int8(host_q, host_s, np.uint16 if dt == "bf16" else np.float32))
+
+
+# ---- config-size properties ----------------------------------------------------------------
+
+def test_config2_shapes_properties():
+    """Llama-8B shapes (config 2) checked through size-independent properties."""
+    rng = np.random.default_rng(2)
+    BF = L.DataType.BF16
+    # rms_norm [16384, 4096]: every row of the output has rms ~= rms(w) and matches
+    # the oracle on a sample of rows
+    x = sample(rng, (16384, 4096), "bf16")
+    w = sample(rng, (4096,), "bf16", 0.1, 1.0)
+    y = empty(x.shape, BF)
+    L.Ops.rms_norm(y, dev(x, BF), dev(w, BF), 1e-5)
+    got = y.numpy()
+    rows = rng.choice(16384, 64, replace=False)
+    assert_close(got[rows], oracle.rms_norm(x[rows], w, 1e-5))
+    # rope q[16384, 32, 128], theta 5e5: norm of every pair preserved; position 0 identity
+    q = sample(rng, (16384, 32, 128), "bf16")
+    pos = np.arange(16384, dtype=np.int64)
+    yq = empty(q.shape, BF)
+    L.Ops.rope(yq, dev(q, BF), dev(pos), 5e5)
+    gq = yq.numpy()
+    assert np.array_equal(gq[0], q[0])
+    qa, qb = bf16_to_f32(q[..., :64]), bf16_to_f32(q[..., 64:])
+    ya, yb = bf16_to_f32(gq[..., :64]), bf16_to_f32(gq[..., 64:])
+    n0, n1 = qa ** 2 + qb ** 2, ya ** 2 + yb ** 2
+    assert np.allclose(n0, n1, rtol=2e-2, atol=1e-3)
+    assert_close(gq[-4:], oracle.rope(q[-4:], pos[-4:], 5e5))
+    no_device_error()

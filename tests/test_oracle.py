@@ -1,0 +1,291 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the parity checker.
+
+1. Golden vectors written by the compiled reference library (tests/golden/golden.npz):
+   the oracle must reproduce every reference output bit for bit.
+2. Where the reference library is built in this container (oracle/_ref), random shapes
+   are compared with it directly.
+3. The functions without a reference counterpart (INT8 quantize / dequantize / KV append,
+   fused add + rms_norm, row-wise argmax) are pinned by closed forms: exactly known
+   quotients and ties, invariants and compositions of already-pinned functions.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from llaisys_amd.hostfmt import bf16_to_f32, f32_to_bf16
+from numerics import assert_exact
+
+# ---- 1. reference golden vectors ----------------------------------------------------
+
+
+def test_golden_rms_norm(golden):
+    n = 0
+    for (op, dt, case), c in golden.items():
+        if op == "rms_norm":
+            assert_exact(oracle.rms_norm(c["x"], c["w"], float(c["eps"])), c["y"], f"{dt} {case}")
+            n += 1
+    assert n == 12
+
+
+def test_golden_add(golden):
+    for (op, dt, case), c in golden.items():
+        if op == "add":
+            assert_exact(oracle.add(c["a"], c["b"]), c["c"], f"{dt} {case}")
+
+
+def test_golden_rope(golden):
+    n = 0
+    for (op, dt, case), c in golden.items():
+        if op == "rope":
+            assert_exact(oracle.rope(c["x"], c["pos"], float(c["theta"])), c["y"], f"{dt} {case}")
+            n += 1
+    assert n == 15
+
+
+def test_golden_swiglu(golden):
+    for (op, dt, case), c in golden.items():
+        if op == "swiglu":
+            assert_exact(oracle.swiglu(c["gate"], c["up"]), c["y"], f"{dt} {case}")
+
+
+def test_golden_embedding(golden):
+    for (op, dt, case), c in golden.items():
+        if op == "embedding":
+            out, st = oracle.embedding(c["idx"], c["w"])
+            assert st == 0
+            assert_exact(out, c["out"], f"{dt} {case}")
+
+
+def test_golden_argmax(golden):
+    n = 0
+    for (op, dt, case), c in golden.items():
+        if op == "argmax":
+            i, v = oracle.argmax(c["vals"])
+            assert i == c["idx"][0], f"{dt} {case}"
+            assert_exact(np.array([v]), c["val"], f"{dt} {case}")
+            n += 1
+    assert n == 16
+
+
+# ---- 2. direct comparison with the compiled reference --------------------------------
+
+@pytest.fixture(scope="module")
+def ref():
+    lib = oracle.reference_library()
+    if lib is None:
+        pytest.skip("reference library not built here (needs /root/reference)")
+    from llaisys_amd.libllaisys import bind
+    return bind(lib)
+
+
+def _ref_call(lib, fn, outs, ins, *scalars):
+    from llaisys_amd.libllaisys import DataType, DeviceType
+    from llaisys_amd.tensor import Tensor
+    keep = [Tensor.from_numpy(a, dt, device=DeviceType.CPU, lib=lib) for a, dt in ins]
+    res = [Tensor(shape, dt, DeviceType.CPU, lib=lib) for shape, dt in outs]
+    getattr(lib, fn)(*[t.lib_tensor() for t in res], *[t.lib_tensor() for t in keep], *scalars)
+    return [t.numpy() for t in res]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_shapes_match_reference(ref, seed):
+    from llaisys_amd.libllaisys import DataType
+    rng = np.random.default_rng(seed)
+    for dt, conv in ((DataType.F32, lambda a: a), (DataType.BF16, f32_to_bf16),
+                     (DataType.F16, lambda a: a.astype(np.float16))):
+        rows, cols = int(rng.integers(1, 9)), int(rng.integers(1, 700))
+        x = conv(rng.standard_normal((rows, cols)).astype(np.float32) * 3)
+        w = conv(rng.standard_normal(cols).astype(np.float32))
+        eps = float(rng.choice([1e-5, 1e-6]))
+        (y,) = _ref_call(ref, "llaisysRmsNorm", [((rows, cols), dt)], [(x, dt), (w, dt)], ctypes.c_float(eps))
+        assert_exact(oracle.rms_norm(x, w, eps), y, "rms_norm")
+        (y,) = _ref_call(ref, "llaisysSwiGLU", [((rows, cols), dt)], [(x, dt), (x[::-1].copy(), dt)])
+        assert_exact(oracle.swiglu(x, x[::-1].copy()), y, "swiglu")
+        seq, nh, half = int(rng.integers(1, 6)), int(rng.integers(1, 4)), int(rng.integers(1, 70))
+        q = conv(rng.standard_normal((seq, nh, 2 * half)).astype(np.float32))
+        pos = rng.integers(0, 40000, size=seq).astype(np.int64)
+        theta = float(rng.choice([1e4, 5e5, 1e6]))
+        (y,) = _ref_call(ref, "llaisysROPE", [(q.shape, dt)], [(q, dt), (pos, DataType.I64)], ctypes.c_float(theta))
+        assert_exact(oracle.rope(q, pos, theta), y, "rope")
+
+
+# ---- 3. closed forms -------------------------------------------------------------------
+
+def test_bf16_rounding_rule():
+    L = oracle.lib()
+    cases = {
+        0x3F808000: 0x3F80,  # exact tie, even LSB stays
+        0x3F818000: 0x3F82,  # exact tie, odd LSB rounds up
+        0x3F807FFF: 0x3F80,  # below half
+        0x3F808001: 0x3F81,  # above half
+        0x7F7FFFFF: 0x7F80,  # overflow rounds to +inf
+        0xFF7FFFFF: 0xFF80,
+        0x00000000: 0x0000,
+        0x80000000: 0x8000,
+    }
+    for bits, want in cases.items():
+        f = np.array([bits], dtype=np.uint32).view(np.float32)[0]
+        assert L.orc_f32_to_bf16(float(f)) == want, hex(bits)
+    # exhaustive widening: bf16 -> f32 is a 16-bit shift
+    b = np.arange(1 << 16, dtype=np.uint32)
+    f = bf16_to_f32(b.astype(np.uint16))
+    assert np.array_equal(f.view(np.uint32), b << 16)
+    # the host helper used to build inputs follows the same rule
+    x = np.random.default_rng(1).standard_normal(10000).astype(np.float32)
+    assert all(L.orc_f32_to_bf16(float(v)) == h for v, h in zip(x[:500], f32_to_bf16(x[:500])))
+
+
+def test_f16_truncation_rule():
+    L = oracle.lib()
+    # f32 -> f16 truncates the mantissa (reference types.cpp:54-55)
+    one_plus = np.float32(1.0) + np.float32(2.0 ** -11) * np.float32(1.9)  # above the f16 half-ulp
+    assert L.orc_f32_to_f16(float(one_plus)) == 0x3C00
+    assert L.orc_f32_to_f16(70000.0) == 0x7C00
+    assert L.orc_f32_to_f16(float("nan")) == 0x7E00
+    # f16 -> f32 is exact for every pattern (compare with numpy's exact widening)
+    h = np.arange(1 << 16, dtype=np.uint16)
+    fin = np.isfinite(h.view(np.float16))
+    got = np.array([L.orc_f16_to_f32(int(v)) for v in h[fin][::97]], dtype=np.float32)
+    assert np.array_equal(got, h[fin][::97].view(np.float16).astype(np.float32))
+
+
+def test_rms_norm_closed_form():
+    # a constant row c gives y_j = w_j * c / sqrt(c^2 + eps) (up to f32 rounding)
+    for c, eps in ((0.5, 1e-6), (3.0, 1e-5), (1e-3, 1e-6)):
+        x = np.full((2, 1536), c, dtype=np.float32)
+        w = np.linspace(0.5, 1.5, 1536).astype(np.float32)
+        y = oracle.rms_norm(x, w, eps)
+        exact = w.astype(np.float64) * c / np.sqrt(c * c + eps)
+        assert np.allclose(y, exact, rtol=2e-6), (c, eps)
+    # eps matters: for tiny rows the result is x*w/sqrt(eps)
+    x = np.full((1, 64), 1e-8, dtype=np.float32)
+    y = oracle.rms_norm(x, np.ones(64, np.float32), 1e-2)
+    assert np.allclose(y, 1e-8 / np.sqrt(1e-2), rtol=1e-5)
+
+
+def test_rope_closed_forms():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((4, 3, 16)).astype(np.float32)
+    # position 0 is the identity
+    assert_exact(oracle.rope(x, np.zeros(4, np.int64), 1e4), x)
+    # head_dim 2: a single pair rotated by angle p (freq = theta^0 = 1)
+    x2 = rng.standard_normal((5, 1, 2)).astype(np.float32)
+    p = np.arange(5, dtype=np.int64) * 7
+    y = oracle.rope(x2, p, 1e4)
+    a, b = x2[:, 0, 0].astype(np.float64), x2[:, 0, 1].astype(np.float64)
+    assert np.allclose(y[:, 0, 0], a * np.cos(p) - b * np.sin(p), rtol=1e-6, atol=1e-7)
+    assert np.allclose(y[:, 0, 1], b * np.cos(p) + a * np.sin(p), rtol=1e-6, atol=1e-7)
+    # rotation preserves the norm of every (j, j + d/2) pair, and pairs are (j, j+d/2)
+    pos = np.arange(4, dtype=np.int64) * 1000
+    y = oracle.rope(x, pos, 1e4)
+    nx = x[..., :8] ** 2 + x[..., 8:] ** 2
+    ny = y[..., :8] ** 2 + y[..., 8:] ** 2
+    assert np.allclose(nx, ny, rtol=1e-5)
+    # frequency j uses theta^(-2j/d): pair j=4 of d=16 at p=1 turns by 1e4^-0.5 = 0.01
+    e = np.zeros((1, 1, 16), np.float32)
+    e[0, 0, 4] = 1.0
+    y = oracle.rope(e, np.ones(1, np.int64), 1e4)
+    assert np.isclose(y[0, 0, 4], np.cos(0.01), rtol=1e-7) and np.isclose(y[0, 0, 12], np.sin(0.01), rtol=1e-6)
+
+
+def test_swiglu_closed_forms():
+    g = np.array([0.0, 40.0, -40.0, 1.0, -2.5], np.float32)
+    u = np.array([3.0, 2.0, 5.0, 1.0, 4.0], np.float32)
+    y = oracle.swiglu(g, u)
+    assert y[0] == 0.0 and y[1] == 80.0 and abs(y[2]) < 1e-15
+    silu = g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))
+    assert np.allclose(y[3:], (u * silu)[3:], rtol=1e-6)
+
+
+def _pow2_row(k, odd):
+    """Row with amax = 127 * 2^-k, so scale = 2^-k exactly and x / scale = odd / 2."""
+    s = np.float32(2.0 ** -k)
+    row = np.concatenate([[127 * s], odd.astype(np.float32) * s / 2]).astype(np.float32)
+    return row, s
+
+
+def test_int8_quantize_exact_quotients():
+    odd = np.arange(-253, 254, 2)  # quotients -126.5 .. 126.5: every half-integer tie
+    for k in (0, 4, 9):
+        row, s = _pow2_row(k, odd)
+        q, scale = oracle.quantize_int8(row[None, :])
+        assert scale[0] == s
+        assert q[0, 0] == 127
+        half = odd / 2
+        want = np.where(np.abs(half - np.floor(half)) == 0.5,
+                        2 * np.round(half / 2), np.round(half))  # ties to even
+        assert np.array_equal(q[0, 1:], want.astype(np.int8))
+    # exact multiples give their multiplier; -amax gives -127
+    s = np.float32(0.25)
+    row = np.array([-127, -3, 0, 5, 126], np.float32) * s
+    q, scale = oracle.quantize_int8(row[None, :])
+    assert scale[0] == s and q.tolist() == [[-127, -3, 0, 5, 126]]
+
+
+def test_int8_special_rows():
+    rows = np.zeros((3, 8), np.float32)
+    rows[1, 3] = np.nan
+    rows[1, 5] = -2.0
+    rows[2, :] = [1, -1, np.nan, 0.5, 0, 0, 0, 0]
+    q, s = oracle.quantize_int8(rows)
+    assert s[0] == 0 and not q[0].any()                     # all-zero row
+    assert s[1] == np.float32(2.0) / np.float32(127.0)      # NaN ignored by amax
+    assert q[1, 3] == 0 and q[1, 5] == -127                 # NaN code is 0
+    assert q[2].tolist() == [127, -127, 0, 64, 0, 0, 0, 0]  # 63.5 rounds to even 64
+
+
+def test_int8_roundtrip_bound_and_dequant():
+    rng = np.random.default_rng(7)
+    for dt in ("f32", "bf16"):
+        x = rng.standard_normal((64, 128)).astype(np.float32)
+        x[rng.random(x.shape) < 0.01] *= 20
+        xin = x if dt == "f32" else f32_to_bf16(x)
+        xf = xin if dt == "f32" else bf16_to_f32(xin)
+        q, s = oracle.quantize_int8(xin)
+        assert np.array_equal(s, np.abs(xf).max(axis=1) / np.float32(127))
+        assert (np.abs(q).max(axis=1) == 127).all()
+        deq = oracle.dequantize_int8(q, s, np.float32)
+        assert np.array_equal(deq, q.astype(np.float32) * s[:, None])
+        assert (np.abs(deq - xf) <= s[:, None] / 2 * (1 + 1e-6)).all()
+        deq16 = oracle.dequantize_int8(q, s, np.uint16)
+        assert np.array_equal(deq16, f32_to_bf16(deq))
+
+
+def test_kv_append_writes_only_its_rows():
+    rng = np.random.default_rng(9)
+    kv = f32_to_bf16(rng.standard_normal((5, 2, 128)).astype(np.float32))
+    cq = np.full((16, 2, 128), 99, np.int8)
+    cs = np.full((16, 2), -1, np.float32)
+    assert oracle.kv_append_int8(cq, cs, kv, 7) == 0
+    q, s = oracle.quantize_int8(kv)
+    assert np.array_equal(cq[7:12], q) and np.array_equal(cs[7:12], s)
+    assert (cq[:7] == 99).all() and (cq[12:] == 99).all() and (cs[:7] == -1).all()
+    assert oracle.kv_append_int8(cq, cs, kv, 12) == -1  # 12 + 5 > 16
+
+
+def test_fused_add_rms_norm_is_the_composition(golden):
+    # residual stream = the reference add (golden), output = rms_norm of that sum
+    for (op, dt, case), c in golden.items():
+        if op == "add" and case == "16x1536":
+            w = np.ones(1536, dtype=c["a"].dtype) if dt != "bf16" else f32_to_bf16(np.ones(1536, np.float32))
+            y, h = oracle.add_rms_norm(c["a"], c["b"], w, 1e-6)
+            assert_exact(h, c["c"], dt)
+            assert_exact(y, oracle.rms_norm(c["c"], w, 1e-6), dt)
+
+
+def test_argmax_rows_is_rowwise_argmax(golden):
+    vals = golden[("argmax", "bf16", "rand")]["vals"].reshape(4, 1024)
+    idx, val = oracle.argmax_rows(vals)
+    for r in range(4):
+        i, v = oracle.argmax(vals[r])
+        assert idx[r] == i and val[r] == v
+
+
+def test_embedding_out_of_range():
+    w = np.arange(12, dtype=np.float32).reshape(4, 3)
+    out, st = oracle.embedding(np.array([1, 4], np.int64), w)
+    assert st == -1 and np.array_equal(out[0], w[1])
+    _, st = oracle.embedding(np.array([-1], np.int32), w)
+    assert st == -1
