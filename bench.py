@@ -100,6 +100,14 @@ class Workload:
             b["val"] = L.Tensor((1,), BF, **dev)
             self.sets.append(b)
 
+    def extra_ops(self):
+        """Reference-ABI forms measured beside the step (q and k RoPE as two calls)."""
+        O = self.L.Ops
+        return [
+            ("rope_q", 2 * T * NH * D * 2 + T * 8, lambda b: O.rope(b["q_out"], b["q"], self.pos, 1e4)),
+            ("rope_k", 2 * T * NKV * D * 2 + T * 8, lambda b: O.rope(b["k_out"], b["k"], self.pos, 1e4)),
+        ]
+
     def ops(self):
         """(name, algorithmic bytes per launch, launch(set)) of one step."""
         O = self.L.Ops
@@ -109,8 +117,8 @@ class Workload:
             ("rms_norm", 2 * tok + H * 2, lambda b: O.rms_norm(b["y_rms"], b["x"], self.w, 1e-6)),
             ("add_rms_norm", 4 * tok + H * 2,
              lambda b: O.add_rms_norm(b["y"], b["h"], b["x"], b["r"], self.w, 1e-6)),
-            ("rope_q", 2 * T * NH * D * 2 + T * 8, lambda b: O.rope(b["q_out"], b["q"], self.pos, 1e4)),
-            ("rope_k", 2 * T * NKV * D * 2 + T * 8, lambda b: O.rope(b["k_out"], b["k"], self.pos, 1e4)),
+            ("rope_qk", 2 * T * (NH + NKV) * D * 2 + T * 8,
+             lambda b: O.rope_qk(b["q_out"], b["q"], b["k_out"], b["k"], self.pos, 1e4)),
             ("swiglu", 3 * T * I * 2, lambda b: O.swiglu(b["act"], b["gate"], b["up"])),
             ("argmax", V * 2 + 8 + 2, lambda b: O.argmax(b["idx"], b["val"], b["logits"])),
         ]
@@ -163,7 +171,7 @@ class Chain:
     def bytes(self):
         t, e = self.TOK, 2
         norm = 4 * t * H * e + H * e
-        rope = 2 * t * (NH + NKV) * D * e + 2 * t * 8
+        rope = 2 * t * (NH + NKV) * D * e + t * 8
         kv = 2 * (t * NKV * D * e + t * NKV * D + t * NKV * 4)
         swi = 3 * t * I * e
         layer = 2 * norm + rope + kv + swi
@@ -173,8 +181,7 @@ class Chain:
         O = self.L.Ops
         for b in self.layers:
             O.add_rms_norm(b["n1"], self.resid, b["attn"], self.resid, b["w1"], 1e-6)
-            O.rope(b["q_out"], b["q"], self.pos, 1e6)
-            O.rope(b["k_out"], b["k"], self.pos, 1e6)
+            O.rope_qk(b["q_out"], b["q"], b["k_out"], b["k"], self.pos, 1e6)
             O.kv_append_int8(b["kc"], b["kcs"], b["k_out"], 0)
             O.kv_append_int8(b["vc"], b["vcs"], b["v"], 0)
             O.add_rms_norm(b["n2"], self.resid, b["mlp"], self.resid, b["w2"], 1e-6)
@@ -268,13 +275,14 @@ def _cpu_model():
 
 
 def traffic_of(kernel):
-    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, read from
-    profiles/traffic.txt ('<kernel> <fetch_bytes> <write_bytes>'), or None."""
+    """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by
+    the counters' reading on a device copy of known size), read from profiles/traffic.txt
+    ('<op> <fetch_bytes> <write_bytes>'), or None."""
     path = ROOT / "profiles" / "traffic.txt"
     if not path.is_file():
         return None
     for line in path.read_text().splitlines():
-        parts = line.split()
+        parts = line.split("#", 1)[0].split()
         if len(parts) == 3 and parts[0] == kernel:
             return int(float(parts[1]) + float(parts[2]))
     return None
@@ -288,6 +296,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-chain", action="store_true")
+    ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain (profiling)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="3 dispatches of a 256 MiB device copy (counter calibration), then 3 of "
+                         "each config-1 op, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the per-layer "
@@ -299,8 +311,29 @@ def main():
     hip = HipEvents()
     stream = L.context_stream(L.DeviceType.AMD, 0)
     api = L.RuntimeAPI(L.DeviceType.AMD)
+    if args.chain_only:
+        ch = Chain(L)
+        graph = L.Graph.capture()
+        ch.run()
+        graph.end()
+        for _ in range(args.steps):
+            graph.launch()
+        api.device_synchronize()
+        return
     print("bench: building config-1 buffers", file=sys.stderr, flush=True)
     wl = Workload(L)
+    if args.traffic_probe:
+        n = 256 << 20
+        src, dst = L.Tensor((n,), L.DataType.U8, device=L.DeviceType.AMD), L.Tensor((n,), L.DataType.U8, device=L.DeviceType.AMD)
+        for _ in range(3):
+            api.memcpy_sync(dst.data_ptr(), src.data_ptr(), n, L.MemcpyKind.D2D)
+        for name, _, fn in wl.ops():
+            for i in range(3):
+                fn(wl.sets[i % NSETS])
+            api.device_synchronize()
+        print(json.dumps({"probe": "copy 256 MiB x3, then each config-1 op x3",
+                          "ops": {name: b for name, b, _ in wl.ops()}}))
+        return
     ops = wl.ops()
     step_bytes = sum(b for _, b, _ in ops)
 
@@ -325,7 +358,7 @@ def main():
 
     per_op = {}
     reps = max(args.steps, 20)
-    for name, nbytes, fn in ops:
+    for name, nbytes, fn in ops + wl.extra_ops():
         for i in range(3):
             fn(wl.sets[i % NSETS])
         hip.record(e0, stream)
@@ -345,18 +378,32 @@ def main():
         ch = Chain(L)
         for _ in range(2):
             ch.run()
-        hip.record(e0, stream)
         nrep = 10
+        hip.record(e0, stream)
         for _ in range(nrep):
             ch.run()
         hip.record(e1, stream)
+        ms_eager = hip.elapsed_ms(e0, e1) / nrep
+        graph = L.Graph.capture()
+        ch.run()
+        graph.end()
+        for _ in range(2):
+            graph.launch()
+        hip.record(e0, stream)
+        for _ in range(nrep):
+            graph.launch()
+        hip.record(e1, stream)
         ms = hip.elapsed_ms(e0, e1) / nrep
+        del graph
         cb = ch.bytes()
         chain = {"workload": "config 4: 28 Qwen2-1.5B layers, 2048-token prefill, bf16, INT8 KV "
-                             "append, final rms_norm + argmax over [2048, 151936]",
+                             "append, final rms_norm + argmax over [2048, 151936]; replayed "
+                             "as one HIP graph",
                  "ms": round(ms, 4), "tokens_per_s": round(Chain.TOK / (ms * 1e-3)),
                  "bytes": cb, "GB_s": round(cb / (ms * 1e-3) / 1e9, 1),
-                 "frac_peak": round(cb / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)}
+                 "frac_peak": round(cb / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                 "ms_eager_launches": round(ms_eager, 4),
+                 "tokens_per_s_eager": round(Chain.TOK / (ms_eager * 1e-3))}
         assert L.take_device_error() == 0
         del ch
 
@@ -373,7 +420,7 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded normal activations, N(0,0.02) table), resident in HBM",
         "config": {"workload": "config 1: Qwen2-1.5B layer ops, bf16, 8192 tokens (embedding, "
-                               "rms_norm, add+rms_norm, rope q+k, swiglu, argmax [1,151936])",
+                               "rms_norm, add+rms_norm, rope q+k (fused launch), swiglu, argmax [1,151936])",
                    "tokens": T, "hidden": H, "intermediate": I, "vocab": V,
                    "buffer_sets": NSETS, "parallelism": "single GPU"},
         "frac_peak": round(value / PEAK_GBS, 4),

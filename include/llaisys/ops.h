@@ -54,6 +54,12 @@ __C {
     __export void llaisysAddRmsNorm(llaisysTensor_t out, llaisysTensor_t residual_out,
                                     llaisysTensor_t in, llaisysTensor_t residual,
                                     llaisysTensor_t weight, float eps);
+    /* RoPE of q [seq, nh_q, head_dim] and k [seq, nh_k, head_dim] with the same pos_ids in
+     * one launch: the reference decoder's two llaisysROPE calls on q and k
+     * (src/models/qwen2/attention.hpp:54-55), each with the semantics of llaisysROPE; the
+     * (cos, sin) table of a token is computed once for both. */
+    __export void llaisysROPEQK(llaisysTensor_t q_out, llaisysTensor_t q_in, llaisysTensor_t k_out,
+                                llaisysTensor_t k_in, llaisysTensor_t pos_ids, float theta);
     /* Row-wise argmax: the reference argmax (argmax_cpu.cpp:9-28) applied to each row of
      * vals [rows, cols]; max_idx [rows] I32/I64, max_val [rows] with the dtype of vals. */
     __export void llaisysArgmaxRows(llaisysTensor_t max_idx, llaisysTensor_t max_val,

@@ -61,6 +61,19 @@ __C {
      * device_synchronize / stream_synchronize of the AMD table raise the same error
      * (print + throw, like every other LLAISYS error) when it is set. */
     __export int llaisysTakeDeviceError(llaisysDeviceType_t, int);
+
+    /* Additive: HIP-graph capture of op sequences, for launch-bound callers (a decoder
+     * layer chain issues ~7 small kernels per layer; replaying a captured graph removes the
+     * per-op host launch cost).  Between Begin and End every op called on this thread for
+     * (device_type, device_id) is recorded instead of run; End returns an executable graph
+     * that Launch replays on the same stream, with the tensors captured at record time.
+     * Only the AMD device supports capture.  Ops whose scratch would have to grow during
+     * capture (a flat argmax over more than 2^29 elements) fail at capture time. */
+    typedef struct LlaisysGraph *llaisysGraph_t;
+    __export void llaisysGraphBeginCapture(llaisysDeviceType_t, int);
+    __export llaisysGraph_t llaisysGraphEndCapture(llaisysDeviceType_t, int);
+    __export void llaisysGraphLaunch(llaisysGraph_t graph);
+    __export void llaisysGraphDestroy(llaisysGraph_t graph);
 }
 
 #endif /* LLAISYS_RUNTIME_H */

@@ -7,7 +7,7 @@ not part of this package.
 from .libllaisys import DataType, DeviceType, MemcpyKind
 from .libllaisys import llaisysStream_t as Stream
 from .ops import Ops
-from .runtime import RuntimeAPI, context_stream, take_device_error
+from .runtime import Graph, RuntimeAPI, context_stream, take_device_error
 from .tensor import Tensor
 
 __all__ = [
@@ -18,6 +18,7 @@ __all__ = [
     "Stream",
     "Tensor",
     "Ops",
+    "Graph",
     "context_stream",
     "take_device_error",
 ]

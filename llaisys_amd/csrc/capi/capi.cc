@@ -48,6 +48,24 @@ __C {
         return llaisys::device::amd::takeError(ctx.runtime().stream());
     }
 
+    void llaisysGraphBeginCapture(llaisysDeviceType_t type, int id) {
+        if (type != LLAISYS_DEVICE_AMD) EXCEPTION_UNSUPPORTED_DEVICE;
+        auto &ctx = llaisys::core::context();
+        ctx.setDevice(type, id);
+        llaisys::device::amd::beginCapture(id, ctx.runtime().stream());
+    }
+
+    llaisysGraph_t llaisysGraphEndCapture(llaisysDeviceType_t type, int id) {
+        if (type != LLAISYS_DEVICE_AMD) EXCEPTION_UNSUPPORTED_DEVICE;
+        auto &ctx = llaisys::core::context();
+        ctx.setDevice(type, id);
+        return llaisys::device::amd::endCapture(ctx.runtime().stream());
+    }
+
+    void llaisysGraphLaunch(llaisysGraph_t g) { llaisys::device::amd::launchGraph(g); }
+
+    void llaisysGraphDestroy(llaisysGraph_t g) { llaisys::device::amd::destroyGraph(g); }
+
     // ---- tensors (reference src/llaisys/tensor.cc:7-118) -------------------------------
     llaisysTensor_t tensorCreate(size_t * shape, size_t ndim, llaisysDataType_t dtype,
                                  llaisysDeviceType_t device_type, int device_id) {
@@ -124,6 +142,11 @@ __C {
                            llaisysTensor_t residual, llaisysTensor_t weight, float eps) {
         llaisys::ops::addRmsNorm(out->tensor, residual_out->tensor, in->tensor, residual->tensor,
                                  weight->tensor, eps);
+    }
+    void llaisysROPEQK(llaisysTensor_t q_out, llaisysTensor_t q_in, llaisysTensor_t k_out,
+                       llaisysTensor_t k_in, llaisysTensor_t pos_ids, float theta) {
+        llaisys::ops::ropeQK(q_out->tensor, q_in->tensor, k_out->tensor, k_in->tensor,
+                             pos_ids->tensor, theta);
     }
     void llaisysArgmaxRows(llaisysTensor_t max_idx, llaisysTensor_t max_val, llaisysTensor_t vals) {
         llaisys::ops::argmaxRows(max_idx->tensor, max_val->tensor, vals->tensor);

@@ -172,3 +172,49 @@ void *workspace(int dev, size_t bytes) {
 }
 
 } // namespace llaisys::device::amd
+
+struct LlaisysGraph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    hipStream_t stream;
+};
+
+namespace llaisys::device::amd {
+
+void beginCapture(int dev, llaisysStream_t s) {
+    // Everything an op may allocate lazily must exist before capture starts.
+    (void)errorWord(dev);
+    (void)workspace(dev, 1);
+    check(hipStreamBeginCapture(static_cast<hipStream_t>(s), hipStreamCaptureModeRelaxed),
+          "hipStreamBeginCapture");
+}
+
+llaisysGraph_t endCapture(llaisysStream_t s) {
+    auto *g = new LlaisysGraph{nullptr, nullptr, static_cast<hipStream_t>(s)};
+    const int st = hipStreamEndCapture(g->stream, &g->graph);
+    if (st != hipSuccess) {
+        delete g;
+        check(st, "hipStreamEndCapture");
+    }
+    const int st2 = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (st2 != hipSuccess) {
+        (void)hipGraphDestroy(g->graph);
+        delete g;
+        check(st2, "hipGraphInstantiate");
+    }
+    return g;
+}
+
+void launchGraph(llaisysGraph_t g) {
+    CHECK_ARGUMENT(g != nullptr, "null graph");
+    check(hipGraphLaunch(g->exec, g->stream), "hipGraphLaunch");
+}
+
+void destroyGraph(llaisysGraph_t g) {
+    if (!g) return;
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+}
+
+} // namespace llaisys::device::amd

@@ -29,6 +29,12 @@ void raiseIfError(llaisysStream_t stream);
 // least `bytes` of device memory, zeroed when first allocated.
 void *workspace(int device_id, size_t bytes);
 
+// HIP-graph capture of the work enqueued on `stream` (the current device's context stream).
+void beginCapture(int device_id, llaisysStream_t stream);
+llaisysGraph_t endCapture(llaisysStream_t stream);
+void launchGraph(llaisysGraph_t g);
+void destroyGraph(llaisysGraph_t g);
+
 // Checks a HIP status code; prints "[ERROR] HIP <what>: <message>" and throws.
 void check(int status, const char *what);
 } // namespace amd

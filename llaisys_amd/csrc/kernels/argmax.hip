@@ -70,10 +70,10 @@ __device__ Best scan(const void *vals, size_t begin, size_t end, bool vec) {
         const size_t nv = (end - begin) / N;
         tail = begin + nv * N;
         for (size_t k = threadIdx.x; k < nv; k += kBlock * kU) {
-            uint4 r[kU];
+            v4u r[kU];
 #pragma unroll
             for (int u = 0; u < kU; ++u)
-                if (k + u * kBlock < nv) r[u] = load16<T>(vals, begin + (k + u * kBlock) * N);
+                if (k + u * kBlock < nv) r[u] = load16Stream<T>(vals, begin + (k + u * kBlock) * N);
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
                 if (k + u * kBlock < nv) {

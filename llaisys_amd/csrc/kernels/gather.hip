@@ -8,6 +8,8 @@
 //
 // Design: pure copy, HBM-bound.  One wavefront per id; lanes copy the row in the widest
 // unit the row size and addresses allow (16 B normally), UNROLL units in flight per lane.
+// Output rows are written with non-temporal stores; table rows use ordinary loads (a
+// repeated id hits the cache, and non-temporal gathers measured ~20 % slower).
 #include "common.hpp"
 #include "launch.hpp"
 #include "rowplan.hpp"
@@ -40,9 +42,9 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
         for (int k = 0; k < kUnroll; ++k) r[k] = src[u + k * kWave];
 #pragma unroll
-        for (int k = 0; k < kUnroll; ++k) dst[u + k * kWave] = r[k];
+        for (int k = 0; k < kUnroll; ++k) __builtin_nontemporal_store(r[k], dst + u + k * kWave);
     }
-    for (; u < units_per_row; u += kWave) dst[u] = src[u];
+    for (; u < units_per_row; u += kWave) __builtin_nontemporal_store(src[u], dst + u);
 }
 
 template <typename Unit>
@@ -63,8 +65,9 @@ void embedding(void *out, const void *index, bool i64, size_t n, const void *w, 
     if (n == 0) return;
     const uintptr_t mis = reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(w) |
                           uintptr_t(row_bytes);
-    if ((mis & 15u) == 0) return launchUnit<uint4>(out, index, i64, n, w, vocab, row_bytes, err, s);
-    if ((mis & 7u) == 0) return launchUnit<uint2>(out, index, i64, n, w, vocab, row_bytes, err, s);
+    typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+    if ((mis & 15u) == 0) return launchUnit<v4u>(out, index, i64, n, w, vocab, row_bytes, err, s);
+    if ((mis & 7u) == 0) return launchUnit<v2u>(out, index, i64, n, w, vocab, row_bytes, err, s);
     if ((mis & 3u) == 0) return launchUnit<uint32_t>(out, index, i64, n, w, vocab, row_bytes, err, s);
     if ((mis & 1u) == 0) return launchUnit<uint16_t>(out, index, i64, n, w, vocab, row_bytes, err, s);
     launchUnit<uint8_t>(out, index, i64, n, w, vocab, row_bytes, err, s);

@@ -24,6 +24,11 @@ void rmsNorm(void *out, void *residual_out, const void *in, const void *residual
 void rope(void *out, const void *in, const int64_t *pos, size_t seq, size_t n_heads,
           size_t head_dim, float theta, llaisysDataType_t dt, hipStream_t stream);
 
+// RoPE of q [seq, nh_q, head_dim] and k [seq, nh_k, head_dim] (same positions) in one launch.
+void ropeQK(void *q_out, const void *q_in, size_t nh_q, void *k_out, const void *k_in,
+            size_t nh_k, const int64_t *pos, size_t seq, size_t head_dim, float theta,
+            llaisysDataType_t dt, hipStream_t stream);
+
 // out = up * gate / (1 + exp(-gate)) over n elements.
 void swiglu(void *out, const void *gate, const void *up, size_t n, llaisysDataType_t dt,
             hipStream_t stream);

@@ -9,6 +9,8 @@
 // Design: HBM-bound; a row lives in registers between the reduction and the scaling so
 // x (and r) are read once and y (and h) written once.  16-byte loads per lane, butterfly
 // reduction within the wavefront, LDS only to join the waves of one row when G > 64.
+// Activations stream (non-temporal loads and stores); the weight row uses cached loads,
+// since every row of the launch reads it.
 // No MFMA: there is no contraction here.
 #include "common.hpp"
 #include "launch.hpp"
@@ -18,7 +20,7 @@ namespace llaisys::kernels {
 
 namespace {
 
-template <typename T, int G, int V, bool kFused>
+template <typename T, int G, int VMAX, bool kFused>
 __global__ void __launch_bounds__(blockFor<G>())
     rmsNormRows(void *__restrict__ out, void *residual_out, const void *__restrict__ in,
                 const void *residual, const void *__restrict__ weight, size_t rows, int cols,
@@ -34,39 +36,52 @@ __global__ void __launch_bounds__(blockFor<G>())
     const int nvec = cols / N;
     const size_t base = row * size_t(cols);
 
-    float x[V][N];
+    // the lane's share of the row, kept as raw 16-byte vectors
+    v4u raw[VMAX];
+#pragma unroll
+    for (int v = 0; v < VMAX; ++v) {
+        const int vi = lane + v * G;
+        if (live && vi < nvec) raw[v] = load16Stream<T>(in, base + size_t(vi) * N);
+    }
+    if constexpr (kFused) {
+#pragma unroll
+        for (int v = 0; v < VMAX; ++v) {
+            const int vi = lane + v * G;
+            if (live && vi < nvec) {
+                float x[N], r[N];
+                F::unpack(raw[v], x);
+                F::unpack(load16Stream<T>(residual, base + size_t(vi) * N), r);
+#pragma unroll
+                for (int e = 0; e < N; ++e) x[e] = x[e] + r[e];
+                raw[v] = F::pack(x); // h = T(x + r), the value the reference's add stores
+                store16Stream<T>(residual_out, base + size_t(vi) * N, raw[v]);
+            }
+        }
+    }
     float ss = 0.0f;
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
+    for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
         if (live && vi < nvec) {
-            F::unpack(load16<T>(in, base + size_t(vi) * N), x[v]);
-            if constexpr (kFused) {
-                float r[N];
-                F::unpack(load16<T>(residual, base + size_t(vi) * N), r);
+            float x[N];
+            F::unpack(raw[v], x);
 #pragma unroll
-                for (int e = 0; e < N; ++e) x[v][e] = F::round(x[v][e] + r[e]);
-                store16<T>(residual_out, base + size_t(vi) * N, F::pack(x[v]));
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < N; ++e) x[v][e] = 0.0f;
+            for (int e = 0; e < N; ++e) ss += x[e] * x[e];
         }
-#pragma unroll
-        for (int e = 0; e < N; ++e) ss += x[v][e] * x[v][e];
     }
     ss = groupReduce<G, SumOp>(ss, red);
     const float rms = sqrtf(ss / float(cols) + eps);
     const float inv = 1.0f / rms;
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
+    for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
         if (live && vi < nvec) {
-            float w[N], y[N];
+            float x[N], w[N], y[N];
+            F::unpack(raw[v], x);
             F::unpack(load16<T>(weight, size_t(vi) * N), w);
 #pragma unroll
-            for (int e = 0; e < N; ++e) y[e] = x[v][e] * w[e] * inv;
-            store16<T>(out, base + size_t(vi) * N, F::pack(y));
+            for (int e = 0; e < N; ++e) y[e] = x[e] * w[e] * inv;
+            store16Stream<T>(out, base + size_t(vi) * N, F::pack(y));
         }
     }
 }
@@ -110,7 +125,7 @@ void launch(void *out, void *res_out, const void *in, const void *res, const voi
     RowPlan plan = vec ? planRow(cols / N) : RowPlan{};
     bool done = false;
     withPlan(plan, [&](auto g, auto v) {
-        constexpr int G = decltype(g)::value, V = decltype(v)::value;
+        constexpr int G = decltype(g)::value, V = decltype(v)::value; // V: vectors per lane
         constexpr int kBlock = blockFor<G>();
         const unsigned grid = blocksFor(rows, kBlock / G);
         if (fused)

@@ -31,16 +31,17 @@ __device__ __forceinline__ uint32_t codeOf(float x, float amax, float scale) {
 template <int N>
 __device__ __forceinline__ void storeCodes(int8_t *q, size_t i, const uint32_t *c) {
     if constexpr (N == 8) {
-        uint2 r;
-        r.x = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-        r.y = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
-        *reinterpret_cast<uint2 *>(q + i) = r;
+        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+        const v2u r{c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24),
+                    c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)};
+        __builtin_nontemporal_store(r, reinterpret_cast<v2u *>(q + i));
     } else {
-        *reinterpret_cast<uint32_t *>(q + i) = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+        __builtin_nontemporal_store(c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24),
+                                    reinterpret_cast<uint32_t *>(q + i));
     }
 }
 
-template <typename T, int G, int V>
+template <typename T, int G, int VMAX>
 __global__ void __launch_bounds__(blockFor<G>())
     quantRows(int8_t *__restrict__ q, float *__restrict__ scale, const void *__restrict__ in,
               size_t rows, int cols) {
@@ -55,27 +56,35 @@ __global__ void __launch_bounds__(blockFor<G>())
     const int nvec = cols / N;
     const size_t base = row * size_t(cols);
 
-    float x[V][N];
+    v4u raw[VMAX];
     float amax = 0.0f;
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
+    for (int v = 0; v < VMAX; ++v) {
+        const int vi = lane + v * G;
+        if (live && vi < nvec) raw[v] = load16Stream<T>(in, base + size_t(vi) * N);
+    }
+#pragma unroll
+    for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
         if (live && vi < nvec) {
-            F::unpack(load16<T>(in, base + size_t(vi) * N), x[v]);
+            float x[N];
+            F::unpack(raw[v], x);
 #pragma unroll
-            for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(x[v][e]));
+            for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(x[e]));
         }
     }
     amax = groupReduce<G, MaxOp>(amax, red);
     const float sc = amax / 127.0f;
     if (live && lane == 0) scale[row] = sc;
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
+    for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
         if (live && vi < nvec) {
+            float x[N];
             uint32_t c[N];
+            F::unpack(raw[v], x);
 #pragma unroll
-            for (int e = 0; e < N; ++e) c[e] = codeOf(x[v][e], amax, sc);
+            for (int e = 0; e < N; ++e) c[e] = codeOf(x[e], amax, sc);
             storeCodes<N>(q, base + size_t(vi) * N, c);
         }
     }

@@ -1,17 +1,19 @@
-// Rotate-half RoPE for gfx950.
+// Rotate-half RoPE for gfx950, for one tensor or for q and k in one launch.
 //
 // Semantics: reference src/ops/rope/cpu/rope_cpu.cpp:28-44.  For token i, head h and
 // j < d/2: freq_j = 1 / pow((double)theta, (double)(2.0f * j / d)), angle = (double)p_i *
 // freq_j, and the pair (x_j, x_{j+d/2}) is rotated in double precision; the result is
 // rounded double -> float -> element type.  freq_j is computed on the host with the same
 // libm pow the reference calls, so the angles are bit-identical; cos/sin come from the
-// device's double-precision libm.
+// device's double-precision libm (within an ulp of glibc's, which the final float rounding
+// absorbs).
 //
-// Design: HBM-bound (about 13 VALU ops per element in f64, well under the 8 TB/s
-// budget).  A block owns a run of tokens; the (cos, sin) pairs of those tokens are
-// computed once into LDS and reused by every head, so the f64 trig costs d/2 sincos per
-// token instead of n_heads * d/2.  Each lane rotates 8 (bf16) or 4 (f32) pairs with two
-// 16-byte loads and two 16-byte stores.
+// Design: HBM-bound.  A 256-thread block owns a run of tokens.  Each lane first issues the
+// 16-byte loads of its (token, head, 8-pair) items (both halves of the head), then the
+// block computes the (cos, sin) pairs of its tokens into LDS -- d/2 sincos per token,
+// shared by every q and k head -- so the f64 trig overlaps the load latency; finally each
+// lane rotates and stores its items.  Loads and stores are non-temporal (read once,
+// written once).  q and k of the same tokens go through one launch.
 #include "common.hpp"
 #include "launch.hpp"
 #include "rowplan.hpp"
@@ -23,11 +25,22 @@ namespace llaisys::kernels {
 
 namespace {
 
-constexpr int kMaxHalf = 128;     // head_dim <= 256 uses the host frequency table
-constexpr int kLdsPairs = 1024;   // (cos, sin) doubles staged per block: 16 KB
+constexpr int kMaxHalf = 128;   // head_dim <= 256 uses the host frequency table
+constexpr int kLdsPairs = 1024; // (cos, sin) doubles staged per block: 16 KB
+constexpr int kMaxItems = 4;    // 16-byte items per lane held in registers
 
 struct FreqTable {
     double f[kMaxHalf];
+};
+
+// Two tensors sharing positions and head_dim; tensor 1 may be absent (n_heads1 == 0).
+struct RopePair {
+    void *out0;
+    const void *in0;
+    void *out1;
+    const void *in1;
+    int n_heads0;
+    int n_heads1;
 };
 
 __device__ __forceinline__ double freqOf(const FreqTable &ft, int j, int d, float theta) {
@@ -35,20 +48,53 @@ __device__ __forceinline__ double freqOf(const FreqTable &ft, int j, int d, floa
     return 1.0 / pow(double(theta), double(2.0f * float(j) / float(d)));
 }
 
-template <typename T>
+// VPH: 16-byte vectors per half head, a power of two (8 for bf16 and head_dim 128), so
+// the item -> (head, vector) split is a shift; the item -> token split uses `tok_magic`
+// (floor(2^32 / items_per_token) + 1, exact for item * items_per_token < 2^32).
+template <typename T, int IPT, int VPH>
 __global__ void __launch_bounds__(256)
-    ropeVec(void *__restrict__ out, const void *__restrict__ in, const int64_t *__restrict__ pos,
-            size_t seq, int n_heads, int d, int tok_per_block, FreqTable ft) {
+    ropeVec(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int tok_per_block,
+            uint32_t tok_magic, FreqTable ft) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
+    constexpr int kHalf = VPH * N;
+    constexpr int kD = 2 * kHalf;
+    constexpr int kShift = __builtin_ctz(VPH);
     __shared__ double2 cs[kLdsPairs];
 
-    const int half = d / 2;
+    const int per_tok = (tp.n_heads0 + tp.n_heads1) * VPH;
     const size_t t0 = size_t(blockIdx.x) * tok_per_block;
     const int ntok = int(min(size_t(tok_per_block), seq - t0));
+    const int items = ntok * per_tok;
 
-    for (int i = threadIdx.x; i < ntok * half; i += 256) {
-        const int tt = i / half, j = i - tt * half;
+    // 1. issue this lane's loads
+    v4u ra[IPT], rb[IPT];
+    size_t off[IPT];
+    int tok[IPT], jvec[IPT];
+    bool second[IPT];
+#pragma unroll
+    for (int k = 0; k < IPT; ++k) {
+        const int it = threadIdx.x + k * 256;
+        if (it < items) {
+            const int tt = int(__umulhi(uint32_t(it), tok_magic));
+            const int rem = it - tt * per_tok;
+            int h = rem >> kShift;
+            const int jv = rem & (VPH - 1);
+            second[k] = h >= tp.n_heads0;
+            const int nh = second[k] ? tp.n_heads1 : tp.n_heads0;
+            if (second[k]) h -= tp.n_heads0;
+            tok[k] = tt;
+            jvec[k] = jv;
+            off[k] = ((t0 + tt) * size_t(nh) + h) * size_t(kD) + size_t(jv) * N;
+            const void *src = second[k] ? tp.in1 : tp.in0;
+            ra[k] = load16Stream<T>(src, off[k]);
+            rb[k] = load16Stream<T>(src, off[k] + kHalf);
+        }
+    }
+
+    // 2. (cos, sin) of this block's tokens
+    for (int i = threadIdx.x; i < ntok * kHalf; i += 256) {
+        const int tt = i / kHalf, j = i % kHalf;
         const double ang = double(pos[t0 + tt]) * ft.f[j];
         double sn, c;
         sincos(ang, &sn, &c);
@@ -56,31 +102,30 @@ __global__ void __launch_bounds__(256)
     }
     __syncthreads();
 
-    const int vph = half / N; // vectors per half head
-    const int items = ntok * n_heads * vph;
-    for (int it = threadIdx.x; it < items; it += 256) {
-        const int jv = it % vph;
-        const int rest = it / vph;
-        const int h = rest % n_heads;
-        const int tt = rest / n_heads;
-        const size_t base = ((t0 + tt) * size_t(n_heads) + h) * size_t(d) + size_t(jv) * N;
-        float a[N], b[N], ya[N], yb[N];
-        F::unpack(load16<T>(in, base), a);
-        F::unpack(load16<T>(in, base + half), b);
-        const double2 *row = cs + tt * half + jv * N;
+    // 3. rotate and store
 #pragma unroll
-        for (int e = 0; e < N; ++e) {
-            const double c = row[e].x, sn = row[e].y;
-            const double A = a[e], B = b[e];
-            ya[e] = float(A * c - B * sn);
-            yb[e] = float(B * c + A * sn);
+    for (int k = 0; k < IPT; ++k) {
+        const int it = threadIdx.x + k * 256;
+        if (it < items) {
+            float a[N], b[N], ya[N], yb[N];
+            F::unpack(ra[k], a);
+            F::unpack(rb[k], b);
+            const double2 *row = cs + tok[k] * kHalf + jvec[k] * N;
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                const double c = row[e].x, sn = row[e].y;
+                const double A = a[e], B = b[e];
+                ya[e] = float(A * c - B * sn);
+                yb[e] = float(B * c + A * sn);
+            }
+            void *dst = second[k] ? tp.out1 : tp.out0;
+            store16Stream<T>(dst, off[k], F::pack(ya));
+            store16Stream<T>(dst, off[k] + kHalf, F::pack(yb));
         }
-        store16<T>(out, base, F::pack(ya));
-        store16<T>(out, base + half, F::pack(yb));
     }
 }
 
-// Any head_dim / alignment: one thread per (token, head, j) pair.
+// Any head_dim / alignment: one thread per (token, head, j) pair of one tensor.
 template <typename T>
 __global__ void __launch_bounds__(256)
     ropeScalar(void *out, const void *in, const int64_t *pos, size_t seq, size_t n_heads,
@@ -103,43 +148,108 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-template <typename T>
-void launch(void *out, const void *in, const int64_t *pos, size_t seq, size_t nh, size_t d,
-            float theta, hipStream_t s) {
-    if (seq == 0 || nh == 0 || d == 0) return;
-    constexpr int N = Fmt<T>::kVec;
-    const size_t half = d / 2;
+FreqTable hostFreqs(size_t d, float theta) {
     FreqTable ft{};
-    for (size_t j = 0; j < half && j < size_t(kMaxHalf); ++j) {
+    for (size_t j = 0; j < d / 2 && j < size_t(kMaxHalf); ++j) {
         // Same expression and libm call as rope_cpu.cpp:31.
         const float ex = 2.0f * float(j) / float(d);
         ft.f[j] = 1.0 / std::pow(double(theta), double(ex));
     }
-    const bool vec = half % N == 0 && half <= size_t(kMaxHalf) && aligned16(out) && aligned16(in);
-    if (vec) {
-        const size_t per_tok = nh * (half / N);
-        size_t tpb = std::max<size_t>(1, 1024 / per_tok);
-        tpb = std::min(tpb, size_t(kLdsPairs) / half);
-        tpb = std::max<size_t>(tpb, 1);
-        if (tpb * per_tok <= size_t(INT32_MAX) && nh <= size_t(INT32_MAX)) {
-            ropeVec<T><<<blocksFor(seq, tpb), 256, 0, s>>>(out, in, pos, seq, int(nh), int(d),
-                                                           int(tpb), ft);
-            return;
-        }
+    return ft;
+}
+
+template <typename T, int IPT>
+void launchIpt(int vph, const RopePair &tp, const int64_t *pos, size_t seq, size_t tpb,
+               uint32_t magic, const FreqTable &ft, hipStream_t s) {
+    const unsigned grid = blocksFor(seq, tpb);
+    switch (vph) {
+    case 2: ropeVec<T, IPT, 2><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
+    case 4: ropeVec<T, IPT, 4><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
+    case 8: ropeVec<T, IPT, 8><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
+    case 16: ropeVec<T, IPT, 16><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
+    case 32: ropeVec<T, IPT, 32><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
+    default: break;
     }
-    const size_t pairs = seq * nh * half;
+}
+
+// Items per block: 256 (one 16-byte item per lane) measured fastest on MI355X for the
+// Qwen2 shapes (rope q+k 8192 tokens: 14.3 us vs 14.5 at 1024, 16.8 at 128); blocks with
+// fewer items leave lanes idle, blocks with more run fewer, longer-latency waves.
+constexpr size_t kItemsPerBlock = 256;
+
+template <typename T>
+bool launchVec(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, const FreqTable &ft,
+               hipStream_t s) {
+    constexpr int N = Fmt<T>::kVec;
+    const size_t half = d / 2;
+    if (half % N != 0 || half > size_t(kMaxHalf)) return false;
+    const size_t vph = half / N;
+    if (vph & (vph - 1)) return false; // not a power of two
+    for (const void *p : {static_cast<const void *>(tp.out0), tp.in0,
+                          static_cast<const void *>(tp.out1), tp.in1})
+        if (p && !aligned16(p)) return false;
+    const size_t per_tok = size_t(tp.n_heads0 + tp.n_heads1) * vph;
+    if (per_tok == 0 || per_tok > size_t(256 * kMaxItems)) return false;
+    size_t tpb = std::max<size_t>(1, kItemsPerBlock / per_tok);
+    tpb = std::min(tpb, size_t(kLdsPairs) / half);
+    const int ipt = int((tpb * per_tok + 255) / 256);
+    const uint32_t magic = uint32_t((uint64_t(1) << 32) / per_tok + 1);
+    switch (ipt) {
+    case 1: launchIpt<T, 1>(int(vph), tp, pos, seq, tpb, magic, ft, s); break;
+    case 2: launchIpt<T, 2>(int(vph), tp, pos, seq, tpb, magic, ft, s); break;
+    case 3: launchIpt<T, 3>(int(vph), tp, pos, seq, tpb, magic, ft, s); break;
+    default: launchIpt<T, 4>(int(vph), tp, pos, seq, tpb, magic, ft, s); break;
+    }
+    return true;
+}
+
+template <typename T>
+void launchScalar(void *out, const void *in, const int64_t *pos, size_t seq, size_t nh,
+                  size_t d, float theta, const FreqTable &ft, hipStream_t s) {
+    const size_t pairs = seq * nh * (d / 2);
+    if (pairs == 0) return;
     const unsigned grid = unsigned(std::min<size_t>(blocksFor(pairs, 256), 65536));
     ropeScalar<T><<<grid, 256, 0, s>>>(out, in, pos, seq, nh, d, theta, ft);
+}
+
+template <typename T>
+void launch(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, float theta,
+            hipStream_t s) {
+    if (seq == 0 || d == 0) return;
+    const FreqTable ft = hostFreqs(d, theta);
+    if (launchVec<T>(tp, pos, seq, d, ft, s)) return;
+    launchScalar<T>(tp.out0, tp.in0, pos, seq, size_t(tp.n_heads0), d, theta, ft, s);
+    if (tp.n_heads1) launchScalar<T>(tp.out1, tp.in1, pos, seq, size_t(tp.n_heads1), d, theta, ft, s);
+}
+
+template <typename T>
+void launchAny(void *qo, const void *qi, size_t nhq, void *ko, const void *ki, size_t nhk,
+               const int64_t *pos, size_t seq, size_t d, float theta, hipStream_t s) {
+    if (nhq > size_t(INT32_MAX / 2) || nhk > size_t(INT32_MAX / 2)) {
+        const FreqTable ft = hostFreqs(d, theta);
+        launchScalar<T>(qo, qi, pos, seq, nhq, d, theta, ft, s);
+        if (nhk) launchScalar<T>(ko, ki, pos, seq, nhk, d, theta, ft, s);
+        return;
+    }
+    launch<T>(RopePair{qo, qi, ko, ki, int(nhq), int(nhk)}, pos, seq, d, theta, s);
 }
 
 } // namespace
 
 void rope(void *out, const void *in, const int64_t *pos, size_t seq, size_t n_heads,
           size_t head_dim, float theta, llaisysDataType_t dt, hipStream_t s) {
+    ropeQK(out, in, n_heads, nullptr, nullptr, 0, pos, seq, head_dim, theta, dt, s);
+}
+
+void ropeQK(void *q_out, const void *q_in, size_t nh_q, void *k_out, const void *k_in,
+            size_t nh_k, const int64_t *pos, size_t seq, size_t head_dim, float theta,
+            llaisysDataType_t dt, hipStream_t s) {
+    if (nh_q == 0 && nh_k == 0) return;
+    if (nh_q == 0) return ropeQK(k_out, k_in, nh_k, nullptr, nullptr, 0, pos, seq, head_dim, theta, dt, s);
     switch (dt) {
-    case LLAISYS_DTYPE_F32: return launch<F32>(out, in, pos, seq, n_heads, head_dim, theta, s);
-    case LLAISYS_DTYPE_BF16: return launch<BF16>(out, in, pos, seq, n_heads, head_dim, theta, s);
-    case LLAISYS_DTYPE_F16: return launch<F16>(out, in, pos, seq, n_heads, head_dim, theta, s);
+    case LLAISYS_DTYPE_F32: return launchAny<F32>(q_out, q_in, nh_q, k_out, k_in, nh_k, pos, seq, head_dim, theta, s);
+    case LLAISYS_DTYPE_BF16: return launchAny<BF16>(q_out, q_in, nh_q, k_out, k_in, nh_k, pos, seq, head_dim, theta, s);
+    case LLAISYS_DTYPE_F16: return launchAny<F16>(q_out, q_in, nh_q, k_out, k_in, nh_k, pos, seq, head_dim, theta, s);
     default: return;
     }
 }

@@ -1,9 +1,16 @@
 // Host-side choice of the lane group and registers per lane for row kernels.
 //
-// A row of `nvec` 16-byte vectors is owned by a group of G consecutive lanes, each lane
-// holding V vectors in registers (vector k of a lane is lane + k*G, so a group's loads
-// are contiguous).  The row is read from HBM once and written once.  G <= 64 reduces in
-// one wavefront with butterflies; G = 256 / 1024 combines wave partials through LDS.
+// A row of `nvec` 16-byte vectors is owned by a group of G consecutive lanes; each lane
+// holds up to VMAX of the row's vectors in registers (vector k of a lane is lane + k*G, so
+// every load instruction of a group covers G*16 contiguous bytes).  The row is read from
+// HBM once and written once.  G <= 64 reduces inside one wavefront with butterflies;
+// G = 256 / 1024 joins the wave partials through LDS.
+//
+// Measured on MI355X (interleaved medians, bf16 rows of 1536 / 4096 at 2-16K rows): up to
+// 4 vectors per lane with a wider group beats fewer, fatter lanes (rms_norm 8192x1536:
+// 8.9 us with 64 lanes x 3 vectors vs 10.0 us with 16 lanes x 12; 16384x4096: 44.8 us with
+// 256 lanes x 2 vs 46.3 us with 64 x 8), so the plan takes the smallest group that keeps
+// each lane at <= 4 vectors, and only rows beyond 4096 vectors use 8 per lane.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -16,21 +23,20 @@ namespace llaisys::kernels {
 
 struct RowPlan {
     int group = 0; // 0: no register-resident plan, use the scalar kernel
-    int vpl = 0;
+    int vmax = 0;
 };
 
+constexpr int kRowGroups[] = {4, 16, 32, 64, 256, 1024};
+constexpr int kRowVmax[] = {4, 8};
+
 inline RowPlan planRow(size_t nvec) {
-    static constexpr int kGroups[] = {16, 64, 256, 1024};
-    static constexpr int kMaxV[] = {2, 8, 8, 8};
-    for (int k = 0; k < 4; ++k) {
-        const size_t g = size_t(kGroups[k]);
-        if (nvec <= g * size_t(kMaxV[k])) {
-            int v = int((nvec + g - 1) / g);
-            if (v == 5) v = 6;
-            if (v == 7) v = 8;
-            return {kGroups[k], v < 1 ? 1 : v};
-        }
-    }
+    // Short rows (a 128-wide KV head) still get 16 lanes, so one load instruction of a
+    // group covers 256 contiguous bytes instead of 64.
+    const size_t min_g = nvec < 16 ? nvec : 16;
+    for (int v : kRowVmax)
+        for (int g : kRowGroups)
+            if (size_t(g) >= min_g && (nvec + size_t(g) - 1) / size_t(g) <= size_t(v))
+                return {g, v};
     return {};
 }
 
@@ -39,36 +45,26 @@ constexpr int blockFor() {
     return G < 256 ? 256 : G;
 }
 
+// Calls f(integral_constant<G>, integral_constant<VMAX>) for the plan.
 template <int G, typename F>
-void withV(int v, F &&f) {
+void withVmax(int v, F &&f) {
     using std::integral_constant;
     switch (v) {
-    case 1: f(integral_constant<int, G>{}, integral_constant<int, 1>{}); break;
-    case 2: f(integral_constant<int, G>{}, integral_constant<int, 2>{}); break;
-    case 3:
-        if constexpr (G > 16) f(integral_constant<int, G>{}, integral_constant<int, 3>{});
-        break;
-    case 4:
-        if constexpr (G > 16) f(integral_constant<int, G>{}, integral_constant<int, 4>{});
-        break;
-    case 6:
-        if constexpr (G > 16) f(integral_constant<int, G>{}, integral_constant<int, 6>{});
-        break;
-    case 8:
-        if constexpr (G > 16) f(integral_constant<int, G>{}, integral_constant<int, 8>{});
-        break;
+    case 4: f(integral_constant<int, G>{}, integral_constant<int, 4>{}); break;
+    case 8: f(integral_constant<int, G>{}, integral_constant<int, 8>{}); break;
     default: break;
     }
 }
 
-// Calls f(integral_constant<G>, integral_constant<V>) for the plan's (G, V).
 template <typename F>
 void withPlan(const RowPlan &p, F &&f) {
     switch (p.group) {
-    case 16: withV<16>(p.vpl, f); break;
-    case 64: withV<64>(p.vpl, f); break;
-    case 256: withV<256>(p.vpl, f); break;
-    case 1024: withV<1024>(p.vpl, f); break;
+    case 4: withVmax<4>(p.vmax, f); break;
+    case 16: withVmax<16>(p.vmax, f); break;
+    case 32: withVmax<32>(p.vmax, f); break;
+    case 64: withVmax<64>(p.vmax, f); break;
+    case 256: withVmax<256>(p.vmax, f); break;
+    case 1024: withVmax<1024>(p.vmax, f); break;
     default: break;
     }
 }

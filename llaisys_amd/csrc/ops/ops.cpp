@@ -171,6 +171,33 @@ void rope(tensor_t out, tensor_t in, tensor_t pos_ids, float theta) {
     launched("rope");
 }
 
+// RoPE of q and k of the same tokens in one launch (the reference decoder calls rope on q
+// and then on k, src/models/qwen2/attention.hpp:54-55; each gets the checks of
+// src/ops/rope/op.cpp:8-51).
+void ropeQK(tensor_t q_out, tensor_t q_in, tensor_t k_out, tensor_t k_in, tensor_t pos_ids,
+            float theta) {
+    CHECK_SAME_DEVICE(q_out, q_in, k_out, k_in, pos_ids);
+    ASSERT(q_in->isContiguous() && q_out->isContiguous() && k_in->isContiguous() &&
+               k_out->isContiguous() && pos_ids->isContiguous(),
+           "RoPE paremeter must be contiguous");
+    ASSERT(q_in->ndim() == 3 && k_in->ndim() == 3, "input shape must be 3");
+    CHECK_SAME_SHAPE(q_in->shape(), q_out->shape());
+    CHECK_SAME_SHAPE(k_in->shape(), k_out->shape());
+    const size_t seq = q_in->shape()[0], d = q_in->shape()[2];
+    ASSERT(k_in->shape()[0] == seq && k_in->shape()[2] == d,
+           "RoPEQK: q and k must share seq_len and head_dim");
+    ASSERT(pos_ids->numel() == seq, "pos_ids length must match Seq_Len");
+    ASSERT(d % 2 == 0, "Head dimension must be even for RoPE");
+    CHECK_SAME_DTYPE(q_in->dtype(), q_out->dtype(), k_in->dtype(), k_out->dtype());
+    ASSERT(pos_ids->dtype() == LLAISYS_DTYPE_I64, "token id data type must be INT64");
+    requireFloat(q_in->dtype());
+    auto s = streamFor(q_in);
+    kernels::ropeQK(q_out->data(), q_in->data(), q_in->shape()[1], k_out->data(), k_in->data(),
+                    k_in->shape()[1], reinterpret_cast<const int64_t *>(pos_ids->data()), seq, d,
+                    theta, q_in->dtype(), s);
+    launched("ropeQK");
+}
+
 // reference src/ops/swiglu/op.cpp:7-38
 void swiglu(tensor_t out, tensor_t gate, tensor_t up) {
     CHECK_SAME_DEVICE(out, gate, up);

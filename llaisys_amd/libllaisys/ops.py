@@ -24,6 +24,7 @@ REFERENCE_OPS = {
 
 ADDED_OPS = {
     "llaisysAddRmsNorm": [T, T, T, T, T, c_float],
+    "llaisysROPEQK": [T, T, T, T, T, c_float],
     "llaisysArgmaxRows": [T, T, T],
     "llaisysQuantizeInt8": [T, T, T],
     "llaisysDequantizeInt8": [T, T, T],

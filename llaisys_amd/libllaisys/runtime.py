@@ -48,6 +48,15 @@ def load_runtime(lib):
     if hasattr(lib, "llaisysGetContextStream"):
         lib.llaisysGetContextStream.argtypes = [llaisysDeviceType_t, c_int]
         lib.llaisysGetContextStream.restype = llaisysStream_t
+    if hasattr(lib, "llaisysGraphBeginCapture"):
+        lib.llaisysGraphBeginCapture.argtypes = [llaisysDeviceType_t, c_int]
+        lib.llaisysGraphBeginCapture.restype = None
+        lib.llaisysGraphEndCapture.argtypes = [llaisysDeviceType_t, c_int]
+        lib.llaisysGraphEndCapture.restype = c_void_p
+        lib.llaisysGraphLaunch.argtypes = [c_void_p]
+        lib.llaisysGraphLaunch.restype = None
+        lib.llaisysGraphDestroy.argtypes = [c_void_p]
+        lib.llaisysGraphDestroy.restype = None
     if hasattr(lib, "llaisysTakeDeviceError"):
         lib.llaisysTakeDeviceError.argtypes = [llaisysDeviceType_t, c_int]
         lib.llaisysTakeDeviceError.restype = c_int

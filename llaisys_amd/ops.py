@@ -60,6 +60,12 @@ class Ops:
                                       weight.lib_tensor(), c_float(eps))
 
     @staticmethod
+    def rope_qk(q_out: Tensor, q_in: Tensor, k_out: Tensor, k_in: Tensor, pos_ids: Tensor,
+                theta: float):
+        LIB_LLAISYS.llaisysROPEQK(q_out.lib_tensor(), q_in.lib_tensor(), k_out.lib_tensor(),
+                                  k_in.lib_tensor(), pos_ids.lib_tensor(), c_float(theta))
+
+    @staticmethod
     def argmax_rows(max_idx: Tensor, max_val: Tensor, vals: Tensor):
         LIB_LLAISYS.llaisysArgmaxRows(max_idx.lib_tensor(), max_val.lib_tensor(),
                                       vals.lib_tensor())

@@ -60,3 +60,34 @@ def take_device_error(device_type=libllaisys.DeviceType.AMD, device_id: int = 0,
     """Waits for the context stream and returns / clears the sticky device error code."""
     lib = lib if lib is not None else LIB_LLAISYS
     return int(lib.llaisysTakeDeviceError(int(device_type), int(device_id)))
+
+
+class Graph:
+    """HIP graph of the ops issued between capture() and end() on (device_type, device_id).
+
+        g = Graph.capture()          # ops below are recorded, not run
+        Ops.swiglu(out, gate, up)
+        g.end()
+        g.launch()                   # replays on the context stream
+    """
+
+    def __init__(self, device_type, device_id, lib):
+        self._lib, self._dt, self._id, self._g = lib, int(device_type), int(device_id), None
+
+    @classmethod
+    def capture(cls, device_type=libllaisys.DeviceType.AMD, device_id: int = 0, lib=None):
+        g = cls(device_type, device_id, lib if lib is not None else LIB_LLAISYS)
+        g._lib.llaisysGraphBeginCapture(g._dt, g._id)
+        return g
+
+    def end(self) -> "Graph":
+        self._g = self._lib.llaisysGraphEndCapture(self._dt, self._id)
+        return self
+
+    def launch(self) -> None:
+        self._lib.llaisysGraphLaunch(self._g)
+
+    def __del__(self):
+        if getattr(self, "_g", None):
+            self._lib.llaisysGraphDestroy(self._g)
+            self._g = None

@@ -109,7 +109,17 @@ def test_rms_norm(dt, shape, eps):
     x, w = sample(rng, shape, dt), sample(rng, shape[-1:], dt, 0.1, 1.0)
     y = empty(shape, DTS[dt])
     L.Ops.rms_norm(y, dev(x, DTS[dt]), dev(w, DTS[dt]), eps)
-    assert_close(y.numpy(), oracle.rms_norm(x, w, eps), f"rms_norm {dt} {shape}")
+    got, exp = y.numpy(), oracle.rms_norm(x, w, eps)
+    if dt == "f32" and shape[-1] > 16384:
+        # The reference sums 1e5 squares left to right in f32; that sum alone drifts by up
+        # to ~1e-5 relative, while the kernel's tree sum stays near the exact value.  Both
+        # are checked: 1e-5 against the f64-accumulated value, 3e-5 against the oracle.
+        xf = x.astype(np.float64)
+        exact = (xf * w) / np.sqrt((xf * xf).mean(axis=-1, keepdims=True) + eps)
+        assert np.abs(got - exact).max() <= 1e-5 * np.abs(exact).max()
+        assert (np.abs(got - exp) <= 3e-5 * np.abs(exp)).all()
+        return
+    assert_close(got, exp, f"rms_norm {dt} {shape}")
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
@@ -397,4 +407,75 @@ def test_config2_shapes_properties():
     n0, n1 = qa ** 2 + qb ** 2, ya ** 2 + yb ** 2
     assert np.allclose(n0, n1, rtol=2e-2, atol=1e-3)
     assert_close(gq[-4:], oracle.rope(q[-4:], pos[-4:], 5e5))
+    no_device_error()
+
+
+# ---- fused q/k RoPE ------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("seq,nhq,nhk,d,p0,theta", [
+    (8192, 12, 2, 128, 0, 1e4),       # config 1
+    (2048, 12, 2, 128, 0, 1e6),       # config 4 (Qwen2 theta)
+    (300, 32, 8, 128, 16000, 5e5),    # config 2 heads
+    (5, 3, 1, 6, 2, 1e4),             # odd half-dim: scalar kernels
+    (17, 64, 64, 128, 7, 1e4),        # more items per token than the register plan holds
+])
+def test_rope_qk_equals_two_ropes(dt, seq, nhq, nhk, d, p0, theta):
+    rng = np.random.default_rng(seed_of(seq, nhq, dt))
+    q, k = sample(rng, (seq, nhq, d), dt), sample(rng, (seq, nhk, d), dt)
+    pos = np.arange(p0, p0 + seq, dtype=np.int64)
+    qo, ko = empty(q.shape, DTS[dt]), empty(k.shape, DTS[dt])
+    L.Ops.rope_qk(qo, dev(q, DTS[dt]), ko, dev(k, DTS[dt]), dev(pos), theta)
+    assert_close(qo.numpy(), oracle.rope(q, pos, theta), "q")
+    assert_close(ko.numpy(), oracle.rope(k, pos, theta), "k")
+
+
+# ---- HIP graph capture ---------------------------------------------------------------------
+
+def test_graph_replays_match_eager():
+    """A captured layer (fused norm, RoPE q/k, INT8 KV append, swiglu, argmax) replayed
+    three times, with eager work and synchronisation between replays; every replay must
+    reproduce the eager results (the outputs are cleared before each replay)."""
+    rng = np.random.default_rng(31)
+    BF, I8, F32, I64 = L.DataType.BF16, L.DataType.I8, L.DataType.F32, L.DataType.I64
+    t = 256
+    x, r = sample(rng, (t, 1536), "bf16"), sample(rng, (t, 1536), "bf16")
+    w = sample(rng, (1536,), "bf16", 0.1, 1.0)
+    q, k = sample(rng, (t, 12, 128), "bf16"), sample(rng, (t, 2, 128), "bf16")
+    g, u = sample(rng, (t, 8960), "bf16"), sample(rng, (t, 8960), "bf16")
+    logits = sample(rng, (4, 151936), "bf16")
+    pos = np.arange(t, dtype=np.int64)
+    tx, tr, tw, tq, tk, tg, tu, tl, tp = (dev(a, BF if a.dtype == np.uint16 else None)
+                                          for a in (x, r, w, q, k, g, u, logits, pos))
+    outs = {"y": empty((t, 1536), BF), "h": empty((t, 1536), BF), "qo": empty(q.shape, BF),
+            "ko": empty(k.shape, BF), "kc": empty((t, 2, 128), I8), "ks": empty((t, 2), F32),
+            "act": empty((t, 8960), BF), "ri": empty((4,), I64), "rv": empty((4,), BF),
+            "fi": empty((1,), I64), "fv": empty((1,), BF)}
+
+    def layer():
+        o = outs
+        L.Ops.add_rms_norm(o["y"], o["h"], tx, tr, tw, 1e-6)
+        L.Ops.rope_qk(o["qo"], tq, o["ko"], tk, tp, 1e6)
+        L.Ops.kv_append_int8(o["kc"], o["ks"], o["ko"], 0)
+        L.Ops.swiglu(o["act"], tg, tu)
+        L.Ops.argmax_rows(o["ri"], o["rv"], tl)
+        L.Ops.argmax(o["fi"], o["fv"], tl)
+
+    layer()
+    eager = {name: tt.numpy() for name, tt in outs.items()}
+    graph = L.Graph.capture()
+    layer()
+    graph.end()
+    api = L.RuntimeAPI(L.DeviceType.AMD)
+    for replay in range(3):
+        for tt in outs.values():  # clear every output with an eager copy
+            z = np.zeros(tt.shape(), dtype=tt.numpy().dtype)
+            api.memcpy_sync(tt.data_ptr(), z.ctypes.data, z.nbytes, L.MemcpyKind.H2D)
+        scratch = empty((t, 8960), BF)
+        L.Ops.swiglu(scratch, tu, tg)  # unrelated eager work between replays
+        api.device_synchronize()
+        graph.launch()
+        api.device_synchronize()
+        for name, tt in outs.items():
+            assert_exact(tt.numpy(), eager[name], f"replay {replay}: {name}")
     no_device_error()
