@@ -48,29 +48,45 @@ __device__ __forceinline__ double freqOf(const FreqTable &ft, int j, int d, floa
     return 1.0 / pow(double(theta), double(2.0f * float(j) / float(d)));
 }
 
-// VPH: 16-byte vectors per half head, a power of two (8 for bf16 and head_dim 128), so
-// the item -> (head, vector) split is a shift; the item -> token split uses `tok_magic`
-// (floor(2^32 / items_per_token) + 1, exact for item * items_per_token < 2^32).
+// Partner exchange: the vector VPH lanes away.  For VPH = 8 (bf16 / f16 with head_dim 128)
+// the partner is in the same 16-lane DPP row, rotated by 8 (= lane ^ 8): a DPP move,
+// no LDS traffic.  Other widths use a cross-lane shuffle.
+template <int VPH>
+__device__ __forceinline__ uint32_t partnerOf(uint32_t v) {
+    if constexpr (VPH == 8)
+        return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
+    else
+        return uint32_t(__shfl_xor(int(v), VPH, kWave));
+}
+
+// Lane layout: item = one 16-byte vector of a head row, items of a row on consecutive
+// lanes, so every load / store instruction of a wavefront covers one contiguous 1 KB
+// (an earlier layout that gave each lane the vector pair (j, j + d/2) split every
+// instruction into 8 half-rows 256 B apart and ran ~20 % slower).  The rotation partner of
+// a vector sits VPH lanes away and is fetched with a cross-lane exchange.  VPH (16-byte
+// vectors per half head) is a power of two <= 32, so a row never straddles a wavefront
+// and item -> (row, vector) is a shift; item -> token uses `tok_magic`
+// (floor(2^32 / items_per_token) + 1, exact while item * items_per_token < 2^32).
 template <typename T, int IPT, int VPH>
 __global__ void __launch_bounds__(256)
     ropeVec(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int tok_per_block,
             uint32_t tok_magic, FreqTable ft) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
+    constexpr int kRowVec = 2 * VPH; // vectors per head row
     constexpr int kHalf = VPH * N;
-    constexpr int kD = 2 * kHalf;
-    constexpr int kShift = __builtin_ctz(VPH);
+    constexpr int kShift = __builtin_ctz(kRowVec);
     __shared__ double2 cs[kLdsPairs];
 
-    const int per_tok = (tp.n_heads0 + tp.n_heads1) * VPH;
+    const int per_tok = (tp.n_heads0 + tp.n_heads1) * kRowVec;
     const size_t t0 = size_t(blockIdx.x) * tok_per_block;
     const int ntok = int(min(size_t(tok_per_block), seq - t0));
     const int items = ntok * per_tok;
 
-    // 1. issue this lane's loads
-    v4u ra[IPT], rb[IPT];
+    // 1. issue this lane's loads (one contiguous 16-byte vector per item)
+    v4u raw[IPT];
     size_t off[IPT];
-    int tok[IPT], jvec[IPT];
+    int tok[IPT];
     bool second[IPT];
 #pragma unroll
     for (int k = 0; k < IPT; ++k) {
@@ -79,16 +95,15 @@ __global__ void __launch_bounds__(256)
             const int tt = int(__umulhi(uint32_t(it), tok_magic));
             const int rem = it - tt * per_tok;
             int h = rem >> kShift;
-            const int jv = rem & (VPH - 1);
+            const int v = rem & (kRowVec - 1);
             second[k] = h >= tp.n_heads0;
             const int nh = second[k] ? tp.n_heads1 : tp.n_heads0;
             if (second[k]) h -= tp.n_heads0;
             tok[k] = tt;
-            jvec[k] = jv;
-            off[k] = ((t0 + tt) * size_t(nh) + h) * size_t(kD) + size_t(jv) * N;
-            const void *src = second[k] ? tp.in1 : tp.in0;
-            ra[k] = load16Stream<T>(src, off[k]);
-            rb[k] = load16Stream<T>(src, off[k] + kHalf);
+            off[k] = ((t0 + tt) * size_t(nh) + h) * size_t(2 * kHalf) + size_t(v) * N;
+            raw[k] = load16Stream<T>(second[k] ? tp.in1 : tp.in0, off[k]);
+        } else {
+            raw[k] = v4u{0, 0, 0, 0};
         }
     }
 
@@ -102,25 +117,32 @@ __global__ void __launch_bounds__(256)
     }
     __syncthreads();
 
-    // 3. rotate and store
+    // 3. exchange with the partner vector, rotate, store.  First half of a row:
+    //    y = x*c - partner*s; second half: y = x*c + partner*s -- the reference's
+    //    a*c - b*s and b*c + a*s with the same operation order (rope_cpu.cpp:40-41).
+    const int v_lane = threadIdx.x & (kRowVec - 1);
+    const bool upper = v_lane >= VPH;
+    const int jv = v_lane & (VPH - 1);
 #pragma unroll
     for (int k = 0; k < IPT; ++k) {
+        v4u other;
+        other.x = partnerOf<VPH>(raw[k].x);
+        other.y = partnerOf<VPH>(raw[k].y);
+        other.z = partnerOf<VPH>(raw[k].z);
+        other.w = partnerOf<VPH>(raw[k].w);
         const int it = threadIdx.x + k * 256;
         if (it < items) {
-            float a[N], b[N], ya[N], yb[N];
-            F::unpack(ra[k], a);
-            F::unpack(rb[k], b);
-            const double2 *row = cs + tok[k] * kHalf + jvec[k] * N;
+            float x[N], p[N], y[N];
+            F::unpack(raw[k], x);
+            F::unpack(other, p);
+            const double2 *row = cs + tok[k] * kHalf + jv * N;
 #pragma unroll
             for (int e = 0; e < N; ++e) {
                 const double c = row[e].x, sn = row[e].y;
-                const double A = a[e], B = b[e];
-                ya[e] = float(A * c - B * sn);
-                yb[e] = float(B * c + A * sn);
+                const double own = x[e], partner = upper ? double(p[e]) : -double(p[e]);
+                y[e] = float(own * c + partner * sn);
             }
-            void *dst = second[k] ? tp.out1 : tp.out0;
-            store16Stream<T>(dst, off[k], F::pack(ya));
-            store16Stream<T>(dst, off[k] + kHalf, F::pack(yb));
+            store16Stream<T>(second[k] ? tp.out1 : tp.out0, off[k], F::pack(y));
         }
     }
 }
@@ -172,9 +194,11 @@ void launchIpt(int vph, const RopePair &tp, const int64_t *pos, size_t seq, size
     }
 }
 
-// Items per block: 256 (one 16-byte item per lane) measured fastest on MI355X for the
-// Qwen2 shapes (rope q+k 8192 tokens: 14.3 us vs 14.5 at 1024, 16.8 at 128); blocks with
-// fewer items leave lanes idle, blocks with more run fewer, longer-latency waves.
+// Items per block: about 256 (one 16-byte item per lane).  Measured on MI355X for the
+// Qwen2 shapes, 224-896 items per block are within 2 %, 128 is 15 % slower.  A persistent
+// variant (blocks looping over token groups with the next group's loads in flight) was
+// slower still: with one token per group the 64 f64 sincos ran on one wavefront while the
+// other three waited at the per-group barrier.
 constexpr size_t kItemsPerBlock = 256;
 
 template <typename T>
@@ -188,9 +212,19 @@ bool launchVec(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, con
     for (const void *p : {static_cast<const void *>(tp.out0), tp.in0,
                           static_cast<const void *>(tp.out1), tp.in1})
         if (p && !aligned16(p)) return false;
-    const size_t per_tok = size_t(tp.n_heads0 + tp.n_heads1) * vph;
+    if (vph > 32) return false; // a head row must fit in one wavefront
+    const size_t per_tok = size_t(tp.n_heads0 + tp.n_heads1) * 2 * vph;
     if (per_tok == 0 || per_tok > size_t(256 * kMaxItems)) return false;
+    // Tokens per block: the fewest that keep >= 90 % of the lanes busy (q only: 4 tokens of
+    // 192 items = 3 full items per lane), else one block's worth of ~256 items.
     size_t tpb = std::max<size_t>(1, kItemsPerBlock / per_tok);
+    for (size_t t = 1; t * per_tok <= size_t(256 * kMaxItems); ++t) {
+        const size_t slots = (t * per_tok + 255) / 256 * 256;
+        if (t * per_tok * 10 >= slots * 9) {
+            tpb = t;
+            break;
+        }
+    }
     tpb = std::min(tpb, size_t(kLdsPairs) / half);
     const int ipt = int((tpb * per_tok + 255) / 256);
     const uint32_t magic = uint32_t((uint64_t(1) << 32) / per_tok + 1);
