@@ -36,12 +36,19 @@ __global__ void __launch_bounds__(blockFor<G>())
     const int nvec = cols / N;
     const size_t base = row * size_t(cols);
 
-    // the lane's share of the row, kept as raw 16-byte vectors
+    // The lane's share of the row, kept as raw 16-byte vectors.  All loads (x and, fused,
+    // the residual) are issued before any store: residual_out may alias residual, so the
+    // compiler could not hoist a residual load above an earlier residual store itself, and
+    // the loads would turn into a chain of dependent round trips.
     v4u raw[VMAX];
+    v4u res[kFused ? VMAX : 1];
 #pragma unroll
     for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
-        if (live && vi < nvec) raw[v] = load16Stream<T>(in, base + size_t(vi) * N);
+        if (live && vi < nvec) {
+            raw[v] = load16Stream<T>(in, base + size_t(vi) * N);
+            if constexpr (kFused) res[v] = load16Stream<T>(residual, base + size_t(vi) * N);
+        }
     }
     if constexpr (kFused) {
 #pragma unroll
@@ -50,7 +57,7 @@ __global__ void __launch_bounds__(blockFor<G>())
             if (live && vi < nvec) {
                 float x[N], r[N];
                 F::unpack(raw[v], x);
-                F::unpack(load16Stream<T>(residual, base + size_t(vi) * N), r);
+                F::unpack(res[v], r);
 #pragma unroll
                 for (int e = 0; e < N; ++e) x[e] = x[e] + r[e];
                 raw[v] = F::pack(x); // h = T(x + r), the value the reference's add stores
