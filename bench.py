@@ -190,6 +190,140 @@ class Chain:
         O.argmax_rows(self.tok_idx, self.tok_val, self.logits)
 
 
+class Pool:
+    """Disjoint buffer sets cut from one allocation per tensor (slice + view keep the byte
+    offset), filled with seeded normal samples; enough sets that one pass over them moves
+    >= 512 MB, so the 256 MB Infinity Cache does not serve the timed launches."""
+
+    def __init__(self, L, rng):
+        self.L, self.rng = L, rng
+        self.dev = dict(device=L.DeviceType.AMD, device_id=0)
+        self.api = L.RuntimeAPI(L.DeviceType.AMD)
+        self.keep = []
+
+    def sets_for(self, nbytes, cap=256):
+        return int(max(2, min(cap, -(-(512 << 20) // max(1, nbytes)))))
+
+    def fill(self, shape, dtype, sets, scale=1.0, loc=0.0):
+        """`sets` tensors of `shape`; the first is sampled, the others copy it."""
+        L = self.L
+        n = int(np.prod(shape))
+        big = L.Tensor((sets * n,), dtype, **self.dev)
+        self.keep.append(big)
+        if dtype == L.DataType.BF16:
+            host = bf16(self.rng, (n,), scale, loc)
+        elif dtype == L.DataType.F32:
+            host = (loc + scale * self.rng.standard_normal(n, dtype=np.float32)).astype(np.float32)
+        else:
+            raise ValueError(dtype)
+        first = big.slice(0, 0, n)
+        first.load(host.ctypes.data_as(ctypes.c_void_p))
+        out = []
+        for k in range(sets):
+            t = big.slice(0, k * n, (k + 1) * n).view(*shape)
+            if k:
+                self.api.memcpy_sync(t.data_ptr(), first.data_ptr(), host.nbytes, L.MemcpyKind.D2D)
+            out.append(t)
+        return out
+
+    def empty(self, shape, dtype, sets):
+        L = self.L
+        n = int(np.prod(shape))
+        big = L.Tensor((sets * n,), dtype, **self.dev)
+        self.keep.append(big)
+        return [big.slice(0, k * n, (k + 1) * n).view(*shape) for k in range(sets)]
+
+    def ints(self, values_list):
+        return [self.L.Tensor.from_numpy(v, **self.dev) for v in values_list]
+
+
+def config_ops(L, rng):
+    """(config, op, algorithmic bytes per launch, launches per call, launch(i)) for the
+    parity configs other than the headline one (2 and 3)."""
+    O, BF, F32, I8, I64 = L.Ops, L.DataType.BF16, L.DataType.F32, L.DataType.I8, L.DataType.I64
+    P = Pool(L, rng)
+    cases = []
+
+    # config 0: Qwen2-1.5B shapes, f32, 128 tokens
+    t0, V0 = 128, 151936
+    table = P.fill((V0, H), F32, 1, 0.02)[0]
+    s = P.sets_for(t0 * H * 4 * 2)
+    ids = P.ints([rng.integers(0, V0, size=t0).astype(np.int64) for _ in range(s)])
+    emb = P.empty((t0, H), F32, s)
+    cases.append(("config0", "embedding f32 128x1536", t0 * 8 + 2 * t0 * H * 4, 1,
+                  lambda i: O.embedding(emb[i % s], ids[i % s], table)))
+    x, y = P.fill((t0, H), F32, s), P.empty((t0, H), F32, s)
+    w = P.fill((H,), F32, 1, 0.1, 1.0)[0]
+    cases.append(("config0", "rms_norm f32 [128,1536]", 2 * t0 * H * 4 + H * 4, 1,
+                  lambda i: O.rms_norm(y[i % s], x[i % s], w, 1e-6)))
+    sq = P.sets_for(t0 * 14 * 128 * 4 * 2)
+    q, k = P.fill((t0, NH, D), F32, sq), P.fill((t0, NKV, D), F32, sq)
+    qo, ko = P.empty((t0, NH, D), F32, sq), P.empty((t0, NKV, D), F32, sq)
+    pos0 = L.Tensor.from_numpy(np.arange(t0, dtype=np.int64), **P.dev)
+    cases.append(("config0", "rope q+k f32 [128,12+2,128]", 2 * t0 * (NH + NKV) * D * 4 + t0 * 8, 1,
+                  lambda i: O.rope_qk(qo[i % sq], q[i % sq], ko[i % sq], k[i % sq], pos0, 1e4)))
+    ss = P.sets_for(3 * t0 * I * 4)
+    g, u, a = P.fill((t0, I), F32, ss), P.fill((t0, I), F32, ss), P.empty((t0, I), F32, ss)
+    cases.append(("config0", "swiglu f32 [128,8960]", 3 * t0 * I * 4, 1,
+                  lambda i: O.swiglu(a[i % ss], g[i % ss], u[i % ss])))
+    sa = P.sets_for(V0 * 4)
+    lg = P.fill((1, V0), F32, sa)
+    mi, mv = P.empty((1,), I64, 1)[0], P.empty((1,), F32, 1)[0]
+    cases.append(("config0", "argmax f32 [1,151936] (latency)", V0 * 4 + 12, 1,
+                  lambda i: O.argmax(mi, mv, lg[i % sa])))
+
+    # config 2: Llama-8B shapes, bf16, 16384 tokens
+    t2, H2, I2, V2 = 16384, 4096, 14336, 128256
+    x2, y2 = P.fill((t2, H2), BF, 2), P.empty((t2, H2), BF, 2)
+    w2 = P.fill((H2,), BF, 1, 0.1, 1.0)[0]
+    cases.append(("config2", "rms_norm [16384,4096]", 2 * t2 * H2 * 2 + H2 * 2, 1,
+                  lambda i: O.rms_norm(y2[i % 2], x2[i % 2], w2, 1e-5)))
+    q2, k2 = P.fill((t2, 32, D), BF, 2), P.fill((t2, 8, D), BF, 2)
+    qo2, ko2 = P.empty((t2, 32, D), BF, 2), P.empty((t2, 8, D), BF, 2)
+    pos2 = L.Tensor.from_numpy(np.arange(t2, dtype=np.int64), **P.dev)
+    cases.append(("config2", "rope q+k [16384,32+8,128] theta 5e5", 2 * t2 * 40 * D * 2 + t2 * 8, 1,
+                  lambda i: O.rope_qk(qo2[i % 2], q2[i % 2], ko2[i % 2], k2[i % 2], pos2, 5e5)))
+    g2, u2, a2 = P.fill((t2, I2), BF, 2), P.fill((t2, I2), BF, 2), P.empty((t2, I2), BF, 2)
+    cases.append(("config2", "swiglu [16384,14336]", 3 * t2 * I2 * 2, 1,
+                  lambda i: O.swiglu(a2[i % 2], g2[i % 2], u2[i % 2])))
+    table2 = P.fill((V2, H2), BF, 1, 0.02)[0]
+    ids2 = P.ints([rng.integers(0, V2, size=t2).astype(np.int64) for _ in range(2)])
+    emb2 = P.empty((t2, H2), BF, 2)
+    cases.append(("config2", "embedding [128256,4096] x 16384 ids", t2 * 8 + 2 * t2 * H2 * 2, 1,
+                  lambda i: O.embedding(emb2[i % 2], ids2[i % 2], table2)))
+
+    # config 3: INT8 weights (per output channel) and KV cache (per token and head)
+    for rows, cols in ((8960, 1536), (1536, 8960)):
+        sw = P.sets_for(rows * cols * 3)
+        wt = P.fill((rows, cols), BF, sw, 0.02)
+        qc, sc = P.empty((rows, cols), I8, sw), P.empty((rows,), F32, sw)
+        dq = P.empty((rows, cols), BF, sw)
+        nb = rows * cols * 3 + rows * 4
+        cases.append(("config3", f"quantize W[{rows},{cols}]", nb, 1,
+                      lambda i, wt=wt, qc=qc, sc=sc, sw=sw: O.quantize_int8(qc[i % sw], sc[i % sw], wt[i % sw])))
+        cases.append(("config3", f"dequantize W[{rows},{cols}]", nb, 1,
+                      lambda i, dq=dq, qc=qc, sc=sc, sw=sw: O.dequantize_int8(dq[i % sw], qc[i % sw], sc[i % sw])))
+    tk = 32768
+    skv = P.sets_for(2 * tk * 2 * D * 3)
+    kv_k, kv_v = P.fill((tk, 2, D), BF, skv), P.fill((tk, 2, D), BF, skv)
+    ckq, cks = P.empty((tk, 2, D), I8, skv), P.empty((tk, 2), F32, skv)
+    cvq, cvs = P.empty((tk, 2, D), I8, skv), P.empty((tk, 2), F32, skv)
+    dk, dv = P.empty((tk, 2, D), BF, skv), P.empty((tk, 2, D), BF, skv)
+    kvb = 2 * (tk * 2 * D * 2 + tk * 2 * D + tk * 2 * 4)
+
+    def append(i):
+        O.kv_append_int8(ckq[i % skv], cks[i % skv], kv_k[i % skv], 0)
+        O.kv_append_int8(cvq[i % skv], cvs[i % skv], kv_v[i % skv], 0)
+
+    def read(i):
+        O.dequantize_int8(dk[i % skv], ckq[i % skv], cks[i % skv])
+        O.dequantize_int8(dv[i % skv], cvq[i % skv], cvs[i % skv])
+
+    cases.append(("config3", "KV append k+v [32768,2,128] (2 launches)", kvb, 2, append))
+    cases.append(("config3", "KV dequant read k+v [32768,2,128] (2 launches)", kvb, 2, read))
+    return cases, P
+
+
 def cpu_baseline(seconds):
     """Reference CPU ops (oracle/_ref, else the oracle port) on a row sample of config 1,
     single thread pinned to one core; GB/s with the same bytes formula as the GPU."""
@@ -296,6 +430,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-chain", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip configs 0, 2 and 3")
     ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain (profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="3 dispatches of a 256 MiB device copy (counter calibration), then 3 of "
@@ -407,6 +542,28 @@ def main():
         assert L.take_device_error() == 0
         del ch
 
+    configs = None
+    if not args.no_configs:
+        print("bench: building config 0 / 2 / 3 buffers", file=sys.stderr, flush=True)
+        cases, pool = config_ops(L, np.random.default_rng(9))
+        configs = {}
+        for cfg, name, nbytes, launches, fn in cases:
+            for i in range(3):
+                fn(i)
+            reps = max(args.steps, 20)
+            hip.record(e0, stream)
+            for i in range(reps):
+                fn(i)
+            hip.record(e1, stream)
+            us = hip.elapsed_ms(e0, e1) / reps * 1e3
+            gbs = nbytes / (us * 1e-6) / 1e9
+            configs.setdefault(cfg, {})[name] = {
+                "us": round(us, 3), "bytes": nbytes, "launches": launches,
+                "GB_s": round(gbs, 1), "frac_peak": round(gbs / PEAK_GBS, 4)}
+        assert L.take_device_error() == 0
+        del cases, pool
+        print("bench: configs " + json.dumps(configs), file=sys.stderr, flush=True)
+
     dom = per_op["swiglu"]
     roof = {"kernel": "swiglu binaryVec<BF16> [8192, 8960]", "bound": "hbm",
             "achieved": dom["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
@@ -426,7 +583,8 @@ def main():
         "frac_peak": round(value / PEAK_GBS, 4),
         "tokens_per_s": round(T / (ms_step * 1e-3)),
         "wall_s_timed": round(wall, 3),
-        "per_op": per_op, "chain": chain, "roofline": roof, "cpu_baseline": cpu,
+        "per_op": per_op, "chain": chain, "configs": configs, "roofline": roof,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
 
