@@ -171,7 +171,8 @@ class Chain:
     def bytes(self):
         t, e = self.TOK, 2
         norm = 4 * t * H * e + H * e
-        rope = 2 * t * (NH + NKV) * D * e + t * 8
+        # fused RoPE + INT8 KV append: q in/out, k and v in, codes and scales out
+        rope = 2 * t * NH * D * e + t * 8
         kv = 2 * (t * NKV * D * e + t * NKV * D + t * NKV * 4)
         swi = 3 * t * I * e
         layer = 2 * norm + rope + kv + swi
@@ -181,9 +182,8 @@ class Chain:
         O = self.L.Ops
         for b in self.layers:
             O.add_rms_norm(b["n1"], self.resid, b["attn"], self.resid, b["w1"], 1e-6)
-            O.rope_qk(b["q_out"], b["q"], b["k_out"], b["k"], self.pos, 1e6)
-            O.kv_append_int8(b["kc"], b["kcs"], b["k_out"], 0)
-            O.kv_append_int8(b["vc"], b["vcs"], b["v"], 0)
+            O.rope_kv_append_int8(b["q_out"], b["q"], b["k"], b["v"], self.pos, 1e6,
+                                  b["kc"], b["kcs"], b["vc"], b["vcs"], 0)
             O.add_rms_norm(b["n2"], self.resid, b["mlp"], self.resid, b["w2"], 1e-6)
             O.swiglu(b["act"], b["gate"], b["up"])
         O.rms_norm(self.final, self.resid, self.wf, 1e-6)

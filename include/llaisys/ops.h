@@ -60,6 +60,21 @@ __C {
      * (cos, sin) table of a token is computed once for both. */
     __export void llaisysROPEQK(llaisysTensor_t q_out, llaisysTensor_t q_in, llaisysTensor_t k_out,
                                 llaisysTensor_t k_in, llaisysTensor_t pos_ids, float theta);
+    /* Fused RoPE + INT8 KV-cache append (quantize-on-append), one launch for the reference
+     * decoder's rope(q), rope(k) and cache update (src/models/qwen2/attention.hpp:54-59,
+     * :108-123) with an INT8 cache:
+     *   q_out = llaisysROPE(q_in, pos_ids, theta)
+     *   k_cache / k_scale rows pos .. pos+seq-1 = llaisysKVAppendInt8 of llaisysROPE(k_in)
+     *   v_cache / v_scale rows pos .. pos+seq-1 = llaisysKVAppendInt8 of v_in
+     * bit-identical to that composition; the rope'd k is never stored in its element type.
+     * q [seq, nh_q, d]; k, v [seq, n_kvh, d]; caches [max_seq, n_kvh, d] I8 and
+     * [max_seq, n_kvh] F32; pos + seq <= max_seq. */
+    __export void llaisysROPEKVAppendInt8(llaisysTensor_t q_out, llaisysTensor_t q_in,
+                                          llaisysTensor_t k_in, llaisysTensor_t v_in,
+                                          llaisysTensor_t pos_ids, float theta,
+                                          llaisysTensor_t k_cache, llaisysTensor_t k_scale,
+                                          llaisysTensor_t v_cache, llaisysTensor_t v_scale,
+                                          size_t pos);
     /* Row-wise argmax: the reference argmax (argmax_cpu.cpp:9-28) applied to each row of
      * vals [rows, cols]; max_idx [rows] I32/I64, max_val [rows] with the dtype of vals. */
     __export void llaisysArgmaxRows(llaisysTensor_t max_idx, llaisysTensor_t max_val,

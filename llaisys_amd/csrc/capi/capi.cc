@@ -148,6 +148,14 @@ __C {
         llaisys::ops::ropeQK(q_out->tensor, q_in->tensor, k_out->tensor, k_in->tensor,
                              pos_ids->tensor, theta);
     }
+    void llaisysROPEKVAppendInt8(llaisysTensor_t q_out, llaisysTensor_t q_in, llaisysTensor_t k_in,
+                                 llaisysTensor_t v_in, llaisysTensor_t pos_ids, float theta,
+                                 llaisysTensor_t k_cache, llaisysTensor_t k_scale,
+                                 llaisysTensor_t v_cache, llaisysTensor_t v_scale, size_t pos) {
+        llaisys::ops::ropeKvAppendInt8(q_out->tensor, q_in->tensor, k_in->tensor, v_in->tensor,
+                                       pos_ids->tensor, theta, k_cache->tensor, k_scale->tensor,
+                                       v_cache->tensor, v_scale->tensor, pos);
+    }
     void llaisysArgmaxRows(llaisysTensor_t max_idx, llaisysTensor_t max_val, llaisysTensor_t vals) {
         llaisys::ops::argmaxRows(max_idx->tensor, max_val->tensor, vals->tensor);
     }

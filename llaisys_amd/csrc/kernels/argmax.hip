@@ -163,7 +163,7 @@ __global__ void __launch_bounds__(kBlock)
     }
 }
 
-constexpr size_t kCounterBytes = 256;
+constexpr size_t kCounterBytes = kScratchReserved;
 
 template <typename T>
 size_t segmentOf() {

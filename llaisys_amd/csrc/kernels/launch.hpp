@@ -29,6 +29,15 @@ void ropeQK(void *q_out, const void *q_in, size_t nh_q, void *k_out, const void 
             size_t nh_k, const int64_t *pos, size_t seq, size_t head_dim, float theta,
             llaisysDataType_t dt, hipStream_t stream);
 
+// Fused RoPE + INT8 KV append: q_out = rope(q); codes / scales of quantize(rope(k)) and
+// quantize(v) written to the cache rows the pointers start at.  Returns false (nothing
+// launched) for shapes the fused kernel does not cover; the caller then composes the ops.
+bool ropeKvAppendFused(void *q_out, const void *q_in, size_t nh_q, const void *k_in,
+                       const void *v_in, size_t nh_kv, int8_t *k_codes, float *k_scale,
+                       int8_t *v_codes, float *v_scale, const int64_t *pos, size_t seq,
+                       size_t head_dim, float theta, llaisysDataType_t dt, hipStream_t stream);
+size_t ropeKvAppendWorkspaceBytes(size_t seq, size_t nh_kv, size_t head_dim, llaisysDataType_t dt);
+
 // out = up * gate / (1 + exp(-gate)) over n elements.
 void swiglu(void *out, const void *gate, const void *up, size_t n, llaisysDataType_t dt,
             hipStream_t stream);
@@ -46,9 +55,14 @@ void embedding(void *out, const void *index, bool index_i64, size_t n_index, con
 void argmaxRows(void *idx, bool idx_i64, void *val, const void *vals, size_t rows, size_t cols,
                 llaisysDataType_t dt, hipStream_t stream);
 
+// Library scratch layout: the first kScratchReserved bytes hold the flat argmax's
+// completion counter, which must stay zero between launches; other users of the scratch
+// start after it.
+constexpr size_t kScratchReserved = 256;
+
 // Flat argmax over n elements; `workspace` (>= argmaxWorkspaceBytes(n)) holds the
-// per-block partials and a completion counter that must be zero before the first call
-// (the kernel leaves it zero again).
+// completion counter (first kScratchReserved bytes, zero before the first call; the kernel
+// leaves it zero again) and the per-block partials after it.
 size_t argmaxWorkspaceBytes(size_t n, llaisysDataType_t dt);
 void argmax(void *idx, bool idx_i64, void *val, const void *vals, size_t n,
             llaisysDataType_t dt, void *workspace, hipStream_t stream);

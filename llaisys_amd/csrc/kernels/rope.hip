@@ -16,6 +16,7 @@
 // written once).  q and k of the same tokens go through one launch.
 #include "common.hpp"
 #include "launch.hpp"
+#include "rope_common.hpp"
 #include "rowplan.hpp"
 
 #include <algorithm>
@@ -25,13 +26,9 @@ namespace llaisys::kernels {
 
 namespace {
 
-constexpr int kMaxHalf = 128;   // head_dim <= 256 uses the host frequency table
-constexpr int kLdsPairs = 1024; // (cos, sin) doubles staged per block: 16 KB
-constexpr int kMaxItems = 4;    // 16-byte items per lane held in registers
+using namespace rope_detail;
 
-struct FreqTable {
-    double f[kMaxHalf];
-};
+constexpr int kMaxItems = 4;    // 16-byte items per lane held in registers
 
 // Two tensors sharing positions and head_dim; tensor 1 may be absent (n_heads1 == 0).
 struct RopePair {
@@ -42,22 +39,6 @@ struct RopePair {
     int n_heads0;
     int n_heads1;
 };
-
-__device__ __forceinline__ double freqOf(const FreqTable &ft, int j, int d, float theta) {
-    if (j < kMaxHalf) return ft.f[j];
-    return 1.0 / pow(double(theta), double(2.0f * float(j) / float(d)));
-}
-
-// Partner exchange: the vector VPH lanes away.  For VPH = 8 (bf16 / f16 with head_dim 128)
-// the partner is in the same 16-lane DPP row, rotated by 8 (= lane ^ 8): a DPP move,
-// no LDS traffic.  Other widths use a cross-lane shuffle.
-template <int VPH>
-__device__ __forceinline__ uint32_t partnerOf(uint32_t v) {
-    if constexpr (VPH == 8)
-        return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
-    else
-        return uint32_t(__shfl_xor(int(v), VPH, kWave));
-}
 
 // Lane layout: item = one 16-byte vector of a head row, items of a row on consecutive
 // lanes, so every load / store instruction of a wavefront covers one contiguous 1 KB
@@ -168,16 +149,6 @@ __global__ void __launch_bounds__(256)
         F::put(out, base + j, float(A * c - B * sn));
         F::put(out, base + j + half, float(B * c + A * sn));
     }
-}
-
-FreqTable hostFreqs(size_t d, float theta) {
-    FreqTable ft{};
-    for (size_t j = 0; j < d / 2 && j < size_t(kMaxHalf); ++j) {
-        // Same expression and libm call as rope_cpu.cpp:31.
-        const float ex = 2.0f * float(j) / float(d);
-        ft.f[j] = 1.0 / std::pow(double(theta), double(ex));
-    }
-    return ft;
 }
 
 template <typename T, int IPT>

@@ -271,3 +271,62 @@ void kvAppendInt8(tensor_t cache_q, tensor_t cache_scale, tensor_t kv, size_t po
 }
 
 } // namespace llaisys::ops
+
+namespace llaisys::ops {
+
+// Fused RoPE + INT8 KV append: the reference decoder's rope(q), rope(k) and cache update
+// (src/models/qwen2/attention.hpp:54-59, :108-123) with the cache in INT8.
+void ropeKvAppendInt8(tensor_t q_out, tensor_t q_in, tensor_t k_in, tensor_t v_in,
+                      tensor_t pos_ids, float theta, tensor_t k_cache, tensor_t k_scale,
+                      tensor_t v_cache, tensor_t v_scale, size_t pos) {
+    CHECK_SAME_DEVICE(q_out, q_in, k_in, v_in, pos_ids, k_cache, k_scale, v_cache, v_scale);
+    for (const auto &t : {q_out, q_in, k_in, v_in, pos_ids, k_cache, k_scale, v_cache, v_scale})
+        ASSERT(t->isContiguous(), "RoPEKVAppend: tensors must be contiguous");
+    ASSERT(q_in->ndim() == 3 && k_in->ndim() == 3 && v_in->ndim() == 3, "input shape must be 3");
+    CHECK_SAME_SHAPE(q_in->shape(), q_out->shape());
+    CHECK_SAME_SHAPE(k_in->shape(), v_in->shape());
+    const size_t seq = q_in->shape()[0], nq = q_in->shape()[1], d = q_in->shape()[2];
+    const size_t nk = k_in->shape()[1];
+    ASSERT(k_in->shape()[0] == seq && k_in->shape()[2] == d,
+           "RoPEKVAppend: q and k must share seq_len and head_dim");
+    ASSERT(pos_ids->numel() == seq, "pos_ids length must match Seq_Len");
+    ASSERT(d % 2 == 0, "Head dimension must be even for RoPE");
+    CHECK_SAME_DTYPE(q_in->dtype(), q_out->dtype(), k_in->dtype(), v_in->dtype());
+    ASSERT(pos_ids->dtype() == LLAISYS_DTYPE_I64, "token id data type must be INT64");
+    requireFloat(q_in->dtype());
+    ASSERT(k_cache->dtype() == LLAISYS_DTYPE_I8 && v_cache->dtype() == LLAISYS_DTYPE_I8,
+           "RoPEKVAppend: cache codes must be INT8");
+    ASSERT(k_scale->dtype() == LLAISYS_DTYPE_F32 && v_scale->dtype() == LLAISYS_DTYPE_F32,
+           "RoPEKVAppend: cache scales must be F32");
+    ASSERT(k_cache->ndim() == 3 && k_scale->ndim() == 2, "RoPEKVAppend: cache [max_seq, n_kvh, d], scales [max_seq, n_kvh]");
+    CHECK_SAME_SHAPE(k_cache->shape(), v_cache->shape());
+    CHECK_SAME_SHAPE(k_scale->shape(), v_scale->shape());
+    const size_t max_seq = k_cache->shape()[0];
+    ASSERT(k_cache->shape()[1] == nk && k_cache->shape()[2] == d, "RoPEKVAppend: kv head shape mismatch");
+    ASSERT(k_scale->shape()[0] == max_seq && k_scale->shape()[1] == nk, "RoPEKVAppend: scale cache shape mismatch");
+    ASSERT(pos <= max_seq && seq <= max_seq - pos, "RoPEKVAppend: append past the cache end");
+    auto s = streamFor(q_in);
+    const size_t r0 = pos * nk;
+    auto *kc = reinterpret_cast<int8_t *>(k_cache->data()) + r0 * d;
+    auto *vc = reinterpret_cast<int8_t *>(v_cache->data()) + r0 * d;
+    auto *ks = reinterpret_cast<float *>(k_scale->data()) + r0;
+    auto *vs = reinterpret_cast<float *>(v_scale->data()) + r0;
+    const auto *p = reinterpret_cast<const int64_t *>(pos_ids->data());
+    if (kernels::ropeKvAppendFused(q_out->data(), q_in->data(), nq, k_in->data(), v_in->data(), nk,
+                                   kc, ks, vc, vs, p, seq, d, theta, q_in->dtype(), s)) {
+        launched("ropeKvAppend");
+        return;
+    }
+    // Shapes outside the fused kernel: the same composition through library scratch.
+    void *tmp = static_cast<char *>(device::amd::workspace(
+                    q_in->deviceId(), kernels::kScratchReserved +
+                                          kernels::ropeKvAppendWorkspaceBytes(seq, nk, d, q_in->dtype()))) +
+                kernels::kScratchReserved;
+    kernels::ropeQK(q_out->data(), q_in->data(), nq, tmp, k_in->data(), nk, p, seq, d, theta,
+                    q_in->dtype(), s);
+    kernels::quantizeInt8(kc, ks, tmp, seq * nk, d, q_in->dtype(), s);
+    kernels::quantizeInt8(vc, vs, v_in->data(), seq * nk, d, q_in->dtype(), s);
+    launched("ropeKvAppend (composed)");
+}
+
+} // namespace llaisys::ops

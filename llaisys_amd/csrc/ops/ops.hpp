@@ -19,5 +19,8 @@ void swiglu(tensor_t out, tensor_t gate, tensor_t up);
 void quantizeInt8(tensor_t q, tensor_t scale, tensor_t in);
 void dequantizeInt8(tensor_t out, tensor_t q, tensor_t scale);
 void kvAppendInt8(tensor_t cache_q, tensor_t cache_scale, tensor_t kv, size_t pos);
+void ropeKvAppendInt8(tensor_t q_out, tensor_t q_in, tensor_t k_in, tensor_t v_in,
+                      tensor_t pos_ids, float theta, tensor_t k_cache, tensor_t k_scale,
+                      tensor_t v_cache, tensor_t v_scale, size_t pos);
 
 } // namespace llaisys::ops

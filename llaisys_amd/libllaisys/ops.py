@@ -25,6 +25,7 @@ REFERENCE_OPS = {
 ADDED_OPS = {
     "llaisysAddRmsNorm": [T, T, T, T, T, c_float],
     "llaisysROPEQK": [T, T, T, T, T, c_float],
+    "llaisysROPEKVAppendInt8": [T, T, T, T, T, c_float, T, T, T, T, c_size_t],
     "llaisysArgmaxRows": [T, T, T],
     "llaisysQuantizeInt8": [T, T, T],
     "llaisysDequantizeInt8": [T, T, T],

@@ -66,6 +66,15 @@ class Ops:
                                   k_in.lib_tensor(), pos_ids.lib_tensor(), c_float(theta))
 
     @staticmethod
+    def rope_kv_append_int8(q_out: Tensor, q_in: Tensor, k_in: Tensor, v_in: Tensor,
+                            pos_ids: Tensor, theta: float, k_cache: Tensor, k_scale: Tensor,
+                            v_cache: Tensor, v_scale: Tensor, pos: int):
+        LIB_LLAISYS.llaisysROPEKVAppendInt8(
+            q_out.lib_tensor(), q_in.lib_tensor(), k_in.lib_tensor(), v_in.lib_tensor(),
+            pos_ids.lib_tensor(), c_float(theta), k_cache.lib_tensor(), k_scale.lib_tensor(),
+            v_cache.lib_tensor(), v_scale.lib_tensor(), c_size_t(pos))
+
+    @staticmethod
     def argmax_rows(max_idx: Tensor, max_val: Tensor, vals: Tensor):
         LIB_LLAISYS.llaisysArgmaxRows(max_idx.lib_tensor(), max_val.lib_tensor(),
                                       vals.lib_tensor())

@@ -479,3 +479,57 @@ def test_graph_replays_match_eager():
         for name, tt in outs.items():
             assert_exact(tt.numpy(), eager[name], f"replay {replay}: {name}")
     no_device_error()
+
+
+# ---- fused RoPE + INT8 KV append ---------------------------------------------------------
+
+@pytest.mark.parametrize("dt", ["bf16", "f32", "f16"])
+@pytest.mark.parametrize("seq,nq,nk,d,pos0,max_seq,theta", [
+    (2048, 12, 2, 128, 0, 2048, 1e6),     # config 4 layer
+    (8192, 12, 2, 128, 0, 8192, 1e4),     # config 1 shape
+    (300, 32, 8, 128, 100, 1024, 5e5),    # Llama-8B heads, append at an offset
+    (1, 12, 2, 128, 4095, 4096, 1e6),     # one decode token at the cache end
+    (7, 3, 1, 6, 2, 16, 1e4),             # odd half-dim: composed fallback
+    (9, 64, 64, 128, 0, 9, 1e4),          # more rows per token than the fused plan holds
+])
+def test_rope_kv_append_equals_composition(dt, seq, nq, nk, d, pos0, max_seq, theta):
+    """The fused op equals llaisysROPEQK followed by two llaisysKVAppendInt8, bit for bit,
+    and that composition matches the oracle (rope within tolerance, codes exact on the
+    GPU's own rope'd k)."""
+    rng = np.random.default_rng(seed_of(seq, nq, dt))
+    T = DTS[dt]
+    q, k, v = sample(rng, (seq, nq, d), dt), sample(rng, (seq, nk, d), dt), sample(rng, (seq, nk, d), dt)
+    pos = np.arange(pos0, pos0 + seq, dtype=np.int64)
+    tq, tk, tv, tp = dev(q, T), dev(k, T), dev(v, T), dev(pos)
+
+    def caches():
+        return (dev(np.full((max_seq, nk, d), 5, np.int8)), dev(np.full((max_seq, nk), -2.0, np.float32)),
+                dev(np.full((max_seq, nk, d), 5, np.int8)), dev(np.full((max_seq, nk), -2.0, np.float32)))
+
+    kc, ks, vc, vs = caches()
+    qo = empty(q.shape, T)
+    L.Ops.rope_kv_append_int8(qo, tq, tk, tv, tp, theta, kc, ks, vc, vs, pos0)
+    # composition through the separate entry points
+    kc2, ks2, vc2, vs2 = caches()
+    qo2, ko2 = empty(q.shape, T), empty(k.shape, T)
+    L.Ops.rope_qk(qo2, tq, ko2, tk, tp, theta)
+    L.Ops.kv_append_int8(kc2, ks2, ko2, pos0)
+    L.Ops.kv_append_int8(vc2, vs2, tv, pos0)
+    for a, b, what in ((qo, qo2, "q"), (kc, kc2, "k codes"), (ks, ks2, "k scales"),
+                       (vc, vc2, "v codes"), (vs, vs2, "v scales")):
+        assert_exact(a.numpy(), b.numpy(), what)
+    # and against the oracle: rope within tolerance, codes of the GPU's rope'd k exact
+    assert_close(qo.numpy(), oracle.rope(q, pos, theta), "q vs oracle")
+    hq, hs = np.full((max_seq, nk, d), 5, np.int8), np.full((max_seq, nk), -2.0, np.float32)
+    assert oracle.kv_append_int8(hq, hs, ko2.numpy(), pos0) == 0
+    assert_exact(kc.numpy(), hq, "k codes vs oracle")
+    assert_exact(ks.numpy(), hs, "k scales vs oracle")
+    hq, hs = np.full((max_seq, nk, d), 5, np.int8), np.full((max_seq, nk), -2.0, np.float32)
+    assert oracle.kv_append_int8(hq, hs, v, pos0) == 0
+    assert_exact(vc.numpy(), hq, "v codes vs oracle")
+    # the composed fallback must leave the flat argmax's scratch counter intact
+    logits = sample(rng, (151936,), "bf16")
+    i, m = empty((1,), L.DataType.I64), empty((1,), L.DataType.BF16)
+    L.Ops.argmax(i, m, dev(logits, L.DataType.BF16))
+    assert i.numpy()[0] == oracle.argmax(logits)[0]
+    no_device_error()
