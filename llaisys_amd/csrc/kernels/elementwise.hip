@@ -23,7 +23,12 @@ namespace llaisys::kernels {
 
 namespace {
 
-constexpr int kU = 2;
+// 16-byte vectors per input per lane, measured per kernel on MI355X: the binary ops
+// (two streamed inputs) are fastest with one (swiglu [8192, 8960]: 69.3 us vs 71.2 with
+// two, 75.1 with four); dequantize, whose lanes read only 8 bytes of codes per vector,
+// needs four to keep enough bytes in flight (8960x1536: 6.7 us vs 8.5 with two).
+constexpr int kBinaryU = 1;
+constexpr int kDequantU = 4;
 
 struct SwigluOp {
     __device__ static float apply(float g, float u) {
@@ -43,7 +48,7 @@ struct AddOp {
     __device__ static float apply(float a, float b) { return a + b; }
 };
 
-template <typename T, typename Op>
+template <typename T, typename Op, int kU>
 __global__ void __launch_bounds__(256)
     binaryVec(void *__restrict__ out, const void *__restrict__ a, const void *__restrict__ b,
               size_t nvec) {
@@ -87,7 +92,7 @@ void launchBinary(void *out, const void *a, const void *b, size_t n, hipStream_t
     constexpr int N = Fmt<T>::kVec;
     if (n % N == 0 && aligned16(out) && aligned16(a) && aligned16(b)) {
         const size_t nvec = n / N;
-        binaryVec<T, Op><<<blocksFor(nvec, 256 * kU), 256, 0, s>>>(out, a, b, nvec);
+        binaryVec<T, Op, kBinaryU><<<blocksFor(nvec, 256 * kBinaryU), 256, 0, s>>>(out, a, b, nvec);
         return;
     }
     const unsigned grid = unsigned(std::min<size_t>(blocksFor(n, 256), 1u << 20));
@@ -125,7 +130,7 @@ __device__ __forceinline__ void loadCodes(const int8_t *q, size_t i, float *f) {
     }
 }
 
-template <typename T>
+template <typename T, int kU>
 __global__ void __launch_bounds__(256)
     dequantVec(void *__restrict__ out, const int8_t *__restrict__ q,
                const float *__restrict__ scale, size_t nvec, size_t vec_per_row) {
@@ -163,7 +168,7 @@ void launchDequant(void *out, const int8_t *q, const float *scale, size_t rows, 
     const size_t code_align = reinterpret_cast<uintptr_t>(q) % N;
     if (cols % N == 0 && aligned16(out) && code_align == 0) {
         const size_t nvec = n / N;
-        dequantVec<T><<<blocksFor(nvec, 256 * kU), 256, 0, s>>>(out, q, scale, nvec, cols / N);
+        dequantVec<T, kDequantU><<<blocksFor(nvec, 256 * kDequantU), 256, 0, s>>>(out, q, scale, nvec, cols / N);
         return;
     }
     const unsigned grid = unsigned(std::min<size_t>(blocksFor(n, 256), 1u << 20));
