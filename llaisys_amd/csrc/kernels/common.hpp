@@ -4,8 +4,14 @@
 // 4 x f32, 8 x bf16 or 8 x f16.  Arithmetic is always f32 (f64 for RoPE).  The 16-bit
 // conversions reproduce the reference's rules bit for bit (src/utils/types.cpp:6-84):
 // bf16 rounds half to even through "+0x7FFF + lsb" with no NaN special case, f16
-// truncates.  The hardware converters are not used because they differ on NaN inputs
-// (bf16, f16) and round instead of truncating (f16).
+// truncates.  `pack` applies these rules to any f32.  `packQ` may use gfx950's
+// v_cvt_pk_bf16_f32 (one instruction per two elements instead of five): compared over all
+// 2^32 f32 inputs on MI355X it equals the reference rule for every non-NaN value and for
+// every quiet NaN whose low 16 bits are zero, and differs only for signalling NaNs and NaN
+// payloads in the low 16 bits (it quiets and truncates them).  Every f32 that a kernel
+// computes by arithmetic from bf16 / f16 inputs is in the first class (a NaN result is
+// quiet and carries an input's payload or the default NaN), so kernels use packQ unless
+// an f32 operand supplied by the caller (eps, theta, a dequantization scale) is a NaN.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -75,6 +81,8 @@ struct Fmt<F32> {
         return v4u{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
                    __float_as_uint(f[3])};
     }
+    __device__ static v4u packQ(const float *f) { return pack(f); }
+    static constexpr uint32_t kSignBits = 0x80000000u; // sign bits of the elements in a word
 };
 
 template <typename Cvt>
@@ -102,15 +110,28 @@ struct Half16 {
         for (int k = 0; k < 4; ++k) w[k] = Cvt::narrow(f[2 * k]) | (Cvt::narrow(f[2 * k + 1]) << 16);
         return v4u{w[0], w[1], w[2], w[3]};
     }
+    __device__ static v4u packQ(const float *f) {
+        return v4u{Cvt::narrow2Q(f[0], f[1]), Cvt::narrow2Q(f[2], f[3]), Cvt::narrow2Q(f[4], f[5]),
+                   Cvt::narrow2Q(f[6], f[7])};
+    }
+    static constexpr uint32_t kSignBits = 0x80008000u;
 };
+
+typedef float v2f __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 struct Bf16Cvt {
     __device__ static float widen(uint32_t b) { return bf16ToF32(b); }
     __device__ static uint32_t narrow(float f) { return f32ToBf16(f); }
+    // two elements, (lo, hi), by v_cvt_pk_bf16_f32 (see packQ above)
+    __device__ static uint32_t narrow2Q(float lo, float hi) {
+        return __builtin_bit_cast(uint32_t, __builtin_convertvector(v2f{lo, hi}, v2bf));
+    }
 };
 struct F16Cvt {
     __device__ static float widen(uint32_t h) { return f16ToF32(h); }
     __device__ static uint32_t narrow(float f) { return f32ToF16(f); }
+    __device__ static uint32_t narrow2Q(float lo, float hi) { return narrow(lo) | (narrow(hi) << 16); }
 };
 
 template <>
@@ -146,9 +167,13 @@ __device__ __forceinline__ void store16Stream(void *base, size_t elem, const v4u
 }
 
 // ---- reductions over a group of G consecutive lanes ------------------------------------
-// G <= 64: butterfly inside the wavefront.  G > 64: butterfly per wave, then the G/64
-// wave partials of the group are combined in a fixed order through LDS (`red` holds one
-// slot per wave of the block).  Every thread of the block must call these (barriers).
+// G <= 64: butterfly inside the wavefront without LDS: DPP quad permutes for distances 1
+// and 2, row half-mirror and row mirror for 4 and 8 (equivalent to xor 4 / xor 8 once the
+// smaller groups are uniform), v_permlane16_swap / v_permlane32_swap for 16 and 32.  Both
+// lanes of a pair combine the same two values in the same order, so every lane of the
+// group ends with the same bits.  G > 64: butterfly per wave, then the G/64 wave partials
+// of the group are combined in a fixed order through LDS (`red` holds one slot per wave of
+// the block).  Every thread of the block must call these (barriers).
 
 struct SumOp {
     __device__ static float apply(float a, float b) { return a + b; }
@@ -158,11 +183,41 @@ struct MaxOp {
     __device__ static float apply(float a, float b) { return b > a ? b : a; }
 };
 
-template <int G, typename Op>
-__device__ __forceinline__ float groupReduce(float v, float *red) {
-    constexpr int kSteps = G < kWave ? G : kWave;
-#pragma unroll
-    for (int m = kSteps / 2; m > 0; m >>= 1) v = Op::apply(v, __shfl_xor(v, m, kWave));
+template <int M, typename Op, typename V>
+__device__ __forceinline__ V butterflyStep(V v) {
+    static_assert(sizeof(V) == 4, "32-bit values");
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if constexpr (M <= 8) {
+        constexpr int kCtrl = M == 1 ? 0xB1 : (M == 2 ? 0x4E : (M == 4 ? 0x141 : 0x140));
+        const uint32_t p = uint32_t(__builtin_amdgcn_mov_dpp(int(u), kCtrl, 0xF, 0xF, false));
+        // lo / hi: the pair's lower lane's value first in both lanes
+        const bool lower = (threadIdx.x & (2 * M - 1)) < M;
+        const V a = __builtin_bit_cast(V, lower ? u : p), b = __builtin_bit_cast(V, lower ? p : u);
+        return Op::apply(a, b);
+    } else {
+        static_assert(M == 16 || M == 32, "distance");
+        const auto r = M == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                               : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return Op::apply(__builtin_bit_cast(V, uint32_t(r[0])), __builtin_bit_cast(V, uint32_t(r[1])));
+    }
+}
+
+// Reduction over aligned groups of G <= 64 consecutive lanes; every lane gets the result.
+template <int G, typename Op, typename V>
+__device__ __forceinline__ V waveGroupReduce(V v) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8 || G == 16 || G == 32 || G == 64, "group");
+    if constexpr (G >= 2) v = butterflyStep<1, Op>(v);
+    if constexpr (G >= 4) v = butterflyStep<2, Op>(v);
+    if constexpr (G >= 8) v = butterflyStep<4, Op>(v);
+    if constexpr (G >= 16) v = butterflyStep<8, Op>(v);
+    if constexpr (G >= 32) v = butterflyStep<16, Op>(v);
+    if constexpr (G >= 64) v = butterflyStep<32, Op>(v);
+    return v;
+}
+
+template <int G, typename Op, typename V>
+__device__ __forceinline__ V groupReduce(V v, V *red) {
+    v = waveGroupReduce<(G < kWave ? G : kWave), Op>(v);
     if constexpr (G > kWave) {
         const int wave = threadIdx.x / kWave;
         if (threadIdx.x % kWave == 0) red[wave] = v;

@@ -73,7 +73,7 @@ __global__ void __launch_bounds__(256)
             F::unpack(rb[k], y);
 #pragma unroll
             for (int e = 0; e < N; ++e) x[e] = Op::apply(x[e], y[e]);
-            store16Stream<T>(out, i * N, F::pack(x));
+            store16Stream<T>(out, i * N, F::packQ(x));
         }
     }
 }
@@ -133,7 +133,7 @@ __device__ __forceinline__ void loadCodes(const int8_t *q, size_t i, float *f) {
 template <typename T, int kU>
 __global__ void __launch_bounds__(256)
     dequantVec(void *__restrict__ out, const int8_t *__restrict__ q,
-               const float *__restrict__ scale, size_t nvec, size_t vec_per_row) {
+               const float *__restrict__ scale, size_t nvec, DivU64 rowdiv) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
     const size_t first = size_t(blockIdx.x) * 256 * kU + threadIdx.x;
@@ -143,10 +143,12 @@ __global__ void __launch_bounds__(256)
         if (i < nvec) {
             float f[N];
             loadCodes<N>(q, i * N, f);
-            const float sc = scale[i / vec_per_row];
+            const float sc = scale[rowdiv.div(i)];
 #pragma unroll
             for (int e = 0; e < N; ++e) f[e] = f[e] * sc;
-            store16Stream<T>(out, i * N, F::pack(f));
+            // a NaN scale is caller data whose payload packQ would not round like the
+            // reference; such vectors take the exact rounding
+            store16Stream<T>(out, i * N, sc == sc ? F::packQ(f) : F::pack(f));
         }
     }
 }
@@ -168,7 +170,7 @@ void launchDequant(void *out, const int8_t *q, const float *scale, size_t rows, 
     const size_t code_align = reinterpret_cast<uintptr_t>(q) % N;
     if (cols % N == 0 && aligned16(out) && code_align == 0) {
         const size_t nvec = n / N;
-        dequantVec<T, kDequantU><<<blocksFor(nvec, 256 * kDequantU), 256, 0, s>>>(out, q, scale, nvec, cols / N);
+        dequantVec<T, kDequantU><<<blocksFor(nvec, 256 * kDequantU), 256, 0, s>>>(out, q, scale, nvec, DivU64(cols / N));
         return;
     }
     const unsigned grid = unsigned(std::min<size_t>(blocksFor(n, 256), 1u << 20));

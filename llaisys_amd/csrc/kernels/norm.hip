@@ -4,7 +4,9 @@
 // s = sum(x^2) in f32, rms = sqrtf(s / cols + eps), inv = 1 / rms, y = T((x * w) * inv).
 // The fused variant first forms h = T(x + r) exactly as src/ops/add/cpu/add_cpu.cpp:12
 // (f32 add, reference rounding), stores h and normalises h.  Only the summation order
-// differs from the reference (a lane-parallel tree instead of a left-to-right loop).
+// differs from the reference (a lane-parallel tree of fused multiply-adds instead of a
+// left-to-right loop).  Outputs use packQ; a NaN eps, the one caller-supplied f32 whose
+// NaN payload could reach them, takes the scalar kernel, which rounds exactly.
 //
 // Design: HBM-bound; a row lives in registers between the reduction and the scaling so
 // x (and r) are read once and y (and h) written once.  16-byte loads per lane, butterfly
@@ -15,6 +17,8 @@
 #include "common.hpp"
 #include "launch.hpp"
 #include "rowplan.hpp"
+
+#include <cmath>
 
 namespace llaisys::kernels {
 
@@ -60,7 +64,7 @@ __global__ void __launch_bounds__(blockFor<G>())
                 F::unpack(res[v], r);
 #pragma unroll
                 for (int e = 0; e < N; ++e) x[e] = x[e] + r[e];
-                raw[v] = F::pack(x); // h = T(x + r), the value the reference's add stores
+                raw[v] = F::packQ(x); // h = T(x + r), the value the reference's add stores
                 store16Stream<T>(residual_out, base + size_t(vi) * N, raw[v]);
             }
         }
@@ -73,7 +77,7 @@ __global__ void __launch_bounds__(blockFor<G>())
             float x[N];
             F::unpack(raw[v], x);
 #pragma unroll
-            for (int e = 0; e < N; ++e) ss += x[e] * x[e];
+            for (int e = 0; e < N; ++e) ss = fmaf(x[e], x[e], ss);
         }
     }
     ss = groupReduce<G, SumOp>(ss, red);
@@ -88,7 +92,7 @@ __global__ void __launch_bounds__(blockFor<G>())
             F::unpack(load16<T>(weight, size_t(vi) * N), w);
 #pragma unroll
             for (int e = 0; e < N; ++e) y[e] = x[e] * w[e] * inv;
-            store16Stream<T>(out, base + size_t(vi) * N, F::pack(y));
+            store16Stream<T>(out, base + size_t(vi) * N, F::packQ(y));
         }
     }
 }
@@ -129,7 +133,7 @@ void launch(void *out, void *res_out, const void *in, const void *res, const voi
     const bool vec = cols % N == 0 && cols <= size_t(INT32_MAX) && aligned16(out) &&
                      aligned16(in) && aligned16(w) &&
                      (!fused || (aligned16(res) && aligned16(res_out)));
-    RowPlan plan = vec ? planRow(cols / N) : RowPlan{};
+    RowPlan plan = vec && !std::isnan(eps) ? planRow(cols / N) : RowPlan{};
     bool done = false;
     withPlan(plan, [&](auto g, auto v) {
         constexpr int G = decltype(g)::value, V = decltype(v)::value; // V: vectors per lane

@@ -8,13 +8,17 @@
 // max is order-independent and every other step is a single correctly rounded operation.
 //
 // Design: the row lives in registers (same lane-group plan as rms_norm), so x is read
-// once; codes are written as 8-byte (bf16/f16 input) or 4-byte (f32) stores per lane and
+// once; amax is an integer max over the packed magnitude bits and the codes come from the
+// division-free correctly rounded quotient of quantize.hpp, ~7 VALU operations per bf16
+// element in all; codes are written as 8-byte (bf16/f16 input) or 4-byte (f32) stores per lane and
 // the scale by the group's first lane.  A KV-cache append is this kernel pointed at the
 // cache rows pos .. pos + n_tok, so the codes go straight into the cache.
 #include "common.hpp"
 #include "launch.hpp"
 #include "quantize.hpp"
 #include "rowplan.hpp"
+
+#include <type_traits>
 
 namespace llaisys::kernels {
 
@@ -36,25 +40,45 @@ __global__ void __launch_bounds__(blockFor<G>())
     const size_t base = row * size_t(cols);
 
     v4u raw[VMAX];
-    float amax = 0.0f;
 #pragma unroll
     for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
         if (live && vi < nvec) raw[v] = load16Stream<T>(in, base + size_t(vi) * N);
     }
+    // amax: integer max of the magnitude bits; the float rule only for a row with a NaN
+    // (the test is uniform over the group, so the group's lanes all take it)
+    using A = AbsBits<T>;
+    uint32_t bits = 0;
 #pragma unroll
     for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
-        if (live && vi < nvec) {
-            float x[N];
-            F::unpack(raw[v], x);
-#pragma unroll
-            for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(x[e]));
-        }
+        if (live && vi < nvec) bits = A::fold(bits, raw[v]);
     }
-    amax = groupReduce<G, MaxOp>(amax, red);
+    bits = groupReduce<G, MaxU32Op>(A::finish(bits), reinterpret_cast<uint32_t *>(red));
+    float amax = A::value(bits);
+    if (__builtin_expect(bits > A::kInf, 0)) {
+        amax = 0.0f;
+#pragma unroll
+        for (int v = 0; v < VMAX; ++v) {
+            const int vi = lane + v * G;
+            if (live && vi < nvec) {
+                float x[N];
+                F::unpack(raw[v], x);
+#pragma unroll
+                for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(x[e]));
+            }
+        }
+        amax = groupReduce<G, MaxOp>(amax, red);
+    }
     const RowQuantizer qz(amax);
     if (live && lane == 0) scale[row] = qz.scale;
+    if (__builtin_expect(qz.exact_only, 0)) {
+        // scale < 2^-96 (or an all-zero row): IEEE quotients, re-reading the row's elements
+        // so that this rare path adds no per-vector code to the common one
+        for (int j = lane; live && j < cols; j += G)
+            q[base + j] = int8_t(codeOf(F::get(in, base + j), amax, qz.scale));
+        return;
+    }
 #pragma unroll
     for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
@@ -62,7 +86,7 @@ __global__ void __launch_bounds__(blockFor<G>())
             float x[N];
             uint32_t c[N];
             F::unpack(raw[v], x);
-            qz.codes<N>(x, c);
+            qz.fastCodes<N, std::is_same_v<T, F32>>(x, c);
             storeCodes<N>(q, base + size_t(vi) * N, c);
         }
     }

@@ -4,16 +4,17 @@
 // j < d/2: freq_j = 1 / pow((double)theta, (double)(2.0f * j / d)), angle = (double)p_i *
 // freq_j, and the pair (x_j, x_{j+d/2}) is rotated in double precision; the result is
 // rounded double -> float -> element type.  freq_j is computed on the host with the same
-// libm pow the reference calls, so the angles are bit-identical; cos/sin come from the
-// device's double-precision libm (within an ulp of glibc's, which the final float rounding
-// absorbs).
+// libm pow the reference calls, so the angles are bit-identical; cos/sin come from
+// sincos.hpp (within an ulp of glibc's, which the final float rounding absorbs).
 //
 // Design: HBM-bound.  A 256-thread block owns a run of tokens.  Each lane first issues the
-// 16-byte loads of its (token, head, 8-pair) items (both halves of the head), then the
-// block computes the (cos, sin) pairs of its tokens into LDS -- d/2 sincos per token,
-// shared by every q and k head -- so the f64 trig overlaps the load latency; finally each
-// lane rotates and stores its items.  Loads and stores are non-temporal (read once,
-// written once).  q and k of the same tokens go through one launch.
+// 16-byte loads of its items, then the block computes the (cos, sin) pairs of its tokens
+// into LDS -- d/2 per token, shared by every q and k head -- while the loads are in
+// flight; after the barrier each lane rotates and stores its items.  The kernel stays at
+// <= 64 VGPRs for the common shapes (8 waves per SIMD): the trig is the ~40-instruction
+// routine of sincos.hpp, the device library only on an out-of-line rare path.  Loads and
+// stores are non-temporal (read once, written once).  q and k of the same tokens go
+// through one launch.
 #include "common.hpp"
 #include "launch.hpp"
 #include "rope_common.hpp"
@@ -43,74 +44,72 @@ struct RopePair {
 // Lane layout: item = one 16-byte vector of a head row, items of a row on consecutive
 // lanes, so every load / store instruction of a wavefront covers one contiguous 1 KB
 // (an earlier layout that gave each lane the vector pair (j, j + d/2) split every
-// instruction into 8 half-rows 256 B apart and ran ~20 % slower).  The rotation partner of
-// a vector sits VPH lanes away and is fetched with a cross-lane exchange.  VPH (16-byte
-// vectors per half head) is a power of two <= 32, so a row never straddles a wavefront
-// and item -> (row, vector) is a shift; item -> token uses `tok_magic`
-// (floor(2^32 / items_per_token) + 1, exact while item * items_per_token < 2^32).
+// instruction into 8 half-rows 256 B apart and ran ~20 % slower).  A block's items are
+// tensor-major: first the ntok * nv0 vectors of tensor 0 for its tokens (one contiguous
+// range of that tensor), then tensor 1's; so an item's address is a per-block base
+// (scalar registers) plus a 32-bit lane offset.  The rotation partner of a vector sits
+// VPH lanes away and is fetched with a cross-lane exchange.  VPH (16-byte vectors per
+// half head) is a power of two <= 32, so a row never straddles a wavefront; item ->
+// token is a multiply by magic_t = floor(2^32 / nv_t) + 1, exact for item * nv_t < 2^32.
 template <typename T, int IPT, int VPH>
 __global__ void __launch_bounds__(256)
     ropeVec(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int tok_per_block,
-            uint32_t tok_magic, FreqTable ft) {
+            uint32_t magic0, uint32_t magic1, FreqTable ft) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
     constexpr int kRowVec = 2 * VPH; // vectors per head row
     constexpr int kHalf = VPH * N;
-    constexpr int kShift = __builtin_ctz(kRowVec);
     __shared__ double2 cs[kLdsPairs];
 
-    const int per_tok = (tp.n_heads0 + tp.n_heads1) * kRowVec;
+    const int nv0 = tp.n_heads0 * kRowVec, nv1 = tp.n_heads1 * kRowVec;
     const size_t t0 = size_t(blockIdx.x) * tok_per_block;
     const int ntok = int(min(size_t(tok_per_block), seq - t0));
-    const int items = ntok * per_tok;
+    const int items0 = ntok * nv0;
+    const int items = items0 + ntok * nv1;
+    const size_t blk0 = t0 * size_t(nv0) * 16, blk1 = t0 * size_t(nv1) * 16; // bytes
+    const char *in0 = static_cast<const char *>(tp.in0) + blk0;
+    const char *in1 = static_cast<const char *>(tp.in1) + blk1;
+    char *out0 = static_cast<char *>(tp.out0) + blk0;
+    char *out1 = static_cast<char *>(tp.out1) + blk1;
+
+    const AngleInputs ang0 = firstAngle(pos, t0, ntok, kHalf, ft); // before the item loads
 
     // 1. issue this lane's loads (one contiguous 16-byte vector per item)
     v4u raw[IPT];
-    size_t off[IPT];
+    uint32_t off[IPT];
     int tok[IPT];
     bool second[IPT];
 #pragma unroll
     for (int k = 0; k < IPT; ++k) {
         const int it = threadIdx.x + k * 256;
-        if (it < items) {
-            const int tt = int(__umulhi(uint32_t(it), tok_magic));
-            const int rem = it - tt * per_tok;
-            int h = rem >> kShift;
-            const int v = rem & (kRowVec - 1);
-            second[k] = h >= tp.n_heads0;
-            const int nh = second[k] ? tp.n_heads1 : tp.n_heads0;
-            if (second[k]) h -= tp.n_heads0;
-            tok[k] = tt;
-            off[k] = ((t0 + tt) * size_t(nh) + h) * size_t(2 * kHalf) + size_t(v) * N;
-            raw[k] = load16Stream<T>(second[k] ? tp.in1 : tp.in0, off[k]);
-        } else {
-            raw[k] = v4u{0, 0, 0, 0};
-        }
+        second[k] = it >= items0;
+        const uint32_t rel = uint32_t(second[k] ? it - items0 : it);
+        tok[k] = int(__umulhi(rel, second[k] ? magic1 : magic0));
+        off[k] = rel * 16u;
+        // unconditional load (idle lanes read the block's first vector), so the compiler can
+        // count these loads as outstanding when the trig waits for its own inputs
+        const char *src = it < items ? (second[k] ? in1 : in0) + off[k] : in0;
+        raw[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
     }
 
-    // 2. (cos, sin) of this block's tokens
-    for (int i = threadIdx.x; i < ntok * kHalf; i += 256) {
-        const int tt = i / kHalf, j = i % kHalf;
-        const double ang = double(pos[t0 + tt]) * ft.f[j];
-        double sn, c;
-        sincos(ang, &sn, &c);
-        cs[i] = make_double2(c, sn);
-    }
-    __syncthreads();
+    // 2. (cos, sin) of this block's tokens, while the loads are in flight
+    blockCosSin(cs, ang0, pos, t0, ntok, kHalf, ft);
 
     // 3. exchange with the partner vector, rotate, store.  First half of a row:
-    //    y = x*c - partner*s; second half: y = x*c + partner*s -- the reference's
-    //    a*c - b*s and b*c + a*s with the same operation order (rope_cpu.cpp:40-41).
+    //    y = x*c + (-partner)*s; second half: y = x*c + partner*s -- the reference's
+    //    a*c - b*s and b*c + a*s with the same roundings (rope_cpu.cpp:40-41); the
+    //    partner's sign is flipped on its packed words, one XOR per 32 bits.
     const int v_lane = threadIdx.x & (kRowVec - 1);
     const bool upper = v_lane >= VPH;
     const int jv = v_lane & (VPH - 1);
+    const uint32_t flip = upper ? 0u : F::kSignBits;
 #pragma unroll
     for (int k = 0; k < IPT; ++k) {
         v4u other;
-        other.x = partnerOf<VPH>(raw[k].x);
-        other.y = partnerOf<VPH>(raw[k].y);
-        other.z = partnerOf<VPH>(raw[k].z);
-        other.w = partnerOf<VPH>(raw[k].w);
+        other.x = partnerOf<VPH>(raw[k].x) ^ flip;
+        other.y = partnerOf<VPH>(raw[k].y) ^ flip;
+        other.z = partnerOf<VPH>(raw[k].z) ^ flip;
+        other.w = partnerOf<VPH>(raw[k].w) ^ flip;
         const int it = threadIdx.x + k * 256;
         if (it < items) {
             float x[N], p[N], y[N];
@@ -120,10 +119,11 @@ __global__ void __launch_bounds__(256)
 #pragma unroll
             for (int e = 0; e < N; ++e) {
                 const double c = row[e].x, sn = row[e].y;
-                const double own = x[e], partner = upper ? double(p[e]) : -double(p[e]);
-                y[e] = float(own * c + partner * sn);
+                y[e] = float(double(x[e]) * c + double(p[e]) * sn);
             }
-            store16Stream<T>(second[k] ? tp.out1 : tp.out0, off[k], F::pack(y));
+            // packQ: the values are arithmetic on the inputs and the host frequencies,
+            // which carry no foreign NaN payload (a NaN theta takes the scalar kernel)
+            __builtin_nontemporal_store(F::packQ(y), reinterpret_cast<v4u *>((second[k] ? out1 : out0) + off[k]));
         }
     }
 }
@@ -143,7 +143,7 @@ __global__ void __launch_bounds__(256)
         const size_t tok = th / n_heads;
         const double ang = double(pos[tok]) * freqOf(ft, int(j), int(d), theta);
         double sn, c;
-        sincos(ang, &sn, &c);
+        angleSinCos(ang, &sn, &c);
         const size_t base = th * d;
         const double A = F::get(in, base + j), B = F::get(in, base + j + half);
         F::put(out, base + j, float(A * c - B * sn));
@@ -153,24 +153,17 @@ __global__ void __launch_bounds__(256)
 
 template <typename T, int IPT>
 void launchIpt(int vph, const RopePair &tp, const int64_t *pos, size_t seq, size_t tpb,
-               uint32_t magic, const FreqTable &ft, hipStream_t s) {
+               uint32_t magic0, uint32_t magic1, const FreqTable &ft, hipStream_t s) {
     const unsigned grid = blocksFor(seq, tpb);
     switch (vph) {
-    case 2: ropeVec<T, IPT, 2><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
-    case 4: ropeVec<T, IPT, 4><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
-    case 8: ropeVec<T, IPT, 8><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
-    case 16: ropeVec<T, IPT, 16><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
-    case 32: ropeVec<T, IPT, 32><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic, ft); break;
+    case 2: ropeVec<T, IPT, 2><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
+    case 4: ropeVec<T, IPT, 4><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
+    case 8: ropeVec<T, IPT, 8><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
+    case 16: ropeVec<T, IPT, 16><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
+    case 32: ropeVec<T, IPT, 32><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
     default: break;
     }
 }
-
-// Items per block: about 256 (one 16-byte item per lane).  Measured on MI355X for the
-// Qwen2 shapes, 224-896 items per block are within 2 %, 128 is 15 % slower.  A persistent
-// variant (blocks looping over token groups with the next group's loads in flight) was
-// slower still: with one token per group the 64 f64 sincos ran on one wavefront while the
-// other three waited at the per-group barrier.
-constexpr size_t kItemsPerBlock = 256;
 
 template <typename T>
 bool launchVec(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, const FreqTable &ft,
@@ -186,24 +179,17 @@ bool launchVec(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, con
     if (vph > 32) return false; // a head row must fit in one wavefront
     const size_t per_tok = size_t(tp.n_heads0 + tp.n_heads1) * 2 * vph;
     if (per_tok == 0 || per_tok > size_t(256 * kMaxItems)) return false;
-    // Tokens per block: the fewest that keep >= 90 % of the lanes busy (q only: 4 tokens of
-    // 192 items = 3 full items per lane), else one block's worth of ~256 items.
-    size_t tpb = std::max<size_t>(1, kItemsPerBlock / per_tok);
-    for (size_t t = 1; t * per_tok <= size_t(256 * kMaxItems); ++t) {
-        const size_t slots = (t * per_tok + 255) / 256 * 256;
-        if (t * per_tok * 10 >= slots * 9) {
-            tpb = t;
-            break;
-        }
-    }
-    tpb = std::min(tpb, size_t(kLdsPairs) / half);
+    const size_t tpb = tokensPerBlock(per_tok, half, 256 * kMaxItems);
     const int ipt = int((tpb * per_tok + 255) / 256);
-    const uint32_t magic = uint32_t((uint64_t(1) << 32) / per_tok + 1);
+    const auto magicOf = [&](int heads) {
+        return heads ? uint32_t((uint64_t(1) << 32) / (size_t(heads) * 2 * vph) + 1) : 0u;
+    };
+    const uint32_t magic0 = magicOf(tp.n_heads0), magic1 = magicOf(tp.n_heads1);
     switch (ipt) {
-    case 1: launchIpt<T, 1>(int(vph), tp, pos, seq, tpb, magic, ft, s); break;
-    case 2: launchIpt<T, 2>(int(vph), tp, pos, seq, tpb, magic, ft, s); break;
-    case 3: launchIpt<T, 3>(int(vph), tp, pos, seq, tpb, magic, ft, s); break;
-    default: launchIpt<T, 4>(int(vph), tp, pos, seq, tpb, magic, ft, s); break;
+    case 1: launchIpt<T, 1>(int(vph), tp, pos, seq, tpb, magic0, magic1, ft, s); break;
+    case 2: launchIpt<T, 2>(int(vph), tp, pos, seq, tpb, magic0, magic1, ft, s); break;
+    case 3: launchIpt<T, 3>(int(vph), tp, pos, seq, tpb, magic0, magic1, ft, s); break;
+    default: launchIpt<T, 4>(int(vph), tp, pos, seq, tpb, magic0, magic1, ft, s); break;
     }
     return true;
 }
@@ -222,7 +208,9 @@ void launch(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, float 
             hipStream_t s) {
     if (seq == 0 || d == 0) return;
     const FreqTable ft = hostFreqs(d, theta);
-    if (launchVec<T>(tp, pos, seq, d, ft, s)) return;
+    // A NaN theta gives NaN frequencies carrying its payload, which the vector kernel's
+    // packQ would not round like the reference; the scalar kernel rounds exactly.
+    if (!std::isnan(theta) && launchVec<T>(tp, pos, seq, d, ft, s)) return;
     launchScalar<T>(tp.out0, tp.in0, pos, seq, size_t(tp.n_heads0), d, theta, ft, s);
     if (tp.n_heads1) launchScalar<T>(tp.out1, tp.in1, pos, seq, size_t(tp.n_heads1), d, theta, ft, s);
 }

@@ -10,7 +10,9 @@
 // 4 vectors per lane with a wider group beats fewer, fatter lanes (rms_norm 8192x1536:
 // 8.9 us with 64 lanes x 3 vectors vs 10.0 us with 16 lanes x 12; 16384x4096: 44.8 us with
 // 256 lanes x 2 vs 46.3 us with 64 x 8), so the plan takes the smallest group that keeps
-// each lane at <= 4 vectors, and only rows beyond 4096 vectors use 8 per lane.
+// each lane at <= 4 vectors -- up to 256 lanes.  A 1024-lane group (one row per block,
+// 16 waves joined through LDS) comes last: INT8 quantize of 1536x8960 ran 8.8 us with
+// 256 lanes x 5 vectors against 11.1 us with 1024 x 2.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,10 +35,14 @@ inline RowPlan planRow(size_t nvec) {
     // Short rows (a 128-wide KV head) still get 16 lanes, so one load instruction of a
     // group covers 256 contiguous bytes instead of 64.
     const size_t min_g = nvec < 16 ? nvec : 16;
+    const auto fits = [&](int g, int v) {
+        return size_t(g) >= min_g && (nvec + size_t(g) - 1) / size_t(g) <= size_t(v);
+    };
     for (int v : kRowVmax)
         for (int g : kRowGroups)
-            if (size_t(g) >= min_g && (nvec + size_t(g) - 1) / size_t(g) <= size_t(v))
-                return {g, v};
+            if (g <= 256 && fits(g, v)) return {g, v};
+    for (int v : kRowVmax)
+        if (fits(1024, v)) return {1024, v};
     return {};
 }
 
@@ -68,6 +74,16 @@ void withPlan(const RowPlan &p, F &&f) {
     default: break;
     }
 }
+
+// Unsigned division by a launch constant d >= 1 without a divide sequence: with
+// m = ceil(2^64 / d) = (2^64 + e) / d, 0 <= e < d, floor(i * m / 2^64) = floor(i / d)
+// whenever i * e < 2^64, which holds for every i < 2^64 / d (any index into a buffer).
+struct DivU64 {
+    uint64_t m = 0; // 0 encodes d == 1
+    DivU64() = default;
+    explicit DivU64(uint64_t d) : m(d <= 1 ? 0 : ~uint64_t(0) / d + 1) {}
+    __device__ uint64_t div(uint64_t i) const { return m == 0 ? i : __umul64hi(i, m); }
+};
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

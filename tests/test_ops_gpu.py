@@ -533,3 +533,136 @@ def test_rope_kv_append_equals_composition(dt, seq, nq, nk, d, pos0, max_seq, th
     L.Ops.argmax(i, m, dev(logits, L.DataType.BF16))
     assert i.numpy()[0] == oracle.argmax(logits)[0]
     no_device_error()
+
+
+# ---- INT8 boundary rows (division-free quotient, packed absmax) ----------------------------
+
+def quant_edge_rows(dt, cols=256, seed=5):
+    """Rows that reach every branch of the quantizer: zero, NaN (quiet, signalling, with
+    low payload bits), +-inf, scales below / around the 2^-96 exact-division threshold,
+    subnormals, exact half-integer ties on a power-of-two scale, signed zeros, the largest
+    finite value, and random +-1 ulp near-ties."""
+    rng = np.random.default_rng(seed)
+    f32 = lambda u: np.array(u, np.uint32).view(np.float32)
+    rows = []
+    base = rng.standard_normal(cols).astype(np.float32)
+    rows.append(np.zeros(cols, np.float32))
+    r = base.copy(); r[[3, 100]] = np.nan; rows.append(r)
+    r = base.copy(); r[5] = np.inf; rows.append(r)
+    r = base.copy(); r[7] = -np.inf; r[9] = np.nan; rows.append(r)
+    rows.append(base * np.float32(1e-30))                        # scale < 2^-96: IEEE path
+    thr = np.float32(127.0) * np.float32(2.0 ** -96)
+    for k in (-2, -1, 0, 1, 2):                                  # amax around the threshold
+        r = base / np.abs(base).max() * thr
+        r[0] = np.nextafter(thr, np.float32(np.inf if k > 0 else 0), dtype=np.float32) if k else thr
+        if abs(k) == 2:
+            r[0] = np.nextafter(r[0], np.float32(np.inf if k > 0 else 0), dtype=np.float32)
+        rows.append(r.astype(np.float32))
+    rows.append(base * np.float32(1e-39))                        # f32 subnormals
+    s = np.float32(2.0 ** -3)
+    ties = (np.arange(cols) % 254 - 127 + 0.5).astype(np.float32) * s
+    ties[0] = 127 * s; rows.append(np.clip(ties, -127 * s, 127 * s))
+    r = base.copy(); r[::2] = 0.0; r[1::4] = -0.0; rows.append(r)
+    r = base.copy(); r[11] = np.finfo(np.float32).max; rows.append(r)
+    amax = np.float32(3.0); sc = amax / np.float32(127.0)
+    k = rng.integers(-126, 126, cols).astype(np.float32)
+    near = ((k + np.float32(0.5)) * sc).astype(np.float32)
+    near = np.where(rng.random(cols) < 0.5, np.nextafter(near, np.float32(0)), np.nextafter(near, np.float32(9)))
+    near[0] = amax; rows.append(near.astype(np.float32))
+    x = np.stack(rows).astype(np.float32)
+    if dt == "f32":
+        x[1, 50] = f32(0x7FC01234)   # quiet NaN with low payload bits
+        x[1, 51] = f32(0xFF812345)   # signalling NaN, negative
+        return x
+    if dt == "bf16":
+        b = f32_to_bf16(x)
+        b[1, 50], b[1, 51], b[3, 52] = 0x7F81, 0xFFC1, 0x7F80  # sNaN, -qNaN, +inf
+        b[-4, 11] = 0x7F7F                                     # largest finite bf16
+        return b
+    with np.errstate(over="ignore"):
+        h = x.astype(np.float16)
+    hv = h.view(np.uint16)
+    hv[1, 50], hv[1, 51] = 0x7C01, 0xFE00                       # sNaN, -qNaN
+    hv[-4, 11] = 0x7BFF                                         # largest finite f16
+    return h
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+def test_quantize_boundary_rows(dt):
+    x = quant_edge_rows(dt)
+    q, s = empty(x.shape, L.DataType.I8), empty(x.shape[:-1], L.DataType.F32)
+    L.Ops.quantize_int8(q, s, dev(x, DTS[dt]))
+    eq, es = oracle.quantize_int8(x)
+    assert_exact(q.numpy(), eq, "codes")
+    assert_exact(s.numpy(), es, "scales")
+    # KV append (same kernel, pointed into a cache) and the dequantized read
+    rows, cols = x.shape
+    kv = x.reshape(rows, 1, cols)
+    cq, cs = dev(np.zeros((rows + 3, 1, cols), np.int8)), dev(np.zeros((rows + 3, 1), np.float32))
+    L.Ops.kv_append_int8(cq, cs, dev(kv, DTS[dt]), 2)
+    assert_exact(cq.numpy()[2:2 + rows, 0], eq, "kv codes")
+    assert_exact(cs.numpy()[2:2 + rows, 0], es, "kv scales")
+    out = empty(x.shape, DTS[dt])
+    L.Ops.dequantize_int8(out, q, s)
+    assert_exact(out.numpy(), oracle.dequantize_int8(eq, es, x.dtype), "dequant")
+    no_device_error()
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_dequantize_caller_scales_with_nan_payloads(dt):
+    """Scales are caller data: NaN scales with payload bits (and infinities) must round
+    like the reference's rule, which the hardware bf16 converter alone would not."""
+    rng = np.random.default_rng(8)
+    rows, cols = 64, 512
+    q = rng.integers(-127, 128, (rows, cols)).astype(np.int8)
+    s = (rng.random(rows).astype(np.float32) + np.float32(0.5)) * np.float32(0.01)
+    bits = s.view(np.uint32)
+    bits[3], bits[10], bits[11] = 0x7FC01234, 0xFF800001, 0x7F800000
+    bits[12] = 0x7FFFFFFF
+    out = empty((rows, cols), DTS[dt])
+    L.Ops.dequantize_int8(out, dev(q), dev(s))
+    assert_exact(out.numpy(), oracle.dequantize_int8(q, s, np.uint16 if dt == "bf16" else np.float16))
+
+
+def test_rms_norm_nan_eps_matches_oracle_nan_pattern():
+    rng = np.random.default_rng(9)
+    x, w = sample(rng, (16, 1536), "bf16"), sample(rng, (1536,), "bf16", 0.1, 1.0)
+    out = empty(x.shape, L.DataType.BF16)
+    L.Ops.rms_norm(out, dev(x, L.DataType.BF16), dev(w, L.DataType.BF16), float("nan"))
+    got = bf16_to_f32(out.numpy())
+    ref = bf16_to_f32(oracle.rms_norm(x, w, float("nan")))
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.isnan(ref).all()
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32", "f16"])
+def test_rope_kv_append_boundary_rows(dt):
+    """NaN / inf / tiny / zero k and v rows through the fused op equal the composition and
+    the oracle's codes."""
+    rows = quant_edge_rows(dt, cols=128)
+    seq = rows.shape[0]
+    rng = np.random.default_rng(10)
+    T = DTS[dt]
+    q = sample(rng, (seq, 12, 128), dt)
+    k = np.stack([rows, rows[::-1]], axis=1)          # [seq, 2, 128]
+    v = np.stack([rows[::-1], rows], axis=1)
+    pos = np.arange(seq, dtype=np.int64) * 977
+    tq, tk, tv, tp = dev(q, T), dev(k, T), dev(v, T), dev(pos)
+    caches = lambda: (dev(np.zeros((seq, 2, 128), np.int8)), dev(np.zeros((seq, 2), np.float32)),
+                      dev(np.zeros((seq, 2, 128), np.int8)), dev(np.zeros((seq, 2), np.float32)))
+    kc, ks, vc, vs = caches()
+    qo = empty(q.shape, T)
+    L.Ops.rope_kv_append_int8(qo, tq, tk, tv, tp, 1e4, kc, ks, vc, vs, 0)
+    kc2, ks2, vc2, vs2 = caches()
+    qo2, ko2 = empty(q.shape, T), empty(k.shape, T)
+    L.Ops.rope_qk(qo2, tq, ko2, tk, tp, 1e4)
+    L.Ops.kv_append_int8(kc2, ks2, ko2, 0)
+    L.Ops.kv_append_int8(vc2, vs2, tv, 0)
+    for a, b, what in ((qo, qo2, "q"), (kc, kc2, "k codes"), (ks, ks2, "k scales"),
+                       (vc, vc2, "v codes"), (vs, vs2, "v scales")):
+        assert_exact(a.numpy(), b.numpy(), what)
+    eq, es = oracle.quantize_int8(v.reshape(seq * 2, 128))
+    assert_exact(vc.numpy().reshape(seq * 2, 128), eq, "v codes vs oracle")
+    assert_exact(vs.numpy().reshape(seq * 2), es, "v scales vs oracle")
+    eq, es = oracle.quantize_int8(ko2.numpy().reshape(seq * 2, 128))
+    assert_exact(kc.numpy().reshape(seq * 2, 128), eq, "k codes vs oracle")
+    no_device_error()
