@@ -5,16 +5,30 @@
 // freq_j, and the pair (x_j, x_{j+d/2}) is rotated in double precision; the result is
 // rounded double -> float -> element type.  freq_j is computed on the host with the same
 // libm pow the reference calls, so the angles are bit-identical; cos/sin come from
-// sincos.hpp (within an ulp of glibc's, which the final float rounding absorbs).
+// sincos.hpp (within an ulp of glibc's, which the final float rounding absorbs).  The
+// wave kernel forms x*c +- p*s as one f64 product and one f64 fma (the reference rounds
+// both products); the double results differ by at most an ulp, which the rounding to
+// float absorbs except within 2^-29 of a float tie.
 //
-// Design: HBM-bound.  A 256-thread block owns a run of tokens.  Each lane first issues the
-// 16-byte loads of its items, then the block computes the (cos, sin) pairs of its tokens
-// into LDS -- d/2 per token, shared by every q and k head -- while the loads are in
-// flight; after the barrier each lane rotates and stores its items.  The kernel stays at
-// <= 64 VGPRs for the common shapes (8 waves per SIMD): the trig is the ~40-instruction
-// routine of sincos.hpp, the device library only on an out-of-line rare path.  Loads and
-// stores are non-temporal (read once, written once).  q and k of the same tokens go
-// through one launch.
+// Design: HBM-bound, no MFMA (no contraction).  Two kernels:
+//  * ropeWave (most shapes): one wavefront per token, no block barrier.  The wave issues
+//    the 16-byte loads of all the token's q and k head rows, computes the token's d/2
+//    (cos, sin) pairs (one per lane) into its own LDS slice while they are in flight, and
+//    each lane then keeps the pairs of its column in registers for every head row.
+//  * ropeVec (few rows per token, e.g. k alone): a 256-thread block owns a run of tokens,
+//    computes their pairs into LDS behind a block barrier and rotates items that read
+//    their pairs from LDS; it packs several tokens into a block, so lanes stay busy.
+// The trig is the ~40-instruction routine of sincos.hpp, the device library only on an
+// out-of-line rare path.  Loads and stores are non-temporal (read once, written once).
+// q and k of the same tokens go through one launch.
+//
+// Measured on MI355X (rocprof kernel durations, same run): q+k of Qwen2 at 8192 tokens
+// 13.2 us with ropeWave vs 13.5 with ropeVec; q alone 12.2 vs 12.8; Llama-8B q+k at
+// 16384 tokens 58.4 vs 62.5.  A pure copy with the same access pattern takes 11.7 us
+// (q+k), so the f64 rotation (about 100 f32-op equivalents per 16-byte item, f64 ops
+// and f32<->f64 conversions issuing at half the f32 rate) costs 1.5 us.  Tried and
+// slower: a persistent double-buffered block loop (18.7-25.8 us), 8 waves/SIMD by
+// register cap (spills, 40 us).
 #include "common.hpp"
 #include "launch.hpp"
 #include "rope_common.hpp"
@@ -128,6 +142,103 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// One wavefront per token, no block barrier.  Lane l of the wave computes angle j = l
+// (and l + 64, ... when d/2 > 64) of its token into the wave's own LDS slice, then reads
+// back the N (cos, sin) pairs of its vector column into registers and uses them for every
+// head row of the token: a row is kRowVec consecutive lanes, so a wave instruction covers
+// 64 / kRowVec rows (q rows first, then k rows) and the lane's column is the same in all
+// of them.  Rows are taken in passes of IPT wave instructions.  Waves past the last token
+// redo the last token and store nothing, so no wave leaves before the loads (a branch
+// there would serialise the kernel-argument loads ahead of the first global load).
+template <typename T, int IPT, int VPH>
+__global__ void __launch_bounds__(256)
+    ropeWave(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int passes, FreqTable ft) {
+    using F = Fmt<T>;
+    constexpr int N = F::kVec;
+    constexpr int kRowVec = 2 * VPH;          // lanes per head row
+    constexpr int kRows = kWave / kRowVec;    // rows per wave instruction
+    constexpr int kHalf = VPH * N;
+    constexpr int kRowBytes = kRowVec * 16;
+    __shared__ double2 cs[256 / kWave][kHalf];
+
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = int(threadIdx.x) % kWave;
+    const size_t t0 = size_t(blockIdx.x) * (256 / kWave) + size_t(wave);
+    const bool live = t0 < seq;                // waves past the end redo the last token
+    const size_t t = live ? t0 : seq - 1;      // and store nothing
+    const int nh0 = tp.n_heads0, rows = nh0 + tp.n_heads1;
+    const int rlane = lane / kRowVec, v_lane = lane % kRowVec;
+    const int jv = v_lane & (VPH - 1);
+    const bool lower = v_lane < VPH;
+    const char *in0 = static_cast<const char *>(tp.in0) + t * size_t(nh0) * kRowBytes + v_lane * 16;
+    const char *in1 = static_cast<const char *>(tp.in1) + t * size_t(tp.n_heads1) * kRowBytes + v_lane * 16 -
+                      size_t(nh0) * kRowBytes;
+    char *out0 = static_cast<char *>(tp.out0) + t * size_t(nh0) * kRowBytes + v_lane * 16;
+    char *out1 = static_cast<char *>(tp.out1) + t * size_t(tp.n_heads1) * kRowBytes + v_lane * 16 -
+                 size_t(nh0) * kRowBytes;
+
+    double c[N], sn[N];
+    int pass = 0;
+    do {
+        v4u raw[IPT];
+#pragma unroll
+        for (int k = 0; k < IPT; ++k) {
+            const int r = (pass * IPT + k) * kRows + rlane;
+            const char *src = (r < nh0 ? in0 : (r < rows ? in1 : in0 - size_t(r) * kRowBytes)) + size_t(r) * kRowBytes;
+            raw[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
+        }
+        if (pass == 0) {
+            const int64_t p = pos[t];
+            bool far = false;
+            for (int j = lane; j < kHalf; j += kWave) {
+                const double ang = double(p) * ft.f[j];
+                double s0 = 0.0, c0 = 0.0;
+                if (fabs(ang) <= kSincosFastLimit)
+                    sincosReduced(ang, &s0, &c0);
+                else
+                    far = true; // also NaN
+                cs[wave][j] = make_double2(c0, s0);
+            }
+            if (__builtin_expect(__any(far), 0)) {
+                for (int j = lane; j < kHalf; j += kWave) {
+                    const double ang = double(p) * ft.f[j];
+                    if (!(fabs(ang) <= kSincosFastLimit)) {
+                        double s0, c0;
+                        librarySinCos(ang, &s0, &c0);
+                        cs[wave][j] = make_double2(c0, s0);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int e = 0; e < N; ++e) {
+                const double2 v = cs[wave][jv * N + e];
+                c[e] = v.x;
+                sn[e] = lower ? -v.y : v.y; // first half: x*c - partner*s
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < IPT; ++k) {
+            v4u other;
+            other.x = partnerOf<VPH>(raw[k].x);
+            other.y = partnerOf<VPH>(raw[k].y);
+            other.z = partnerOf<VPH>(raw[k].z);
+            other.w = partnerOf<VPH>(raw[k].w);
+            const int r = (pass * IPT + k) * kRows + rlane;
+            if (live && r < rows) {
+                float x[N], q[N], y[N];
+                F::unpack(raw[k], x);
+                F::unpack(other, q);
+#pragma unroll
+                for (int e = 0; e < N; ++e) y[e] = float(fma(double(q[e]), sn[e], double(x[e]) * c[e]));
+                __builtin_nontemporal_store(F::packQ(y), reinterpret_cast<v4u *>((r < nh0 ? out0 : out1) + size_t(r) * kRowBytes));
+            }
+        }
+    } while (++pass < passes);
+}
+
 // Any head_dim / alignment: one thread per (token, head, j) pair of one tensor.
 template <typename T>
 __global__ void __launch_bounds__(256)
@@ -148,6 +259,33 @@ __global__ void __launch_bounds__(256)
         const double A = F::get(in, base + j), B = F::get(in, base + j + half);
         F::put(out, base + j, float(A * c - B * sn));
         F::put(out, base + j + half, float(B * c + A * sn));
+    }
+}
+
+template <typename T, int IPT>
+void launchWaveIpt(int vph, int passes, const RopePair &tp, const int64_t *pos, size_t seq,
+                   const FreqTable &ft, hipStream_t s) {
+    const unsigned grid = blocksFor(seq, 256 / kWave);
+    switch (vph) {
+    case 2: ropeWave<T, IPT, 2><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
+    case 4: ropeWave<T, IPT, 4><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
+    case 8: ropeWave<T, IPT, 8><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
+    case 16: ropeWave<T, IPT, 16><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
+    case 32: ropeWave<T, IPT, 32><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
+    default: break;
+    }
+}
+
+// `instr` wave instructions per token, taken in passes of at most 4 (registers).
+template <typename T>
+void launchWave(int vph, int instr, const RopePair &tp, const int64_t *pos, size_t seq,
+                const FreqTable &ft, hipStream_t s) {
+    const int passes = (instr + 3) / 4, ipt = (instr + passes - 1) / passes;
+    switch (ipt) {
+    case 1: launchWaveIpt<T, 1>(vph, passes, tp, pos, seq, ft, s); break;
+    case 2: launchWaveIpt<T, 2>(vph, passes, tp, pos, seq, ft, s); break;
+    case 3: launchWaveIpt<T, 3>(vph, passes, tp, pos, seq, ft, s); break;
+    default: launchWaveIpt<T, 4>(vph, passes, tp, pos, seq, ft, s); break;
     }
 }
 
@@ -185,6 +323,15 @@ bool launchVec(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, con
         return heads ? uint32_t((uint64_t(1) << 32) / (size_t(heads) * 2 * vph) + 1) : 0u;
     };
     const uint32_t magic0 = magicOf(tp.n_heads0), magic1 = magicOf(tp.n_heads1);
+    // One wave per token when its instructions keep >= 3/4 of the lanes busy (q+k of Qwen2:
+    // 14 of 16 rows, q alone and Llama-8B q+k: all); a launch of few rows per token (k
+    // alone) packs several tokens per block with ropeVec instead.
+    const int rpi = int(kWave / (2 * vph));
+    const int instr = int((size_t(tp.n_heads0 + tp.n_heads1) + rpi - 1) / rpi);
+    if (size_t(tp.n_heads0 + tp.n_heads1) * 4 >= size_t(instr) * rpi * 3) {
+        launchWave<T>(int(vph), instr, tp, pos, seq, ft, s);
+        return true;
+    }
     switch (ipt) {
     case 1: launchIpt<T, 1>(int(vph), tp, pos, seq, tpb, magic0, magic1, ft, s); break;
     case 2: launchIpt<T, 2>(int(vph), tp, pos, seq, tpb, magic0, magic1, ft, s); break;
