@@ -319,6 +319,16 @@ def config_ops(L, rng):
         O.dequantize_int8(dk[i % skv], ckq[i % skv], cks[i % skv])
         O.dequantize_int8(dv[i % skv], cvq[i % skv], cvs[i % skv])
 
+    def append_pair(i):
+        j = i % skv
+        O.kv_append_int8_pair(ckq[j], cks[j], cvq[j], cvs[j], kv_k[j], kv_v[j], 0)
+
+    def read_pair(i):
+        j = i % skv
+        O.dequantize_int8_pair(dk[j], ckq[j], cks[j], dv[j], cvq[j], cvs[j])
+
+    cases.append(("config3", "KV append k+v [32768,2,128] (pair, 1 launch)", kvb, 1, append_pair))
+    cases.append(("config3", "KV dequant read k+v [32768,2,128] (pair, 1 launch)", kvb, 1, read_pair))
     cases.append(("config3", "KV append k+v [32768,2,128] (2 launches)", kvb, 2, append))
     cases.append(("config3", "KV dequant read k+v [32768,2,128] (2 launches)", kvb, 2, read))
     return cases, P

@@ -95,6 +95,20 @@ __C {
      * cache_scale [max_seq, n_kvh] (F32).  Requires pos + n_tok <= max_seq. */
     __export void llaisysKVAppendInt8(llaisysTensor_t cache_q, llaisysTensor_t cache_scale,
                                       llaisysTensor_t kv, size_t pos);
+    /* The k and v cache appends of one decoder step (the reference updates both caches,
+     * src/models/qwen2/attention.hpp:108-123) in one launch: equal to
+     * llaisysKVAppendInt8(k_cache, k_scale, k, pos) followed by
+     * llaisysKVAppendInt8(v_cache, v_scale, v, pos); k and v share dtype and head_dim. */
+    __export void llaisysKVAppendInt8Pair(llaisysTensor_t k_cache, llaisysTensor_t k_scale,
+                                          llaisysTensor_t v_cache, llaisysTensor_t v_scale,
+                                          llaisysTensor_t k, llaisysTensor_t v, size_t pos);
+    /* Two dequantizations in one launch (the k and v slices of an INT8 cache read for
+     * attention, src/models/qwen2/attention.hpp:70-73): equal to
+     * llaisysDequantizeInt8(out0, q0, scale0) followed by llaisysDequantizeInt8(out1, q1,
+     * scale1); the outputs share dtype and last dimension. */
+    __export void llaisysDequantizeInt8Pair(llaisysTensor_t out0, llaisysTensor_t q0,
+                                            llaisysTensor_t scale0, llaisysTensor_t out1,
+                                            llaisysTensor_t q1, llaisysTensor_t scale1);
 }
 
 #endif /* LLAISYS_OPS_H */

@@ -169,6 +169,17 @@ __C {
                              llaisysTensor_t kv, size_t pos) {
         llaisys::ops::kvAppendInt8(cache_q->tensor, cache_scale->tensor, kv->tensor, pos);
     }
+    void llaisysKVAppendInt8Pair(llaisysTensor_t k_cache, llaisysTensor_t k_scale,
+                                 llaisysTensor_t v_cache, llaisysTensor_t v_scale,
+                                 llaisysTensor_t k, llaisysTensor_t v, size_t pos) {
+        llaisys::ops::kvAppendInt8Pair(k_cache->tensor, k_scale->tensor, v_cache->tensor,
+                                       v_scale->tensor, k->tensor, v->tensor, pos);
+    }
+    void llaisysDequantizeInt8Pair(llaisysTensor_t out0, llaisysTensor_t q0, llaisysTensor_t scale0,
+                                   llaisysTensor_t out1, llaisysTensor_t q1, llaisysTensor_t scale1) {
+        llaisys::ops::dequantizeInt8Pair(out0->tensor, q0->tensor, scale0->tensor, out1->tensor,
+                                         q1->tensor, scale1->tensor);
+    }
 
     // ---- model API: out of scope, exported so the reference ctypes loader binds --------
     struct LlaisysQwen2Model *llaisysQwen2ModelCreate(const struct LlaisysQwen2Meta *,

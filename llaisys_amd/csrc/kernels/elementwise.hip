@@ -134,13 +134,31 @@ __device__ __forceinline__ void loadCodes(const int8_t *q, size_t i, float *f) {
     }
 }
 
+// Up to two dequantizations with the same row length and type in one launch (k and v of a
+// cache read): blocks [0, nb0) take job 0, the rest job 1.
+struct DequantJob {
+    void *out;
+    const int8_t *q;
+    const float *scale;
+    size_t nvec;
+};
+struct DequantJobs {
+    DequantJob job[2];
+    unsigned nb0;
+};
+
 template <typename T, int kU>
 __global__ void __launch_bounds__(256)
-    dequantVec(void *__restrict__ out, const int8_t *__restrict__ q,
-               const float *__restrict__ scale, size_t nvec, DivU64 rowdiv) {
+    dequantVec(DequantJobs jobs, DivU64 rowdiv) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
-    const size_t first = size_t(blockIdx.x) * 256 * kU + threadIdx.x;
+    const bool second = blockIdx.x >= jobs.nb0; // block-uniform
+    void *__restrict__ out = second ? jobs.job[1].out : jobs.job[0].out;
+    const int8_t *__restrict__ q = second ? jobs.job[1].q : jobs.job[0].q;
+    const float *__restrict__ scale = second ? jobs.job[1].scale : jobs.job[0].scale;
+    const size_t nvec = second ? jobs.job[1].nvec : jobs.job[0].nvec;
+    const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
+    const size_t first = size_t(blk) * 256 * kU + threadIdx.x;
 #pragma unroll
     for (int k = 0; k < kU; ++k) {
         const size_t i = first + size_t(k) * 256;
@@ -165,20 +183,36 @@ __global__ void __launch_bounds__(256)
         F::put(out, i, float(q[i]) * scale[i / cols]);
 }
 
+struct DequantArgs {
+    void *out;
+    const int8_t *q;
+    const float *scale;
+    size_t rows;
+};
+
 template <typename T>
-void launchDequant(void *out, const int8_t *q, const float *scale, size_t rows, size_t cols,
-                   hipStream_t s) {
-    const size_t n = rows * cols;
-    if (n == 0) return;
+void launchDequant(const DequantArgs &a0, const DequantArgs &a1, size_t cols, hipStream_t s) {
     constexpr int N = Fmt<T>::kVec;
-    const size_t code_align = reinterpret_cast<uintptr_t>(q) % N;
-    if (cols % N == 0 && aligned16(out) && code_align == 0) {
-        const size_t nvec = n / N;
-        dequantVec<T, kDequantU><<<blocksFor(nvec, 256 * kDequantU), 256, 0, s>>>(out, q, scale, nvec, DivU64(cols / N));
+    constexpr size_t kPerBlock = size_t(256) * kDequantU;
+    const auto vecOk = [&](const DequantArgs &a) {
+        return a.rows == 0 || (aligned16(a.out) && reinterpret_cast<uintptr_t>(a.q) % N == 0);
+    };
+    const size_t nv0 = cols % N == 0 ? a0.rows * cols / N : 0;
+    const size_t nv1 = cols % N == 0 ? a1.rows * cols / N : 0;
+    const size_t nb0 = (nv0 + kPerBlock - 1) / kPerBlock, nb1 = (nv1 + kPerBlock - 1) / kPerBlock;
+    if (cols % N == 0 && vecOk(a0) && vecOk(a1) && nb0 + nb1 < (size_t(1) << 31)) {
+        if (nb0 + nb1 == 0) return;
+        const DequantJobs jobs{{DequantJob{a0.out, a0.q, a0.scale, nv0}, DequantJob{a1.out, a1.q, a1.scale, nv1}},
+                               unsigned(nb0)};
+        dequantVec<T, kDequantU><<<unsigned(nb0 + nb1), 256, 0, s>>>(jobs, DivU64(cols / N));
         return;
     }
-    const unsigned grid = unsigned(std::min<size_t>(blocksFor(n, 256), 1u << 20));
-    dequantScalar<T><<<grid, 256, 0, s>>>(out, q, scale, n, cols);
+    for (const DequantArgs *a : {&a0, &a1}) {
+        const size_t n = a->rows * cols;
+        if (n == 0) continue;
+        const unsigned grid = unsigned(std::min<size_t>(blocksFor(n, 256), 1u << 20));
+        dequantScalar<T><<<grid, 256, 0, s>>>(a->out, a->q, a->scale, n, cols);
+    }
 }
 
 } // namespace
@@ -192,14 +226,21 @@ void add(void *c, const void *a, const void *b, size_t n, llaisysDataType_t dt, 
     dispatchBinary<AddOp>(c, a, b, n, dt, s);
 }
 
-void dequantizeInt8(void *out, const int8_t *q, const float *scale, size_t rows, size_t cols,
-                    llaisysDataType_t dt, hipStream_t s) {
+void dequantizeInt8Pair(void *out0, const int8_t *q0, const float *scale0, size_t rows0,
+                        void *out1, const int8_t *q1, const float *scale1, size_t rows1,
+                        size_t cols, llaisysDataType_t dt, hipStream_t s) {
+    const DequantArgs a0{out0, q0, scale0, rows0}, a1{out1, q1, scale1, rows1};
     switch (dt) {
-    case LLAISYS_DTYPE_F32: return launchDequant<F32>(out, q, scale, rows, cols, s);
-    case LLAISYS_DTYPE_BF16: return launchDequant<BF16>(out, q, scale, rows, cols, s);
-    case LLAISYS_DTYPE_F16: return launchDequant<F16>(out, q, scale, rows, cols, s);
+    case LLAISYS_DTYPE_F32: return launchDequant<F32>(a0, a1, cols, s);
+    case LLAISYS_DTYPE_BF16: return launchDequant<BF16>(a0, a1, cols, s);
+    case LLAISYS_DTYPE_F16: return launchDequant<F16>(a0, a1, cols, s);
     default: return;
     }
+}
+
+void dequantizeInt8(void *out, const int8_t *q, const float *scale, size_t rows, size_t cols,
+                    llaisysDataType_t dt, hipStream_t s) {
+    dequantizeInt8Pair(out, q, scale, rows, nullptr, nullptr, nullptr, 0, cols, dt, s);
 }
 
 } // namespace llaisys::kernels

@@ -71,8 +71,18 @@ void argmax(void *idx, bool idx_i64, void *val, const void *vals, size_t n,
 void quantizeInt8(int8_t *q, float *scale, const void *in, size_t rows, size_t cols,
                   llaisysDataType_t dt, hipStream_t stream);
 
+// Two quantizations of rows of the same length and type in one launch (rows1 may be 0).
+void quantizeInt8Pair(int8_t *q0, float *scale0, const void *in0, size_t rows0, int8_t *q1,
+                      float *scale1, const void *in1, size_t rows1, size_t cols,
+                      llaisysDataType_t dt, hipStream_t stream);
+
 // out = T(float(q) * scale[row]).
 void dequantizeInt8(void *out, const int8_t *q, const float *scale, size_t rows, size_t cols,
                     llaisysDataType_t dt, hipStream_t stream);
+
+// Two dequantizations of rows of the same length and type in one launch (rows1 may be 0).
+void dequantizeInt8Pair(void *out0, const int8_t *q0, const float *scale0, size_t rows0,
+                        void *out1, const int8_t *q1, const float *scale1, size_t rows1,
+                        size_t cols, llaisysDataType_t dt, hipStream_t stream);
 
 } // namespace llaisys::kernels

@@ -12,29 +12,50 @@
 // division-free correctly rounded quotient of quantize.hpp, ~7 VALU operations per bf16
 // element in all; codes are written as 8-byte (bf16/f16 input) or 4-byte (f32) stores per lane and
 // the scale by the group's first lane.  A KV-cache append is this kernel pointed at the
-// cache rows pos .. pos + n_tok, so the codes go straight into the cache.
+// cache rows pos .. pos + n_tok, so the codes go straight into the cache; k and v of an
+// append go through one launch (two jobs), which saves a launch's fixed cost of about
+// 2 us (fill, first-load latency, drain) on a 25 MB job.
 #include "common.hpp"
 #include "launch.hpp"
 #include "quantize.hpp"
 #include "rowplan.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace llaisys::kernels {
 
 namespace {
 
+// Up to two quantizations of rows of the same length and type in one launch (k and v of a
+// KV append): blocks [0, nb0) take job 0, the rest job 1.
+struct QuantJob {
+    int8_t *q;
+    float *scale;
+    const void *in;
+    size_t rows;
+};
+struct QuantJobs {
+    QuantJob job[2];
+    unsigned nb0;
+};
+
 template <typename T, int G, int VMAX>
 __global__ void __launch_bounds__(blockFor<G>())
-    quantRows(int8_t *__restrict__ q, float *__restrict__ scale, const void *__restrict__ in,
-              size_t rows, int cols) {
+    quantRows(QuantJobs jobs, int cols) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
     constexpr int kBlock = blockFor<G>();
     __shared__ float red[kBlock / kWave];
 
+    const bool second = blockIdx.x >= jobs.nb0; // block-uniform
+    int8_t *__restrict__ q = second ? jobs.job[1].q : jobs.job[0].q;
+    float *__restrict__ scale = second ? jobs.job[1].scale : jobs.job[0].scale;
+    const void *__restrict__ in = second ? jobs.job[1].in : jobs.job[0].in;
+    const size_t rows = second ? jobs.job[1].rows : jobs.job[0].rows;
+    const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
     const int lane = threadIdx.x % G;
-    const size_t row = size_t(blockIdx.x) * (kBlock / G) + threadIdx.x / G;
+    const size_t row = size_t(blk) * (kBlock / G) + threadIdx.x / G;
     const bool live = row < rows;
     const int nvec = cols / N;
     const size_t base = row * size_t(cols);
@@ -108,33 +129,62 @@ __global__ void __launch_bounds__(256)
 }
 
 template <typename T>
-void launch(int8_t *q, float *scale, const void *in, size_t rows, size_t cols, hipStream_t s) {
-    if (rows == 0) return;
+void launch(const QuantJob &j0, const QuantJob &j1, size_t cols, hipStream_t s) {
     constexpr int N = Fmt<T>::kVec;
-    const bool vec = cols > 0 && cols % N == 0 && cols <= size_t(INT32_MAX) && aligned16(in) &&
-                     reinterpret_cast<uintptr_t>(q) % N == 0;
+    const auto vecOk = [&](const QuantJob &j) {
+        return j.rows == 0 || (aligned16(j.in) && reinterpret_cast<uintptr_t>(j.q) % N == 0);
+    };
+    const bool vec = cols > 0 && cols % N == 0 && cols <= size_t(INT32_MAX) && vecOk(j0) && vecOk(j1);
     RowPlan plan = vec ? planRow(cols / N) : RowPlan{};
     bool done = false;
     withPlan(plan, [&](auto g, auto v) {
         constexpr int G = decltype(g)::value, V = decltype(v)::value;
         constexpr int kBlock = blockFor<G>();
-        quantRows<T, G, V><<<blocksFor(rows, kBlock / G), kBlock, 0, s>>>(q, scale, in, rows,
-                                                                          int(cols));
+        const unsigned nb0 = blocksFor(j0.rows, kBlock / G), nb1 = blocksFor(j1.rows, kBlock / G);
+        if (nb0 + nb1 == 0) return;
+        quantRows<T, G, V><<<nb0 + nb1, kBlock, 0, s>>>(QuantJobs{{j0, j1}, nb0}, int(cols));
         done = true;
     });
-    if (!done) quantRowsScalar<T><<<unsigned(rows), 256, 0, s>>>(q, scale, in, rows, cols);
+    if (done) return;
+    for (const QuantJob *j : {&j0, &j1})
+        if (j->rows)
+            quantRowsScalar<T><<<unsigned(j->rows), 256, 0, s>>>(j->q, j->scale, j->in, j->rows, cols);
+}
+
+template <typename T>
+void launchAny(const QuantJob &j0, const QuantJob &j1, size_t cols, hipStream_t s) {
+    // a job too large for the block index space is split; real KV / weight shapes never are
+    constexpr size_t kMaxRows = size_t(1) << 30;
+    if (j0.rows > kMaxRows || j1.rows > kMaxRows) {
+        for (const QuantJob *j : {&j0, &j1})
+            for (size_t r = 0; r < j->rows; r += kMaxRows) {
+                const QuantJob part{j->q + r * cols, j->scale + r,
+                                    static_cast<const char *>(j->in) + r * cols * Fmt<T>::kBytes,
+                                    std::min(kMaxRows, j->rows - r)};
+                launch<T>(part, QuantJob{}, cols, s);
+            }
+        return;
+    }
+    launch<T>(j0, j1, cols, s);
 }
 
 } // namespace
 
-void quantizeInt8(int8_t *q, float *scale, const void *in, size_t rows, size_t cols,
-                  llaisysDataType_t dt, hipStream_t s) {
+void quantizeInt8Pair(int8_t *q0, float *scale0, const void *in0, size_t rows0, int8_t *q1,
+                      float *scale1, const void *in1, size_t rows1, size_t cols,
+                      llaisysDataType_t dt, hipStream_t s) {
+    const QuantJob j0{q0, scale0, in0, rows0}, j1{q1, scale1, in1, rows1};
     switch (dt) {
-    case LLAISYS_DTYPE_F32: return launch<F32>(q, scale, in, rows, cols, s);
-    case LLAISYS_DTYPE_BF16: return launch<BF16>(q, scale, in, rows, cols, s);
-    case LLAISYS_DTYPE_F16: return launch<F16>(q, scale, in, rows, cols, s);
+    case LLAISYS_DTYPE_F32: return launchAny<F32>(j0, j1, cols, s);
+    case LLAISYS_DTYPE_BF16: return launchAny<BF16>(j0, j1, cols, s);
+    case LLAISYS_DTYPE_F16: return launchAny<F16>(j0, j1, cols, s);
     default: return;
     }
+}
+
+void quantizeInt8(int8_t *q, float *scale, const void *in, size_t rows, size_t cols,
+                  llaisysDataType_t dt, hipStream_t s) {
+    quantizeInt8Pair(q, scale, in, rows, nullptr, nullptr, nullptr, 0, cols, dt, s);
 }
 
 } // namespace llaisys::kernels

@@ -246,28 +246,77 @@ void dequantizeInt8(tensor_t out, tensor_t q, tensor_t scale) {
     launched("dequantizeInt8");
 }
 
-// Replaces the f32 cache-row copy of src/models/qwen2/attention.hpp:108-123.
-void kvAppendInt8(tensor_t cache_q, tensor_t cache_scale, tensor_t kv, size_t pos) {
+namespace {
+// Checks of one INT8 KV append; returns the first cache row, pos * n_kvh.
+size_t checkKvAppend(const tensor_t &cache_q, const tensor_t &cache_scale, const tensor_t &kv,
+                     size_t pos, const char *op) {
     CHECK_SAME_DEVICE(cache_q, cache_scale, kv);
     ASSERT(cache_q->isContiguous() && cache_scale->isContiguous() && kv->isContiguous(),
-           "KVAppendInt8: tensors must be contiguous");
-    ASSERT(cache_q->dtype() == LLAISYS_DTYPE_I8, "KVAppendInt8: cache codes must be INT8");
-    ASSERT(cache_scale->dtype() == LLAISYS_DTYPE_F32, "KVAppendInt8: cache scales must be F32");
+           op << ": tensors must be contiguous");
+    ASSERT(cache_q->dtype() == LLAISYS_DTYPE_I8, op << ": cache codes must be INT8");
+    ASSERT(cache_scale->dtype() == LLAISYS_DTYPE_F32, op << ": cache scales must be F32");
     requireFloat(kv->dtype());
     ASSERT(cache_q->ndim() == 3 && kv->ndim() == 3 && cache_scale->ndim() == 2,
-           "KVAppendInt8: cache [max_seq, n_kvh, d], scales [max_seq, n_kvh], kv [n_tok, n_kvh, d]");
+           op << ": cache [max_seq, n_kvh, d], scales [max_seq, n_kvh], kv [n_tok, n_kvh, d]");
     const size_t max_seq = cache_q->shape()[0], nkvh = cache_q->shape()[1], d = cache_q->shape()[2];
     const size_t ntok = kv->shape()[0];
-    ASSERT(kv->shape()[1] == nkvh && kv->shape()[2] == d, "KVAppendInt8: kv head shape mismatch");
+    ASSERT(kv->shape()[1] == nkvh && kv->shape()[2] == d, op << ": kv head shape mismatch");
     ASSERT(cache_scale->shape()[0] == max_seq && cache_scale->shape()[1] == nkvh,
-           "KVAppendInt8: scale cache shape mismatch");
-    ASSERT(pos <= max_seq && ntok <= max_seq - pos, "KVAppendInt8: append past the cache end");
+           op << ": scale cache shape mismatch");
+    ASSERT(pos <= max_seq && ntok <= max_seq - pos, op << ": append past the cache end");
+    return pos * nkvh;
+}
+} // namespace
+
+// Replaces the f32 cache-row copy of src/models/qwen2/attention.hpp:108-123.
+void kvAppendInt8(tensor_t cache_q, tensor_t cache_scale, tensor_t kv, size_t pos) {
+    const size_t r0 = checkKvAppend(cache_q, cache_scale, kv, pos, "KVAppendInt8");
     auto s = streamFor(kv);
-    const size_t r0 = pos * nkvh;
+    const size_t d = kv->shape()[2];
     kernels::quantizeInt8(reinterpret_cast<int8_t *>(cache_q->data()) + r0 * d,
                           reinterpret_cast<float *>(cache_scale->data()) + r0, kv->data(),
-                          ntok * nkvh, d, kv->dtype(), s);
+                          kv->numel() / (d ? d : 1), d, kv->dtype(), s);
     launched("quantizeInt8");
+}
+
+// The k and v appends of one decoder step (attention.hpp:108-123 updates both caches) in
+// one launch; equal to kvAppendInt8(k_cache, k_scale, k, pos) then
+// kvAppendInt8(v_cache, v_scale, v, pos).
+void kvAppendInt8Pair(tensor_t k_cache, tensor_t k_scale, tensor_t v_cache, tensor_t v_scale,
+                      tensor_t k, tensor_t v, size_t pos) {
+    const size_t rk = checkKvAppend(k_cache, k_scale, k, pos, "KVAppendInt8Pair");
+    const size_t rv = checkKvAppend(v_cache, v_scale, v, pos, "KVAppendInt8Pair");
+    CHECK_SAME_DEVICE(k, v);
+    CHECK_SAME_DTYPE(k->dtype(), v->dtype());
+    ASSERT(k->shape()[2] == v->shape()[2], "KVAppendInt8Pair: k and v must share head_dim");
+    auto s = streamFor(k);
+    const size_t d = k->shape()[2], div = d ? d : 1;
+    kernels::quantizeInt8Pair(reinterpret_cast<int8_t *>(k_cache->data()) + rk * d,
+                              reinterpret_cast<float *>(k_scale->data()) + rk, k->data(),
+                              k->numel() / div, reinterpret_cast<int8_t *>(v_cache->data()) + rv * d,
+                              reinterpret_cast<float *>(v_scale->data()) + rv, v->data(),
+                              v->numel() / div, d, k->dtype(), s);
+    launched("quantizeInt8Pair");
+}
+
+// Two dequantizations in one launch (e.g. the k and v slices of an INT8 cache); equal to
+// dequantizeInt8(out0, q0, scale0) then dequantizeInt8(out1, q1, scale1).
+void dequantizeInt8Pair(tensor_t out0, tensor_t q0, tensor_t scale0, tensor_t out1, tensor_t q1,
+                        tensor_t scale1) {
+    checkQuantPair(q0, scale0, out0, "DequantizeInt8Pair");
+    checkQuantPair(q1, scale1, out1, "DequantizeInt8Pair");
+    CHECK_SAME_DEVICE(out0, out1);
+    CHECK_SAME_DTYPE(out0->dtype(), out1->dtype());
+    const size_t cols = lastDim(out0);
+    ASSERT(lastDim(out1) == cols, "DequantizeInt8Pair: outputs must share the last dimension");
+    auto s = streamFor(out0);
+    kernels::dequantizeInt8Pair(out0->data(), reinterpret_cast<const int8_t *>(q0->data()),
+                                reinterpret_cast<const float *>(scale0->data()),
+                                cols ? out0->numel() / cols : 0, out1->data(),
+                                reinterpret_cast<const int8_t *>(q1->data()),
+                                reinterpret_cast<const float *>(scale1->data()),
+                                cols ? out1->numel() / cols : 0, cols, out0->dtype(), s);
+    launched("dequantizeInt8Pair");
 }
 
 } // namespace llaisys::ops

@@ -19,6 +19,10 @@ void swiglu(tensor_t out, tensor_t gate, tensor_t up);
 void quantizeInt8(tensor_t q, tensor_t scale, tensor_t in);
 void dequantizeInt8(tensor_t out, tensor_t q, tensor_t scale);
 void kvAppendInt8(tensor_t cache_q, tensor_t cache_scale, tensor_t kv, size_t pos);
+void kvAppendInt8Pair(tensor_t k_cache, tensor_t k_scale, tensor_t v_cache, tensor_t v_scale,
+                      tensor_t k, tensor_t v, size_t pos);
+void dequantizeInt8Pair(tensor_t out0, tensor_t q0, tensor_t scale0, tensor_t out1, tensor_t q1,
+                        tensor_t scale1);
 void ropeKvAppendInt8(tensor_t q_out, tensor_t q_in, tensor_t k_in, tensor_t v_in,
                       tensor_t pos_ids, float theta, tensor_t k_cache, tensor_t k_scale,
                       tensor_t v_cache, tensor_t v_scale, size_t pos);

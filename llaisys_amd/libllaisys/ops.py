@@ -30,6 +30,8 @@ ADDED_OPS = {
     "llaisysQuantizeInt8": [T, T, T],
     "llaisysDequantizeInt8": [T, T, T],
     "llaisysKVAppendInt8": [T, T, T, c_size_t],
+    "llaisysKVAppendInt8Pair": [T, T, T, T, T, T, c_size_t],
+    "llaisysDequantizeInt8Pair": [T, T, T, T, T, T],
 }
 
 

@@ -91,3 +91,17 @@ class Ops:
     def kv_append_int8(cache_q: Tensor, cache_scale: Tensor, kv: Tensor, pos: int):
         LIB_LLAISYS.llaisysKVAppendInt8(cache_q.lib_tensor(), cache_scale.lib_tensor(),
                                         kv.lib_tensor(), c_size_t(pos))
+
+    @staticmethod
+    def kv_append_int8_pair(k_cache: Tensor, k_scale: Tensor, v_cache: Tensor, v_scale: Tensor,
+                            k: Tensor, v: Tensor, pos: int):
+        LIB_LLAISYS.llaisysKVAppendInt8Pair(k_cache.lib_tensor(), k_scale.lib_tensor(),
+                                            v_cache.lib_tensor(), v_scale.lib_tensor(),
+                                            k.lib_tensor(), v.lib_tensor(), c_size_t(pos))
+
+    @staticmethod
+    def dequantize_int8_pair(out0: Tensor, q0: Tensor, scale0: Tensor, out1: Tensor, q1: Tensor,
+                             scale1: Tensor):
+        LIB_LLAISYS.llaisysDequantizeInt8Pair(out0.lib_tensor(), q0.lib_tensor(),
+                                              scale0.lib_tensor(), out1.lib_tensor(),
+                                              q1.lib_tensor(), scale1.lib_tensor())

@@ -380,6 +380,62 @@ def test_kv_append(dt):
     assert_exact(out.numpy(), oracle.dequantize_int8(host_q, host_s, np.uint16 if dt == "bf16" else np.float32))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("pos, ntok", [(0, 2048), (5000, 1), (31000, 1768)])
+def test_kv_append_pair_equals_two_appends(dt, pos, ntok):
+    """llaisysKVAppendInt8Pair: one launch for k and v, bit-identical to two
+    llaisysKVAppendInt8 calls and to the oracle, rows outside pos .. pos+ntok untouched;
+    then llaisysDequantizeInt8Pair of both caches against two single dequantizations."""
+    rng = np.random.default_rng(pos + ntok)
+    max_seq, nkvh, d = 32768, 2, 128
+    k = with_outliers(rng, (ntok, nkvh, d), dt, 1.0)
+    v = with_outliers(rng, (ntok, nkvh, d), dt, 1.0)
+    k[0, 1] = 0  # an all-zero (token, head) row
+    fill_q, fill_s = np.full((max_seq, nkvh, d), 7, np.int8), np.full((max_seq, nkvh), -1.0, np.float32)
+    kc, ks, vc, vs = dev(fill_q), dev(fill_s), dev(fill_q), dev(fill_s)
+    L.Ops.kv_append_int8_pair(kc, ks, vc, vs, dev(k, DTS[dt]), dev(v, DTS[dt]), pos)
+    hk_q, hk_s, hv_q, hv_s = fill_q.copy(), fill_s.copy(), fill_q.copy(), fill_s.copy()
+    assert oracle.kv_append_int8(hk_q, hk_s, k, pos) == 0
+    assert oracle.kv_append_int8(hv_q, hv_s, v, pos) == 0
+    assert_exact(kc.numpy(), hk_q, "k codes")
+    assert_exact(ks.numpy(), hk_s, "k scales")
+    assert_exact(vc.numpy(), hv_q, "v codes")
+    assert_exact(vs.numpy(), hv_s, "v scales")
+    # the single-tensor entry point writes the same bytes
+    kc1, ks1 = dev(fill_q), dev(fill_s)
+    L.Ops.kv_append_int8(kc1, ks1, dev(k, DTS[dt]), pos)
+    assert_exact(kc1.numpy(), kc.numpy(), "pair vs single codes")
+    assert_exact(ks1.numpy(), ks.numpy(), "pair vs single scales")
+    # paired dequantized read of the appended rows of both caches
+    sl = lambda t: t.slice(0, pos, pos + ntok)
+    ko, vo = empty((ntok, nkvh, d), DTS[dt]), empty((ntok, nkvh, d), DTS[dt])
+    L.Ops.dequantize_int8_pair(ko, sl(kc), sl(ks), vo, sl(vc), sl(vs))
+    et = np.uint16 if dt == "bf16" else (np.float16 if dt == "f16" else np.float32)
+    assert_exact(ko.numpy(), oracle.dequantize_int8(hk_q[pos:pos + ntok], hk_s[pos:pos + ntok], et), "k read")
+    assert_exact(vo.numpy(), oracle.dequantize_int8(hv_q[pos:pos + ntok], hv_s[pos:pos + ntok], et), "v read")
+
+
+def test_quant_pairs_unaligned_and_empty():
+    """Pair entry points on shapes the vector kernels do not take (odd rows, an odd byte
+    offset) and with an empty second job."""
+    rng = np.random.default_rng(5)
+    a = with_outliers(rng, (9, 3, 7), "bf16", 1.0)
+    b = with_outliers(rng, (9, 3, 7), "bf16", 1.0)
+    qa, sa = empty((20, 3, 7), L.DataType.I8), empty((20, 3), L.DataType.F32)
+    qb, sb = empty((20, 3, 7), L.DataType.I8), empty((20, 3), L.DataType.F32)
+    L.Ops.kv_append_int8_pair(qa, sa, qb, sb, dev(a, L.DataType.BF16), dev(b, L.DataType.BF16), 3)
+    for q, s, x in ((qa, sa, a), (qb, sb, b)):
+        eq, es = oracle.quantize_int8(x.reshape(-1, 7))
+        assert_exact(q.numpy()[3:12].reshape(-1, 7), eq)
+        assert_exact(s.numpy()[3:12].reshape(-1), es)
+    # empty second job, and outputs that start at an odd element
+    oa, ob = empty((9, 3, 7), L.DataType.BF16), empty((0, 3, 7), L.DataType.BF16)
+    qz, sz = empty((0, 3, 7), L.DataType.I8), empty((0, 3), L.DataType.F32)
+    L.Ops.dequantize_int8_pair(oa, qa.slice(0, 3, 12), sa.slice(0, 3, 12), ob, qz, sz)
+    eq, es = oracle.quantize_int8(a.reshape(-1, 7))
+    assert_exact(oa.numpy().reshape(-1, 7), oracle.dequantize_int8(eq, es, np.uint16))
+
+
 # ---- config-size properties ----------------------------------------------------------------
 
 def test_config2_shapes_properties():
