@@ -142,8 +142,8 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// One wavefront per token, no block barrier.  Lane l of the wave computes angle j = l
-// (and l + 64, ... when d/2 > 64) of its token into the wave's own LDS slice, then reads
+// One wavefront per token, no block barrier.  Each lane computes one (cos, sin) pair (two
+// or more when d/2 > 64) of its token into the wave's own LDS slice, then reads
 // back the N (cos, sin) pairs of its vector column into registers and uses them for every
 // head row of the token: a row is kRowVec consecutive lanes, so a wave instruction covers
 // 64 / kRowVec rows (q rows first, then k rows) and the lane's column is the same in all
@@ -159,7 +159,12 @@ __global__ void __launch_bounds__(256)
     constexpr int kRows = kWave / kRowVec;    // rows per wave instruction
     constexpr int kHalf = VPH * N;
     constexpr int kRowBytes = kRowVec * 16;
+    // (cos, sin) of angle j = jv * N + e sits in slot e * VPH + jv, and lane l computes the
+    // angle of slot l: both the write and every read instruction (same e, consecutive jv)
+    // touch consecutive 16-byte slots, with no LDS bank conflicts (slots N * 16 bytes apart
+    // had shown 4 % of the kernel's time in bank conflicts)
     __shared__ double2 cs[256 / kWave][kHalf];
+    const auto angleOf = [](int slot) { return (slot % VPH) * N + slot / VPH; };
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
@@ -190,22 +195,23 @@ __global__ void __launch_bounds__(256)
         if (pass == 0) {
             const int64_t p = pos[t];
             bool far = false;
-            for (int j = lane; j < kHalf; j += kWave) {
+            for (int sl = lane; sl < kHalf; sl += kWave) {
+                const int j = angleOf(sl);
                 const double ang = double(p) * ft.f[j];
                 double s0 = 0.0, c0 = 0.0;
                 if (fabs(ang) <= kSincosFastLimit)
                     sincosReduced(ang, &s0, &c0);
                 else
                     far = true; // also NaN
-                cs[wave][j] = make_double2(c0, s0);
+                cs[wave][sl] = make_double2(c0, s0);
             }
             if (__builtin_expect(__any(far), 0)) {
-                for (int j = lane; j < kHalf; j += kWave) {
-                    const double ang = double(p) * ft.f[j];
+                for (int sl = lane; sl < kHalf; sl += kWave) {
+                    const double ang = double(p) * ft.f[angleOf(sl)];
                     if (!(fabs(ang) <= kSincosFastLimit)) {
                         double s0, c0;
                         librarySinCos(ang, &s0, &c0);
-                        cs[wave][j] = make_double2(c0, s0);
+                        cs[wave][sl] = make_double2(c0, s0);
                     }
                 }
             }
@@ -214,7 +220,7 @@ __global__ void __launch_bounds__(256)
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
             for (int e = 0; e < N; ++e) {
-                const double2 v = cs[wave][jv * N + e];
+                const double2 v = cs[wave][e * VPH + jv];
                 c[e] = v.x;
                 sn[e] = lower ? -v.y : v.y; // first half: x*c - partner*s
             }
