@@ -43,11 +43,13 @@ def lib():
             "orc_quantize_int8": [P, P, P, c_size_t, c_size_t, c_int],
             "orc_dequantize_int8": [P, P, P, c_size_t, c_size_t, c_int],
             "orc_kv_append_int8": [P, P, c_size_t, P, c_size_t, c_size_t, c_size_t, c_size_t, c_int],
+            "orc_self_attention": [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t, c_size_t,
+                                   c_size_t, c_float, c_int],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = c_int if name in ("orc_embedding", "orc_kv_append_int8") else None
+            fn.restype = c_int if name in ("orc_embedding", "orc_kv_append_int8", "orc_self_attention") else None
         for name in ("orc_f32_to_bf16", "orc_f32_to_f16"):
             getattr(L, name).argtypes = [c_float]
             getattr(L, name).restype = ctypes.c_uint16
@@ -166,3 +168,26 @@ def kv_append_int8(cache_q, cache_scale, kv, pos):
     max_seq, nkvh, d = cache_q.shape
     return lib().orc_kv_append_int8(_p(cache_q), _p(cache_scale), max_seq, _p(kv), kv.shape[0],
                                     nkvh, d, pos, _code(kv))
+
+
+def self_attention(q, k, v, scale):
+    """Reference self_attention (self_attention_cpu.cpp:13-115): q [seq, nh, d],
+    k [total, nkvh, d], v [total, nkvh, dv] of one dtype; returns [seq, nh, dv]."""
+    q, k, v = _c(q), _c(k), _c(v)
+    assert q.dtype == k.dtype == v.dtype
+    seq, nh, d = q.shape
+    total, nkvh, dv = v.shape
+    assert k.shape == (total, nkvh, d)
+    out = np.empty((seq, nh, dv), dtype=q.dtype)
+    rc = lib().orc_self_attention(_p(out), _p(q), _p(k), _p(v), seq, total, nh, nkvh, d, dv,
+                                  float(scale), _code(q))
+    assert rc == 0, "invalid head split"
+    return out
+
+
+def self_attention_int8kv(q, k_codes, k_scale, v_codes, v_scale, scale):
+    """Attention over an INT8 cache: self_attention of q with k and v dequantized into
+    q's element type (the composition llaisysDequantizeInt8 then llaisysSelfAttention)."""
+    k = dequantize_int8(k_codes, k_scale, q.dtype)
+    v = dequantize_int8(v_codes, v_scale, q.dtype)
+    return self_attention(q, k, v, scale)

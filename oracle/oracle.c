@@ -10,9 +10,11 @@
  * -ffp-contract=off keeps every multiply and add separately rounded, as in the
  * reference's g++ -std=c++17 build on x86-64.
  *
- * Pinning (tests/test_oracle.py): rms_norm, rope, swiglu, add, embedding, argmax and the
- * bf16/f16 conversions are compared bit-for-bit with golden vectors written by the
- * compiled reference library (tests/golden/); the INT8 functions and the fused
+ * Pinning (tests/test_oracle.py): rms_norm, rope, swiglu, add, embedding, argmax,
+ * self_attention and the bf16/f16 conversions are compared bit-for-bit with golden vectors
+ * written by the compiled reference library (tests/golden/) and with that library on
+ * random shapes; self_attention also against a textbook f64 evaluation and closed forms
+ * (one key, equal keys, causality, the GQA head mapping); the INT8 functions and the fused
  * add+rms_norm have no reference counterpart and are pinned by closed-form checks
  * (codes of exact scale multiples, +-127 at the row's absmax, round-half-even ties,
  * zero rows, and add+rms_norm == add then rms_norm of the reference goldens).
@@ -20,6 +22,7 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ---- scalar conversions: src/utils/types.cpp:6-84 ---------------------------------- */
@@ -286,5 +289,58 @@ int orc_kv_append_int8(int8_t *cache_q, float *cache_scale, size_t max_seq, cons
     if (pos > max_seq || n_tok > max_seq - pos) return -1;
     size_t r0 = pos * n_kvh;
     orc_quantize_int8(cache_q + r0 * d, cache_scale + r0, kv, n_tok * n_kvh, d, dt);
+    return 0;
+}
+
+/* ---- self_attention: src/ops/self_attention/cpu/self_attention_cpu.cpp:13-115 ---------
+ * q [seq, nh, d], k [total, nkvh, d], v [total, nkvh, dv], out [seq, nh, dv], nh a
+ * multiple of nkvh; q head h reads kv head h / (nh / nkvh).  Per (head, query):
+ * scores[t] = (sequential f32 sum of q*k) * scale (:76-92); the query sits at
+ * current_pos = total - seq + i in size_t arithmetic (:95, so seq > total wraps and masks
+ * nothing); keys t > current_pos get -inf, max over all scores (:101-108); -inf scores
+ * become 0, the rest expf(s - max), summed left to right (:110-118); each divided by the
+ * sum (:120-122); out[dv] = sequential f32 sum of p * v, rounded to the element type
+ * (:127-140).  Returns -1 (nothing written) on a zero nkvh or nh % nkvh != 0. */
+int orc_self_attention(void *out, const void *q, const void *k, const void *v, size_t seq,
+                       size_t total, size_t nh, size_t nkvh, size_t d, size_t dv, float scale,
+                       int dt) {
+    if (nkvh == 0 || nh % nkvh != 0) return -1;
+    const size_t group = nh / nkvh;
+    float *scores = (float *)malloc((total ? total : 1) * sizeof(float));
+    if (!scores) return -1;
+    for (size_t h = 0; h < nh; h++) {
+        const size_t kvh = h / group;
+        for (size_t i = 0; i < seq; i++) {
+            const size_t qo = i * nh * d + h * d;
+            for (size_t t = 0; t < total; t++) {
+                const size_t ko = t * nkvh * d + kvh * d;
+                float dot = 0.0f;
+                for (size_t e = 0; e < d; e++) dot += ld(q, qo + e, dt) * ld(k, ko + e, dt);
+                scores[t] = dot * scale;
+            }
+            const size_t cur = total - seq + i;
+            float mx = -INFINITY;
+            for (size_t t = 0; t < total; t++) {
+                if (t > cur) scores[t] = -INFINITY;
+                if (scores[t] > mx) mx = scores[t];
+            }
+            float sum = 0.0f;
+            for (size_t t = 0; t < total; t++) {
+                if (scores[t] == -INFINITY)
+                    scores[t] = 0.0f;
+                else
+                    scores[t] = expf(scores[t] - mx);
+                sum += scores[t];
+            }
+            for (size_t t = 0; t < total; t++) scores[t] /= sum;
+            const size_t oo = i * nh * dv + h * dv;
+            for (size_t e = 0; e < dv; e++) {
+                float val = 0.0f;
+                for (size_t t = 0; t < total; t++) val += scores[t] * ld(v, t * nkvh * dv + kvh * dv + e, dt);
+                st(out, oo + e, dt, val);
+            }
+        }
+    }
+    free(scores);
     return 0;
 }

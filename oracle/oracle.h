@@ -49,4 +49,9 @@ void orc_dequantize_int8(void *out, const int8_t *q, const float *scale, size_t 
 int orc_kv_append_int8(int8_t *cache_q, float *cache_scale, size_t max_seq, const void *kv,
                        size_t n_tok, size_t n_kvh, size_t head_dim, size_t pos, int dtype);
 
+/* self_attention_cpu.cpp:13-115; -1 on an invalid head split */
+int orc_self_attention(void *out, const void *q, const void *k, const void *v, size_t seq,
+                       size_t total, size_t nh, size_t nkvh, size_t d, size_t dv, float scale,
+                       int dtype);
+
 #endif

@@ -147,6 +147,32 @@ def main():
             key = f"embedding/{dt}/{idt.name}"
             g.update({f"{key}/w": w, f"{key}/idx": idx, f"{key}/out": out.numpy()})
 
+    # self_attention: the reference test shapes (test/ops/self_attention.py: qlen, kvlen, nh,
+    # nkvh, hd = (2,2,1,1,4), (5,11,4,2,8)), a Qwen2-1.5B GQA decode row and prefill block
+    # (12 q heads on 2 kv heads, head_dim 128), a single key, and seq_len > total_len (the
+    # reference's size_t current_pos wraps, so the early queries see every key).  Seeds are
+    # their own sequence, so the cases above keep their values.
+    sa_seed = [0]
+
+    def sa_rng():
+        sa_seed[0] += 1
+        return np.random.default_rng(5000 + sa_seed[0])
+
+    for dt in ("f32", "bf16", "f16"):
+        for ql, kl, nh, nkvh, hd in ((2, 2, 1, 1, 4), (5, 11, 4, 2, 8), (1, 37, 12, 2, 128),
+                                     (16, 16, 12, 2, 128), (4, 1, 2, 1, 8), (3, 2, 2, 1, 8)):
+            r = sa_rng()
+            q = sample(r, (ql, nh, hd), dt)
+            k = sample(r, (kl, nkvh, hd), dt)
+            v = sample(r, (kl, nkvh, hd), dt)
+            scale = np.float32(1.0 / hd ** 0.5)
+            out = R.empty((ql, nh, hd), DT[dt])
+            lib.llaisysSelfAttention(out.lib_tensor(), R.h(q, DT[dt]), R.h(k, DT[dt]), R.h(v, DT[dt]),
+                                     ctypes.c_float(scale))
+            key = f"self_attention/{dt}/{ql}x{kl}x{nh}x{nkvh}x{hd}"
+            g.update({f"{key}/q": q, f"{key}/k": k, f"{key}/v": v, f"{key}/scale": scale,
+                      f"{key}/out": out.numpy()})
+
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT} ({OUT.stat().st_size / 1e6:.2f} MB, {len(g)} arrays)")
 

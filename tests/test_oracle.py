@@ -109,6 +109,16 @@ def test_random_shapes_match_reference(ref, seed):
         theta = float(rng.choice([1e4, 5e5, 1e6]))
         (y,) = _ref_call(ref, "llaisysROPE", [(q.shape, dt)], [(q, dt), (pos, DataType.I64)], ctypes.c_float(theta))
         assert_exact(oracle.rope(q, pos, theta), y, "rope")
+        nkvh = int(rng.integers(1, 3))
+        nh, hd = nkvh * int(rng.integers(1, 4)), int(rng.integers(1, 40))
+        ql, kl = int(rng.integers(1, 7)), int(rng.integers(1, 30))
+        qa = conv(rng.standard_normal((ql, nh, hd)).astype(np.float32))
+        ka = conv(rng.standard_normal((kl, nkvh, hd)).astype(np.float32))
+        va = conv(rng.standard_normal((kl, nkvh, hd)).astype(np.float32))
+        sc = float(1.0 / np.sqrt(hd))
+        (y,) = _ref_call(ref, "llaisysSelfAttention", [((ql, nh, hd), dt)], [(qa, dt), (ka, dt), (va, dt)],
+                         ctypes.c_float(sc))
+        assert_exact(oracle.self_attention(qa, ka, va, sc), y, "self_attention")
 
 
 # ---- 3. closed forms -------------------------------------------------------------------
@@ -289,3 +299,102 @@ def test_embedding_out_of_range():
     assert st == -1 and np.array_equal(out[0], w[1])
     _, st = oracle.embedding(np.array([-1], np.int32), w)
     assert st == -1
+
+
+# ---- self_attention ------------------------------------------------------------------
+
+def test_golden_self_attention(golden):
+    n = 0
+    for (op, dt, case), c in golden.items():
+        if op == "self_attention":
+            got = oracle.self_attention(c["q"], c["k"], c["v"], float(c["scale"]))
+            assert_exact(got, c["out"], f"{dt} {case}")
+            n += 1
+    assert n == 18
+
+
+def _f32(a):
+    return bf16_to_f32(a) if a.dtype == np.uint16 else a.astype(np.float32)
+
+
+def _attention_f64(q, k, v, scale):
+    """Textbook causal GQA attention in f64 (the query at total - seq + i sees keys <= it)."""
+    q, k, v = _f32(q).astype(np.float64), _f32(k).astype(np.float64), _f32(v).astype(np.float64)
+    seq, nh, d = q.shape
+    total, nkvh, _ = k.shape
+    g = nh // nkvh
+    out = np.zeros((seq, nh, v.shape[2]))
+    for h in range(nh):
+        for i in range(seq):
+            cur = total - seq + i
+            vis = total if cur < 0 else min(cur + 1, total)
+            s = k[:vis, h // g] @ q[i, h] * scale
+            p = np.exp(s - s.max())
+            out[i, h] = (p / p.sum()) @ v[:vis, h // g]
+    return out
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_self_attention_against_f64(dt):
+    # GQA, causal offset total - seq, against the textbook formula in f64
+    rng = np.random.default_rng(3)
+    mk = lambda shape: f32_to_bf16(rng.standard_normal(shape).astype(np.float32)) if dt == "bf16" \
+        else rng.standard_normal(shape).astype(np.float32)
+    q, k, v = mk((7, 6, 16)), mk((19, 2, 16)), mk((19, 2, 16))
+    got = _f32(oracle.self_attention(q, k, v, 0.25))
+    exp = _attention_f64(q, k, v, 0.25)
+    tol = 1e-5 if dt == "f32" else 2 ** -7
+    assert np.abs(got - exp).max() <= tol * np.abs(exp).max()
+
+
+def test_self_attention_closed_forms():
+    rng = np.random.default_rng(4)
+    # one key: softmax is exactly 1, the output is exactly v[0] of the head's kv head
+    q = rng.standard_normal((3, 4, 8)).astype(np.float32)
+    k = rng.standard_normal((1, 2, 8)).astype(np.float32)
+    v = rng.standard_normal((1, 2, 8)).astype(np.float32)
+    out = oracle.self_attention(q, k, v, 0.3)
+    for h in range(4):
+        assert np.array_equal(out[:, h], np.broadcast_to(v[0, h // 2], (3, 8)))
+    # equal keys: uniform weights over the visible keys -> prefix means of v
+    total, seq = 9, 4
+    k = np.ones((total, 1, 8), np.float32)
+    v = rng.standard_normal((total, 1, 8)).astype(np.float32)
+    q = rng.standard_normal((seq, 1, 8)).astype(np.float32)
+    out = oracle.self_attention(q, k, v, 1.0)
+    for i in range(seq):
+        vis = total - seq + i + 1
+        assert np.allclose(out[i, 0], v[:vis, 0].mean(0), rtol=1e-6, atol=1e-6)
+    # causality: keys and values after a query's position do not change its output
+    q = rng.standard_normal((5, 2, 8)).astype(np.float32)
+    k = rng.standard_normal((12, 1, 8)).astype(np.float32)
+    v = rng.standard_normal((12, 1, 8)).astype(np.float32)
+    base = oracle.self_attention(q, k, v, 0.5)
+    k2, v2 = k.copy(), v.copy()
+    k2[9:] = 100.0
+    v2[9:] = -100.0
+    moved = oracle.self_attention(q, k2, v2, 0.5)
+    assert np.array_equal(base[:2], moved[:2])      # queries at 7, 8 see keys 0..8 only
+    assert not np.array_equal(base[2:], moved[2:])  # later queries see the changed keys
+    # GQA mapping: q head h uses kv head h // (nh / nkvh), as a run with that head alone
+    q = rng.standard_normal((3, 6, 8)).astype(np.float32)
+    k = rng.standard_normal((10, 2, 8)).astype(np.float32)
+    v = rng.standard_normal((10, 2, 8)).astype(np.float32)
+    full = oracle.self_attention(q, k, v, 0.4)
+    for h in range(6):
+        one = oracle.self_attention(q[:, h:h + 1].copy(), k[:, h // 3:h // 3 + 1].copy(),
+                                    v[:, h // 3:h // 3 + 1].copy(), 0.4)
+        assert np.array_equal(full[:, h], one[:, 0])
+
+
+def test_self_attention_int8kv_is_the_composition():
+    rng = np.random.default_rng(6)
+    q = f32_to_bf16(rng.standard_normal((4, 6, 16)).astype(np.float32))
+    k = f32_to_bf16(rng.standard_normal((10, 2, 16)).astype(np.float32))
+    v = f32_to_bf16(rng.standard_normal((10, 2, 16)).astype(np.float32))
+    kq, ks = oracle.quantize_int8(k)
+    vq, vs = oracle.quantize_int8(v)
+    got = oracle.self_attention_int8kv(q, kq, ks, vq, vs, 0.25)
+    exp = oracle.self_attention(q, oracle.dequantize_int8(kq, ks, np.uint16),
+                                oracle.dequantize_int8(vq, vs, np.uint16), 0.25)
+    assert_exact(got, exp)
