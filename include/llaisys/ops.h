@@ -7,10 +7,10 @@
  * (src/utils/check.hpp:7-88).  On LLAISYS_DEVICE_AMD every op is one or two asynchronous
  * HIP kernel launches on the context stream (llaisysGetContextStream).
  *
- * Scope of this library: the bandwidth-bound per-layer ops.  llaisysLinear,
- * llaisysRearrange and llaisysSelfAttention are exported so that the reference's ctypes
- * loader binds, and raise "Unimplemented function" (the reference's own rearrange is a
- * stub, src/ops/rearrange/op.cpp:4-6).  Ops on CPU tensors raise "Unsupported device":
+ * Scope of this library: the bandwidth-bound per-layer ops and the attention that reads
+ * their INT8 KV cache.  llaisysLinear and llaisysRearrange are exported so that the
+ * reference's ctypes loader binds, and raise "Unimplemented function" (the reference's own
+ * rearrange is a stub, src/ops/rearrange/op.cpp:4-6).  Ops on CPU tensors raise "Unsupported device":
  * this library has no CPU compute path.
  */
 #ifndef LLAISYS_OPS_H
@@ -39,7 +39,10 @@ __C {
     /* reference ops.h:13 -- rotate-half RoPE on [seq, n_heads, head_dim], pos_ids I64 */
     __export void llaisysROPE(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t pos_ids,
                               float theta);
-    /* reference ops.h:14 -- out of scope here: raises "Unimplemented function" */
+    /* reference ops.h:14 -- causal GQA attention (src/ops/self_attention/op.cpp:19-45,
+     * cpu/self_attention_cpu.cpp:13-115): q [seq, nh, d], k [total, nkvh, d],
+     * v [total, nkvh, dv], attn_val [seq, nh, dv], one dtype; query i sees keys
+     * t <= total - seq + i; f32 softmax of (q . k) * scale. */
     __export void llaisysSelfAttention(llaisysTensor_t attn_val, llaisysTensor_t q,
                                        llaisysTensor_t k, llaisysTensor_t v, float scale);
     /* reference ops.h:15 -- out = up * gate / (1 + exp(-gate)) */
@@ -109,6 +112,15 @@ __C {
     __export void llaisysDequantizeInt8Pair(llaisysTensor_t out0, llaisysTensor_t q0,
                                             llaisysTensor_t scale0, llaisysTensor_t out1,
                                             llaisysTensor_t q1, llaisysTensor_t scale1);
+    /* llaisysSelfAttention over an INT8 KV cache (the reference decoder's attention over
+     * its cache slice, src/models/qwen2/attention.hpp:70-73, with the cache of
+     * llaisysKVAppendInt8): k_codes [total, nkvh, d] and v_codes [total, nkvh, dv] I8,
+     * k_scale / v_scale [total, nkvh] F32.  Equal to llaisysDequantizeInt8 of both caches
+     * into q's dtype followed by llaisysSelfAttention; the caches are read as codes. */
+    __export void llaisysSelfAttentionInt8KV(llaisysTensor_t attn_val, llaisysTensor_t q,
+                                             llaisysTensor_t k_codes, llaisysTensor_t k_scale,
+                                             llaisysTensor_t v_codes, llaisysTensor_t v_scale,
+                                             float scale);
 }
 
 #endif /* LLAISYS_OPS_H */

@@ -131,9 +131,9 @@ __C {
     void llaisysROPE(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t pos_ids, float theta) {
         llaisys::ops::rope(out->tensor, in->tensor, pos_ids->tensor, theta);
     }
-    void llaisysSelfAttention(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t, llaisysTensor_t,
-                              float) {
-        TO_BE_IMPLEMENTED();
+    void llaisysSelfAttention(llaisysTensor_t attn_val, llaisysTensor_t q, llaisysTensor_t k,
+                              llaisysTensor_t v, float scale) {
+        llaisys::ops::selfAttention(attn_val->tensor, q->tensor, k->tensor, v->tensor, scale);
     }
     void llaisysSwiGLU(llaisysTensor_t out, llaisysTensor_t gate, llaisysTensor_t up) {
         llaisys::ops::swiglu(out->tensor, gate->tensor, up->tensor);
@@ -174,6 +174,12 @@ __C {
                                  llaisysTensor_t k, llaisysTensor_t v, size_t pos) {
         llaisys::ops::kvAppendInt8Pair(k_cache->tensor, k_scale->tensor, v_cache->tensor,
                                        v_scale->tensor, k->tensor, v->tensor, pos);
+    }
+    void llaisysSelfAttentionInt8KV(llaisysTensor_t attn_val, llaisysTensor_t q,
+                                    llaisysTensor_t k_codes, llaisysTensor_t k_scale,
+                                    llaisysTensor_t v_codes, llaisysTensor_t v_scale, float scale) {
+        llaisys::ops::selfAttentionInt8KV(attn_val->tensor, q->tensor, k_codes->tensor,
+                                          k_scale->tensor, v_codes->tensor, v_scale->tensor, scale);
     }
     void llaisysDequantizeInt8Pair(llaisysTensor_t out0, llaisysTensor_t q0, llaisysTensor_t scale0,
                                    llaisysTensor_t out1, llaisysTensor_t q1, llaisysTensor_t scale1) {

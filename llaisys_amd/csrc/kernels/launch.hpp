@@ -85,4 +85,14 @@ void dequantizeInt8Pair(void *out0, const int8_t *q0, const float *scale0, size_
                         void *out1, const int8_t *q1, const float *scale1, size_t rows1,
                         size_t cols, llaisysDataType_t dt, hipStream_t stream);
 
+// Causal GQA self-attention: q [seq, nh, d], k [total, nkvh, d], v [total, nkvh, dv],
+// out [seq, nh, dv].  With k_scale / v_scale non-null, k and v are INT8 codes with one F32
+// scale per (token, kv head) row.  `ws` (ws_bytes) holds the partials of a split launch;
+// selfAttentionWorkspaceBytes(d) is always enough.
+size_t selfAttentionWorkspaceBytes(size_t head_dim);
+void selfAttention(void *out, const void *q, const void *k, const void *v, const float *k_scale,
+                   const float *v_scale, size_t seq, size_t total, size_t nh, size_t nkvh,
+                   size_t d, size_t dv, float scale, llaisysDataType_t dt, void *ws,
+                   size_t ws_bytes, hipStream_t stream);
+
 } // namespace llaisys::kernels

@@ -319,6 +319,73 @@ void dequantizeInt8Pair(tensor_t out0, tensor_t q0, tensor_t scale0, tensor_t ou
     launched("dequantizeInt8Pair");
 }
 
+namespace {
+// Shape checks of reference src/ops/self_attention/op.cpp:19-45 (messages kept), plus the
+// ones a GPU kernel needs (a non-zero kv head count, the output's head_dim).
+void checkAttention(const tensor_t &attn_val, const tensor_t &q, const tensor_t &k,
+                    const tensor_t &v) {
+    ASSERT(attn_val->isContiguous() && q->isContiguous() && k->isContiguous() && v->isContiguous(),
+           "Tensor shoule be contiguous");
+    ASSERT(q->shape().size() == 3, "Q shape must be 3D");
+    ASSERT(k->shape().size() == 3, "K shape must be 3D");
+    ASSERT(v->shape().size() == 3, "V shape must be 3D");
+    ASSERT(attn_val->shape().size() == 3, "Attn_Val shape must be 3D");
+    const size_t seq = q->shape()[0], nh = q->shape()[1], d = q->shape()[2];
+    const size_t total = k->shape()[0], nkvh = k->shape()[1];
+    ASSERT(seq == attn_val->shape()[0], "attn_val seq_len mismatch");
+    ASSERT(nh == attn_val->shape()[1], "attn_val nhead mismatch");
+    ASSERT(total == v->shape()[0], "K/V total_len mismatch");
+    ASSERT(d == k->shape()[2], "K head_dim mismatch");
+    ASSERT(nkvh == v->shape()[1], "K/V head mismatch");
+    ASSERT(nkvh > 0 && nh % nkvh == 0, "nhead must be divisible by kv_head (GQA)");
+    ASSERT(attn_val->shape()[2] == v->shape()[2], "attn_val v_head_dim mismatch");
+}
+
+void launchAttention(const tensor_t &attn_val, const tensor_t &q, const tensor_t &k,
+                     const tensor_t &v, const float *ks, const float *vs, float scale) {
+    auto s = streamFor(q);
+    const size_t d = q->shape()[2];
+    const size_t reserved = kernels::kScratchReserved;
+    const size_t need = kernels::selfAttentionWorkspaceBytes(d);
+    char *ws = static_cast<char *>(device::amd::workspace(q->deviceId(), reserved + need));
+    kernels::selfAttention(attn_val->data(), q->data(), k->data(), v->data(), ks, vs, q->shape()[0],
+                           k->shape()[0], q->shape()[1], k->shape()[1], d, v->shape()[2], scale,
+                           q->dtype(), ws + reserved, need, s);
+    launched("selfAttention");
+}
+} // namespace
+
+// reference src/ops/self_attention/op.cpp:19-45
+void selfAttention(tensor_t attn_val, tensor_t q, tensor_t k, tensor_t v, float scale) {
+    CHECK_SAME_DEVICE(attn_val, q, k, v);
+    checkAttention(attn_val, q, k, v);
+    CHECK_SAME_DTYPE(attn_val->dtype(), q->dtype(), k->dtype(), v->dtype());
+    requireFloat(q->dtype());
+    launchAttention(attn_val, q, k, v, nullptr, nullptr, scale);
+}
+
+// Attention over an INT8 cache: the composition dequantizeInt8 (into q's dtype) then
+// selfAttention, reading the caches as codes.
+void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor_t k_scale,
+                         tensor_t v_codes, tensor_t v_scale, float scale) {
+    CHECK_SAME_DEVICE(attn_val, q, k_codes, v_codes);
+    CHECK_SAME_DEVICE(q, k_scale, v_scale);
+    checkAttention(attn_val, q, k_codes, v_codes);
+    CHECK_SAME_DTYPE(attn_val->dtype(), q->dtype());
+    requireFloat(q->dtype());
+    ASSERT(k_codes->dtype() == LLAISYS_DTYPE_I8 && v_codes->dtype() == LLAISYS_DTYPE_I8,
+           "SelfAttentionInt8KV: cache codes must be INT8");
+    ASSERT(k_scale->dtype() == LLAISYS_DTYPE_F32 && v_scale->dtype() == LLAISYS_DTYPE_F32,
+           "SelfAttentionInt8KV: cache scales must be F32");
+    ASSERT(k_scale->isContiguous() && v_scale->isContiguous(), "Tensor shoule be contiguous");
+    const size_t total = k_codes->shape()[0], nkvh = k_codes->shape()[1];
+    ASSERT(k_scale->ndim() == 2 && k_scale->shape()[0] == total && k_scale->shape()[1] == nkvh &&
+               v_scale->ndim() == 2 && v_scale->shape()[0] == total && v_scale->shape()[1] == nkvh,
+           "SelfAttentionInt8KV: scales must be [total_len, kv_head]");
+    launchAttention(attn_val, q, k_codes, v_codes, reinterpret_cast<const float *>(k_scale->data()),
+                    reinterpret_cast<const float *>(v_scale->data()), scale);
+}
+
 } // namespace llaisys::ops
 
 namespace llaisys::ops {

@@ -21,6 +21,9 @@ void dequantizeInt8(tensor_t out, tensor_t q, tensor_t scale);
 void kvAppendInt8(tensor_t cache_q, tensor_t cache_scale, tensor_t kv, size_t pos);
 void kvAppendInt8Pair(tensor_t k_cache, tensor_t k_scale, tensor_t v_cache, tensor_t v_scale,
                       tensor_t k, tensor_t v, size_t pos);
+void selfAttention(tensor_t attn_val, tensor_t q, tensor_t k, tensor_t v, float scale);
+void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor_t k_scale,
+                         tensor_t v_codes, tensor_t v_scale, float scale);
 void dequantizeInt8Pair(tensor_t out0, tensor_t q0, tensor_t scale0, tensor_t out1, tensor_t q1,
                         tensor_t scale1);
 void ropeKvAppendInt8(tensor_t q_out, tensor_t q_in, tensor_t k_in, tensor_t v_in,

@@ -32,6 +32,7 @@ ADDED_OPS = {
     "llaisysKVAppendInt8": [T, T, T, c_size_t],
     "llaisysKVAppendInt8Pair": [T, T, T, T, T, T, c_size_t],
     "llaisysDequantizeInt8Pair": [T, T, T, T, T, T],
+    "llaisysSelfAttentionInt8KV": [T, T, T, T, T, T, c_float],
 }
 
 

@@ -1,8 +1,8 @@
 """Ops: the LLAISYS operators as static methods.
 
-The nine reference methods match python/llaisys/ops.py:6-55 (linear, rearrange and
-self_attention raise in this library: out of scope); the rest wrap the additive entry
-points of include/llaisys/ops.h.
+The nine reference methods match python/llaisys/ops.py:6-55 (linear and rearrange raise
+in this library: out of scope); the rest wrap the additive entry points of
+include/llaisys/ops.h.
 """
 from ctypes import c_float, c_size_t
 
@@ -98,6 +98,14 @@ class Ops:
         LIB_LLAISYS.llaisysKVAppendInt8Pair(k_cache.lib_tensor(), k_scale.lib_tensor(),
                                             v_cache.lib_tensor(), v_scale.lib_tensor(),
                                             k.lib_tensor(), v.lib_tensor(), c_size_t(pos))
+
+    @staticmethod
+    def self_attention_int8kv(attn_val: Tensor, q: Tensor, k_codes: Tensor, k_scale: Tensor,
+                              v_codes: Tensor, v_scale: Tensor, scale: float):
+        LIB_LLAISYS.llaisysSelfAttentionInt8KV(attn_val.lib_tensor(), q.lib_tensor(),
+                                               k_codes.lib_tensor(), k_scale.lib_tensor(),
+                                               v_codes.lib_tensor(), v_scale.lib_tensor(),
+                                               c_float(scale))
 
     @staticmethod
     def dequantize_int8_pair(out0: Tensor, q0: Tensor, scale0: Tensor, out1: Tensor, q1: Tensor,

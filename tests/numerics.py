@@ -51,3 +51,35 @@ def assert_exact(got, exp, what=""):
     got, exp = np.asarray(got), np.asarray(exp)
     assert got.shape == exp.shape and got.dtype == exp.dtype, (what, got.shape, exp.shape)
     assert np.array_equal(got.view(np.uint8), exp.view(np.uint8)), f"{what}: not bit-identical"
+
+
+def _as_f32(a):
+    a = np.asarray(a)
+    if a.dtype == np.uint16:
+        return (a.astype(np.uint32) << 16).view(np.float32)
+    return a.astype(np.float32)
+
+
+def assert_attention_close(got, exp, v, what=""):
+    """Attention outputs against the oracle.  Each output is a softmax-weighted sum over up
+    to `total` keys; the reference accumulates it left to right in f32, so its own rounding
+    error is of the order of 2^-24 * sqrt(total) * max|v|, and an output that cancels to
+    near 0 cannot be matched to a few ulps by any other summation order.  Bound: within the
+    op's usual tolerance (2 ulps for bf16 / f16, 1e-5 relative for f32) OR within an
+    absolute floor of 2^-16 * max|v|."""
+    got, exp = np.asarray(got), np.asarray(exp)
+    assert got.shape == exp.shape and got.dtype == exp.dtype, (what, got.shape, exp.shape)
+    g, e = _as_f32(got).astype(np.float64), _as_f32(exp).astype(np.float64)
+    assert np.array_equal(np.isnan(g), np.isnan(e)), f"{what}: NaN pattern differs"
+    fin = np.isfinite(e)
+    floor = 2.0 ** -16 * float(np.abs(_as_f32(v)).max(initial=0.0))
+    absd = np.abs(g[fin] - e[fin])
+    if exp.dtype == np.float32:
+        ok = absd <= F32_RTOL * np.abs(e[fin])
+    elif exp.dtype == np.uint16:
+        ok = bf16_ulp_distance(got[fin], exp[fin]) <= HALF_ULPS
+    else:
+        ok = _f16_ulps(got[fin], exp[fin]) <= HALF_ULPS
+    ok |= absd <= floor
+    assert ok.all(), (f"{what}: {(~ok).sum()} of {ok.size} outputs beyond tolerance "
+                      f"(max abs diff {absd.max():.3g}, floor {floor:.3g})")

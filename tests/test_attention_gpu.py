@@ -1,0 +1,103 @@
+"""Self-attention on the GPU (llaisysSelfAttention, llaisysSelfAttentionInt8KV) against the
+oracle's restatement of the reference kernel (self_attention_cpu.cpp:13-115), which
+tests/test_oracle.py pins to the compiled reference.  Tolerance: numerics.assert_attention_close.
+The INT8 form must equal, bit for bit, dequantizing the caches and attending."""
+import zlib
+
+import numpy as np
+import pytest
+
+import llaisys_amd as L
+import oracle
+from llaisys_amd.hostfmt import f32_to_bf16
+from numerics import assert_attention_close, assert_exact
+
+pytestmark = pytest.mark.gpu
+
+AMD = dict(device=L.DeviceType.AMD, device_id=0)
+DTS = {"f32": L.DataType.F32, "bf16": L.DataType.BF16, "f16": L.DataType.F16}
+NP = {"f32": np.float32, "bf16": np.uint16, "f16": np.float16}
+
+
+def sample(rng, shape, dt):
+    x = rng.standard_normal(shape, dtype=np.float32)
+    return {"f32": x, "bf16": f32_to_bf16(x), "f16": x.astype(np.float16)}[dt]
+
+
+def dev(a, dt=None):
+    return L.Tensor.from_numpy(a, dt, **AMD)
+
+
+def attend(q, k, v, scale, dt):
+    out = L.Tensor(q.shape[:2] + (v.shape[2],), DTS[dt], **AMD)
+    L.Ops.self_attention(out, dev(q, DTS[dt]), dev(k, DTS[dt]), dev(v, DTS[dt]), scale)
+    return out.numpy()
+
+
+SHAPES = [
+    # seq, total, nh, nkvh, d  -- reference test shapes, Qwen2-1.5B decode (split keys) and
+    # prefill, a prefix cache, seq > total (size_t wrap), head_dim 64, Llama GQA 4, group > 8
+    (2, 2, 1, 1, 4), (5, 11, 4, 2, 8),
+    (1, 37, 12, 2, 128), (1, 4097, 12, 2, 128),
+    (256, 256, 12, 2, 128), (64, 300, 12, 2, 128),
+    (3, 2, 2, 1, 128), (9, 40, 4, 2, 64),
+    (1, 2048, 32, 8, 128), (5, 70, 16, 1, 128),
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_self_attention_matches_oracle(dt, shape):
+    seq, total, nh, nkvh, d = shape
+    rng = np.random.default_rng(zlib.crc32(repr((dt, shape)).encode()))
+    q, k, v = sample(rng, (seq, nh, d), dt), sample(rng, (total, nkvh, d), dt), sample(rng, (total, nkvh, d), dt)
+    scale = 1.0 / np.sqrt(d)
+    got = attend(q, k, v, scale, dt)
+    assert_attention_close(got, oracle.self_attention(q, k, v, scale), v, f"{dt} {shape}")
+
+
+def test_self_attention_golden_on_gpu(golden):
+    n = 0
+    for (op, dt, case), c in golden.items():
+        if op == "self_attention":
+            got = attend(c["q"], c["k"], c["v"], float(c["scale"]), dt)
+            assert_attention_close(got, c["out"], c["v"], f"golden {dt} {case}")
+            n += 1
+    assert n == 18
+
+
+def test_self_attention_empty_cache_gives_zeros():
+    q = f32_to_bf16(np.ones((2, 4, 128), np.float32))
+    out = L.Tensor((2, 4, 128), L.DataType.BF16, **AMD)
+    kz = L.Tensor((0, 2, 128), L.DataType.BF16, **AMD)
+    L.Ops.self_attention(out, dev(q, L.DataType.BF16), kz, kz, 0.1)
+    assert not out.numpy().any()
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("shape", [(1, 4097, 12, 2, 128), (128, 128, 12, 2, 128), (5, 11, 4, 2, 8), (7, 33, 4, 2, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_self_attention_int8kv(dt, shape):
+    """INT8 cache (1% outliers x20, as config 3): equal to dequantize-then-attend on the GPU,
+    and within tolerance of the oracle's composition."""
+    seq, total, nh, nkvh, d = shape
+    rng = np.random.default_rng(zlib.crc32(repr(("int8", dt, shape)).encode()))
+    x = rng.standard_normal((2, total, nkvh, d), dtype=np.float32)
+    x[rng.random(x.shape) < 0.01] *= 20
+    kv = {"f32": x, "bf16": f32_to_bf16(x), "f16": x.astype(np.float16)}[dt]
+    kq, ks = oracle.quantize_int8(kv[0])
+    vq, vs = oracle.quantize_int8(kv[1])
+    q = sample(rng, (seq, nh, d), dt)
+    scale = 1.0 / np.sqrt(d)
+    out = L.Tensor((seq, nh, d), DTS[dt], **AMD)
+    tq = dev(q, DTS[dt])
+    tkq, tks, tvq, tvs = dev(kq), dev(ks), dev(vq), dev(vs)
+    L.Ops.self_attention_int8kv(out, tq, tkq, tks, tvq, tvs, scale)
+    # the composition on the GPU: dequantize both caches, then attend
+    kd, vd = L.Tensor((total, nkvh, d), DTS[dt], **AMD), L.Tensor((total, nkvh, d), DTS[dt], **AMD)
+    L.Ops.dequantize_int8_pair(kd, tkq, tks, vd, tvq, tvs)
+    ref = L.Tensor((seq, nh, d), DTS[dt], **AMD)
+    L.Ops.self_attention(ref, tq, kd, vd, scale)
+    assert_exact(out.numpy(), ref.numpy(), "int8 vs dequantize + attend")
+    exp = oracle.self_attention_int8kv(q, kq, ks, vq, vs, scale)
+    assert_attention_close(out.numpy(), exp, oracle.dequantize_int8(vq, vs, NP[dt]), f"int8 {dt} {shape}")
