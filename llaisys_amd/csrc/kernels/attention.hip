@@ -34,9 +34,6 @@ namespace llaisys::kernels {
 
 namespace {
 
-constexpr int kU = 4;              // load instructions of K (and V) per batch
-constexpr int kMaxWavesPerBlock = 8;
-constexpr int kChunkKeys = 256;    // smallest key chunk of a split launch
 
 // Row reader: 8 consecutive elements of a K or V row as f32.
 template <typename T, bool kInt8>
@@ -95,7 +92,7 @@ struct AttnArgs {
     const float *vs;
     float *part;     // partials of a split launch: [(i * nh + h) * nchunks + c][D + 2]
     size_t seq, total;
-    int nh, nkvh, group, head_blocks, nchunks, chunk;
+    int nh, nkvh, group, slices, nchunks, chunk;
     float scale;
 };
 
@@ -105,50 +102,64 @@ __device__ __forceinline__ size_t visibleKeys(size_t total, size_t seq, size_t i
     return cur >= total ? total : cur + 1;
 }
 
-template <typename T, bool kInt8, int D>
-__global__ void __launch_bounds__(kWave * kMaxWavesPerBlock)
-    attnWave(AttnArgs a) {
+constexpr int kWaves = 8; // waves per block of the vector kernel
+
+// One block per (query, kv head, slice of G q heads, key chunk); its kWaves waves take the
+// chunk's key tiles (KPW * U keys) in turn, every wave holding the G heads' q, running max,
+// sum and output columns in registers, so each K / V row is loaded once per block.  The
+// waves' states merge through LDS; the block then writes the output (one chunk) or the
+// chunk's partial (split launch).
+template <typename T, bool kInt8, int D, int G, int U>
+__global__ void __launch_bounds__(kWave * kWaves)
+    attnGroup(AttnArgs a) {
     using IO = RowIO<T, kInt8>;
-    constexpr int R = D / 8;          // lanes per key row
-    constexpr int KPW = kWave / R;    // keys per load instruction
+    constexpr int R = D / 8;       // lanes per key row
+    constexpr int KPW = kWave / R; // keys per load instruction
+    constexpr int TILE = KPW * U;  // keys per wave per step
+    __shared__ float st[kWaves][G][D + 2];
+
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
     const int rs = lane / R, col = (lane % R) * 8;
 
-    // block -> (query, kv head, head block, chunk); the latest queries (most keys) first
+    // block -> (query, kv head, head slice, chunk); the latest queries (most keys) first
     unsigned b = blockIdx.x;
     const int c = int(b % unsigned(a.nchunks));
     b /= unsigned(a.nchunks);
-    const int hb = int(b % unsigned(a.head_blocks));
-    b /= unsigned(a.head_blocks);
+    const int sl = int(b % unsigned(a.slices));
+    b /= unsigned(a.slices);
     const int g = int(b % unsigned(a.nkvh));
     const size_t i = a.seq - 1 - size_t(b / unsigned(a.nkvh));
-    const int hg = hb * kMaxWavesPerBlock + wave; // head within the kv group
-    if (hg >= a.group) return;                    // wave-uniform; no block barrier below
-    const int h = g * a.group + hg;
+    const int h0 = g * a.group + sl * G; // first q head of the slice
 
     const size_t vis = visibleKeys(a.total, a.seq, i);
     const size_t k0 = size_t(c) * size_t(a.chunk);
     const size_t k1 = min(vis, k0 + size_t(a.chunk));
 
-    float qv[8];
-    {
-        const char *qp = static_cast<const char *>(a.q) + ((i * a.nh + h) * D + col) * Fmt<T>::kBytes;
+    float qv[G][8];
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+        const char *qp = static_cast<const char *>(a.q) + ((i * a.nh + h0 + j) * D + col) * Fmt<T>::kBytes;
         typename RowIO<T, false>::Raw r;
 #pragma unroll
         for (int k = 0; k < RowIO<T, false>::kRegs; ++k) r.r[k] = *reinterpret_cast<const v4u *>(qp + 16 * k);
-        RowIO<T, false>::unpack(r, 0.0f, qv);
+        RowIO<T, false>::unpack(r, 0.0f, qv[j]);
     }
-    float m = -INFINITY, l = 0.0f, o[8];
+    float m[G], l[G], o[G][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+    for (int j = 0; j < G; ++j) {
+        m[j] = -INFINITY;
+        l[j] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[j][e] = 0.0f;
+    }
 
-    for (size_t kb = k0; kb < k1; kb += size_t(KPW) * kU) {
-        typename IO::Raw kr[kU], vr[kU];
-        float ksc[kU], vsc[kU];
-        bool ok[kU];
+    for (size_t kb = k0 + size_t(wave) * TILE; kb < k1; kb += size_t(kWaves) * TILE) {
+        typename IO::Raw kr[U], vr[U];
+        float ksc[U], vsc[U];
+        bool ok[U];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
+        for (int u = 0; u < U; ++u) {
             const size_t key = kb + size_t(u * KPW + rs);
             ok[u] = key < k1;
             const size_t row = (ok[u] ? key : k0) * size_t(a.nkvh) + size_t(g);
@@ -161,99 +172,159 @@ __global__ void __launch_bounds__(kWave * kMaxWavesPerBlock)
                 ksc[u] = vsc[u] = 0.0f;
             }
         }
-        float s[kU];
-        float mx = m;
+        float s[G][U];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
+        for (int u = 0; u < U; ++u) {
             float kf[8];
             IO::unpack(kr[u], ksc[u], kf);
-            float dot = 0.0f;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(qv[e], kf[e], dot);
-            dot = waveGroupReduce<R, SumOp>(dot);
-            s[u] = ok[u] ? dot * a.scale : -INFINITY;
-            mx = fmaxf(mx, s[u]);
+            for (int j = 0; j < G; ++j) {
+                float dot = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) dot = __builtin_fmaf(qv[j][e], kf[e], dot);
+                dot = waveGroupReduce<R, SumOp>(dot);
+                s[j][u] = ok[u] ? dot * a.scale : -INFINITY;
+            }
         }
-        // a -inf score is weight 0 (reference :111-113); m == mx keeps the state as is
-        const float corr = mx == m ? 1.0f : __expf(m - mx);
-        l *= corr;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] *= corr;
+        for (int j = 0; j < G; ++j) {
+            float mx = m[j];
 #pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            const float p = s[u] == -INFINITY ? 0.0f : __expf(s[u] - mx);
+            for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[j][u]);
+            // a -inf score is weight 0 (reference :111-113); m == mx keeps the state as is
+            const float corr = mx == m[j] ? 1.0f : __expf(m[j] - mx);
+            l[j] *= corr;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[j][e] *= corr;
+            m[j] = mx;
+#pragma unroll
+            for (int u = 0; u < U; ++u) s[j][u] = s[j][u] == -INFINITY ? 0.0f : __expf(s[j][u] - mx);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
             float vf[8];
             IO::unpack(vr[u], vsc[u], vf);
-            l += p;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = __builtin_fmaf(p, vf[e], o[e]);
+            for (int j = 0; j < G; ++j) {
+                l[j] += s[j][u];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[j][e] = __builtin_fmaf(s[j][u], vf[e], o[j][e]);
+            }
         }
-        m = mx;
     }
 
     // merge the KPW key slots of the wave (lanes R, 2R, ... apart hold the same columns)
 #pragma unroll
     for (int off = R; off < kWave; off *= 2) {
-        const float mo = __shfl_xor(m, off, kWave), lo = __shfl_xor(l, off, kWave);
-        const float M = fmaxf(m, mo);
-        const float fa = m == M ? 1.0f : __expf(m - M);
-        const float fb = mo == M ? 1.0f : __expf(mo - M);
-        // (a slot that saw no key has m = -inf and l = 0, o = 0: its factor may be 1 only
-        // when M is -inf too, and then every term is 0)
-        l = l * fa + lo * fb;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float oo = __shfl_xor(o[e], off, kWave);
-            o[e] = o[e] * fa + oo * fb;
+        for (int j = 0; j < G; ++j) {
+            const float mo = __shfl_xor(m[j], off, kWave), lo = __shfl_xor(l[j], off, kWave);
+            const float M = fmaxf(m[j], mo);
+            // a slot that saw no key has m = -inf, l = 0, o = 0; its factor is 1 only when M
+            // is -inf too, and then every term is 0
+            const float fa = m[j] == M ? 1.0f : __expf(m[j] - M);
+            const float fb = mo == M ? 1.0f : __expf(mo - M);
+            l[j] = l[j] * fa + lo * fb;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float oo = __shfl_xor(o[j][e], off, kWave);
+                o[j][e] = o[j][e] * fa + oo * fb;
+            }
+            m[j] = M;
         }
-        m = M;
     }
-    if (lane >= R) return;
-    if (a.nchunks == 1) {
-        float y[8];
-        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    if (lane < R) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = o[e] * inv;
-        char *op = static_cast<char *>(a.out) + ((i * a.nh + h) * D + col) * Fmt<T>::kBytes;
-        // pack: the reference rounding also for a NaN carrying the caller's scale payload
-        if constexpr (Fmt<T>::kBytes == 2) {
-            *reinterpret_cast<v4u *>(op) = Fmt<T>::pack(y);
+        for (int j = 0; j < G; ++j) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) st[wave][j][col + e] = o[j][e];
+            if (lane == 0) {
+                st[wave][j][D] = m[j];
+                st[wave][j][D + 1] = l[j];
+            }
+        }
+    }
+    __syncthreads();
+    // merge the waves: thread t -> (head j, column e) pairs
+    for (int p = threadIdx.x; p < G * D; p += kWave * kWaves) {
+        const int j = p / D, e = p % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, st[w][j][D]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = st[w][j][D];
+            const float f = mw == M ? 1.0f : __expf(mw - M); // 1 for M = -inf, where l = o = 0
+            L += st[w][j][D + 1] * f;
+            O += st[w][j][e] * f;
+        }
+        const size_t ih = i * a.nh + size_t(h0 + j);
+        if (a.nchunks == 1) {
+            // put: the reference rounding, also for a NaN carrying the caller's scale payload
+            Fmt<T>::put(a.out, ih * D + e, L > 0.0f ? O / L : 0.0f);
         } else {
-            *reinterpret_cast<v4u *>(op) = Fmt<T>::pack(y);
-            *reinterpret_cast<v4u *>(op + 16) = Fmt<T>::pack(y + 4);
+            float *pp = a.part + (ih * size_t(a.nchunks) + c) * (D + 2);
+            pp[e] = O;
+            if (e == 0) {
+                pp[D] = M;
+                pp[D + 1] = L;
+            }
         }
-        return;
-    }
-    float *pp = a.part + ((i * a.nh + h) * size_t(a.nchunks) + c) * (D + 2);
-    *reinterpret_cast<float4 *>(pp + col) = make_float4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<float4 *>(pp + col + 4) = make_float4(o[4], o[5], o[6], o[7]);
-    if (lane == 0) {
-        pp[D] = m;
-        pp[D + 1] = l;
     }
 }
 
-// Merge of the chunk partials of a split launch: one 64-thread block per (query, head).
+// Merge of the chunk partials of a split launch: one 1024-thread block per (query, head);
+// thread t takes column t % D of the chunks c = t / D (mod 1024 / D), so the partials are
+// read in a few rounds of independent loads.
+constexpr int kCombineThreads = 1024;
+
 template <typename T>
-__global__ void __launch_bounds__(kWave)
-    attnCombine(void *out, const float *part, int nh, int nchunks, int D) {
+__global__ void __launch_bounds__(kCombineThreads)
+    attnCombine(void *out, const float *part, int nchunks, int D) {
+    __shared__ float w[1024];  // per-chunk factor exp(m_c - M), nchunks <= 1024
+    __shared__ float red[kCombineThreads];
+    __shared__ float MM, LL;
     const size_t ih = blockIdx.x; // i * nh + h
     const float *pp = part + ih * size_t(nchunks) * (D + 2);
-    float M = -INFINITY;
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, pp[size_t(c) * (D + 2) + D]);
-    float L = 0.0f;
-    for (int c = 0; c < nchunks; ++c) {
-        const float mc = pp[size_t(c) * (D + 2) + D];
-        if (mc != -INFINITY) L += pp[size_t(c) * (D + 2) + D + 1] * __expf(mc - M);
+    const int t = threadIdx.x;
+    float mc = -INFINITY;
+    if (t < nchunks) mc = pp[size_t(t) * (D + 2) + D];
+    red[t] = mc;
+    __syncthreads();
+    if (t == 0) {
+        float M = -INFINITY;
+        for (int k = 0; k < nchunks; ++k) M = fmaxf(M, red[k]);
+        MM = M;
     }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    for (int e = threadIdx.x; e < D; e += kWave) {
-        float acc = 0.0f;
-        for (int c = 0; c < nchunks; ++c) {
-            const float mc = pp[size_t(c) * (D + 2) + D];
-            if (mc != -INFINITY) acc += pp[size_t(c) * (D + 2) + e] * __expf(mc - M);
-        }
-        Fmt<T>::put(out, ih * D + e, acc * inv);
+    __syncthreads();
+    const float M = MM;
+    if (t < nchunks) {
+        const float f = mc == M ? 1.0f : __expf(mc - M); // mc = -inf: l = o = 0
+        w[t] = f;
+        red[t] = pp[size_t(t) * (D + 2) + D + 1] * f;
+    }
+    __syncthreads();
+    if (t == 0) {
+        float L = 0.0f;
+        for (int k = 0; k < nchunks; ++k) L += red[k];
+        LL = L;
+    }
+    __syncthreads();
+    const int parts = kCombineThreads / D;
+    const int e = t % D, pidx = t / D;
+    float acc = 0.0f;
+    if (pidx < parts) {
+#pragma unroll 8
+        for (int k = pidx; k < nchunks; k += parts) acc += pp[size_t(k) * (D + 2) + e] * w[k];
+    }
+    red[t] = acc;
+    __syncthreads();
+    if (t < D) {
+        float O = 0.0f;
+        for (int k = 0; k < parts; ++k) O += red[k * D + t];
+        const float L = LL;
+        Fmt<T>::put(out, ih * D + t, L > 0.0f ? O / L : 0.0f);
     }
 }
 
@@ -303,6 +374,30 @@ __global__ void __launch_bounds__(kWave)
     for (int e = lane; e < dv; e += kWave) Fmt<T>::put(a.out, ih * dv + e, acc[e] * inv);
 }
 
+// Heads per wave for a kv group: the largest supported count that divides it.
+int sliceOf(int group) {
+    for (int g : {8, 6, 4, 2})
+        if (group % g == 0) return g;
+    return 1;
+}
+
+template <typename T, bool kInt8, int D, int G>
+void launchGroup(const AttnArgs &a, size_t blocks, hipStream_t s) {
+    constexpr int U = kInt8 ? 8 : 4; // 16 bytes of K and V codes per lane per step, or 32 of elements
+    attnGroup<T, kInt8, D, G, U><<<unsigned(blocks), kWave * kWaves, 0, s>>>(a);
+}
+
+template <typename T, bool kInt8, int D>
+void launchD(const AttnArgs &a, int G, size_t blocks, hipStream_t s) {
+    switch (G) {
+    case 8: return launchGroup<T, kInt8, D, 8>(a, blocks, s);
+    case 6: return launchGroup<T, kInt8, D, 6>(a, blocks, s);
+    case 4: return launchGroup<T, kInt8, D, 4>(a, blocks, s);
+    case 2: return launchGroup<T, kInt8, D, 2>(a, blocks, s);
+    default: return launchGroup<T, kInt8, D, 1>(a, blocks, s);
+    }
+}
+
 template <typename T, bool kInt8>
 void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s) {
     if (a.seq == 0 || a.nh == 0) return;
@@ -315,29 +410,31 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
         attnScalar<T, kInt8><<<unsigned(a.seq * size_t(a.nh)), kWave, size_t(dv) * sizeof(float), s>>>(a, d, dv);
         return;
     }
-    // Split the keys when few (query, head) pairs would leave the GPU idle: aim at ~8192
-    // waves, chunks of at least kChunkKeys keys, partials within the workspace.
-    const size_t pairs = a.seq * size_t(a.nh);
+    const int G = sliceOf(a.group);
+    a.slices = a.group / G;
+    // A block's waves each take one step of keys per chunk when the launch is split: about
+    // 2048 waves for decode, partials within the workspace and at most 1024 per (query, head).
+    const int U = kInt8 ? 8 : 4;
+    const size_t tile = size_t(kWave / (d / 8)) * U * kWaves; // keys per block step
+    const size_t groups = a.seq * size_t(a.nkvh) * size_t(a.slices);
     size_t nchunks = 1;
-    if (pairs < 4096 && a.total > size_t(kChunkKeys)) {
-        nchunks = std::min((a.total + kChunkKeys - 1) / kChunkKeys, (8192 + pairs - 1) / pairs);
-        const size_t per = size_t(d + 2) * sizeof(float);
-        nchunks = std::max<size_t>(1, std::min(nchunks, ws_bytes / (pairs * per)));
+    if (groups < 512 && a.total > tile) {
+        nchunks = std::min<size_t>((a.total + tile - 1) / tile, 1024);
+        const size_t per = size_t(d + 2) * sizeof(float) * a.seq * size_t(a.nh);
+        nchunks = std::max<size_t>(1, std::min(nchunks, ws_bytes / per));
     }
     a.nchunks = int(nchunks);
     a.chunk = int(std::min<size_t>(nchunks == 1 ? std::max<size_t>(a.total, 1)
                                                 : (a.total + nchunks - 1) / nchunks,
                                    size_t(INT32_MAX)));
     a.part = static_cast<float *>(ws);
-    a.head_blocks = (a.group + kMaxWavesPerBlock - 1) / kMaxWavesPerBlock;
-    const int waves = std::min(a.group, kMaxWavesPerBlock);
-    const size_t blocks = a.seq * size_t(a.nkvh) * size_t(a.head_blocks) * nchunks;
-    switch (d) {
-    case 64: attnWave<T, kInt8, 64><<<unsigned(blocks), waves * kWave, 0, s>>>(a); break;
-    default: attnWave<T, kInt8, 128><<<unsigned(blocks), waves * kWave, 0, s>>>(a); break;
-    }
+    const size_t blocks = groups * nchunks;
+    if (d == 64)
+        launchD<T, kInt8, 64>(a, G, blocks, s);
+    else
+        launchD<T, kInt8, 128>(a, G, blocks, s);
     if (nchunks > 1)
-        attnCombine<T><<<unsigned(pairs), kWave, 0, s>>>(a.out, a.part, a.nh, a.nchunks, d);
+        attnCombine<T><<<unsigned(a.seq * size_t(a.nh)), kCombineThreads, 0, s>>>(a.out, a.part, a.nchunks, d);
 }
 
 template <bool kInt8>
@@ -352,10 +449,11 @@ void dispatch(AttnArgs a, int d, int dv, llaisysDataType_t dt, void *ws, size_t 
 
 } // namespace
 
-size_t selfAttentionWorkspaceBytes(size_t head_dim) {
-    // a split launch has pairs < 4096 and at most ceil(8192 / pairs) chunks per pair, so
-    // fewer than 8192 + 4096 partials of head_dim + 2 floats
-    return size_t(8192 + 4096) * (head_dim + 2) * sizeof(float);
+size_t selfAttentionWorkspaceBytes(size_t seq, size_t nh, size_t head_dim) {
+    // up to 1024 partials of head_dim + 2 floats per (query, head), capped at 64 MiB: a
+    // smaller workspace only lowers the chunk count (decode: 12 heads x 1024 x 520 B)
+    return std::min<size_t>(std::min<size_t>(seq * nh, 4096) * 1024 * (head_dim + 2) * sizeof(float),
+                            size_t(64) << 20);
 }
 
 void selfAttention(void *out, const void *q, const void *k, const void *v, const float *k_scale,

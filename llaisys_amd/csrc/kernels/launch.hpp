@@ -88,8 +88,8 @@ void dequantizeInt8Pair(void *out0, const int8_t *q0, const float *scale0, size_
 // Causal GQA self-attention: q [seq, nh, d], k [total, nkvh, d], v [total, nkvh, dv],
 // out [seq, nh, dv].  With k_scale / v_scale non-null, k and v are INT8 codes with one F32
 // scale per (token, kv head) row.  `ws` (ws_bytes) holds the partials of a split launch;
-// selfAttentionWorkspaceBytes(d) is always enough.
-size_t selfAttentionWorkspaceBytes(size_t head_dim);
+// selfAttentionWorkspaceBytes(seq, nh, d) lets it split decode launches fully.
+size_t selfAttentionWorkspaceBytes(size_t seq, size_t nh, size_t head_dim);
 void selfAttention(void *out, const void *q, const void *k, const void *v, const float *k_scale,
                    const float *v_scale, size_t seq, size_t total, size_t nh, size_t nkvh,
                    size_t d, size_t dv, float scale, llaisysDataType_t dt, void *ws,

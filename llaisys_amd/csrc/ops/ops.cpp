@@ -346,7 +346,7 @@ void launchAttention(const tensor_t &attn_val, const tensor_t &q, const tensor_t
     auto s = streamFor(q);
     const size_t d = q->shape()[2];
     const size_t reserved = kernels::kScratchReserved;
-    const size_t need = kernels::selfAttentionWorkspaceBytes(d);
+    const size_t need = kernels::selfAttentionWorkspaceBytes(q->shape()[0], q->shape()[1], d);
     char *ws = static_cast<char *>(device::amd::workspace(q->deviceId(), reserved + need));
     kernels::selfAttention(attn_val->data(), q->data(), k->data(), v->data(), ks, vs, q->shape()[0],
                            k->shape()[0], q->shape()[1], k->shape()[1], d, v->shape()[2], scale,

@@ -10,7 +10,7 @@ import pytest
 import llaisys_amd as L
 import oracle
 from llaisys_amd.hostfmt import f32_to_bf16
-from numerics import assert_attention_close, assert_exact
+from numerics import assert_attention_close
 
 pytestmark = pytest.mark.gpu
 
@@ -78,8 +78,9 @@ def test_self_attention_empty_cache_gives_zeros():
 @pytest.mark.parametrize("shape", [(1, 4097, 12, 2, 128), (128, 128, 12, 2, 128), (5, 11, 4, 2, 8), (7, 33, 4, 2, 64)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_self_attention_int8kv(dt, shape):
-    """INT8 cache (1% outliers x20, as config 3): equal to dequantize-then-attend on the GPU,
-    and within tolerance of the oracle's composition."""
+    """INT8 cache (1% outliers x20, as config 3) against dequantize-then-attend on the GPU
+    (the same values in another key tiling, so within the attention tolerance rather than bit
+    for bit) and against the oracle's composition."""
     seq, total, nh, nkvh, d = shape
     rng = np.random.default_rng(zlib.crc32(repr(("int8", dt, shape)).encode()))
     x = rng.standard_normal((2, total, nkvh, d), dtype=np.float32)
@@ -98,6 +99,7 @@ def test_self_attention_int8kv(dt, shape):
     L.Ops.dequantize_int8_pair(kd, tkq, tks, vd, tvq, tvs)
     ref = L.Tensor((seq, nh, d), DTS[dt], **AMD)
     L.Ops.self_attention(ref, tq, kd, vd, scale)
-    assert_exact(out.numpy(), ref.numpy(), "int8 vs dequantize + attend")
+    vdq = oracle.dequantize_int8(vq, vs, NP[dt])
+    assert_attention_close(out.numpy(), ref.numpy(), vdq, "int8 vs dequantize + attend")
     exp = oracle.self_attention_int8kv(q, kq, ks, vq, vs, scale)
-    assert_attention_close(out.numpy(), exp, oracle.dequantize_int8(vq, vs, NP[dt]), f"int8 {dt} {shape}")
+    assert_attention_close(out.numpy(), exp, vdq, f"int8 {dt} {shape}")
