@@ -334,6 +334,43 @@ def config_ops(L, rng):
     return cases, P
 
 
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def attention_ops(L, rng):
+    """(name, kind, amount per launch, launch(i)) for self-attention at Qwen2-1.5B heads
+    (12 q / 2 kv, head_dim 128): one-token decode over a 32768-token cache, INT8 and bf16
+    (kind "bytes": K and V read once + q + out), and a 2048-token causal prefill (kind
+    "flops": 4 * heads * head_dim * visible keys summed over the queries)."""
+    O, BF, F32, I8 = L.Ops, L.DataType.BF16, L.DataType.F32, L.DataType.I8
+    P = Pool(L, rng)
+    nh, nkv, d, tk = 12, 2, 128, 32768
+    sk = P.sets_for(tk * nkv * d * 2 * 2)
+    q1 = P.fill((1, nh, d), BF, sk)
+    kb, vb = P.fill((tk, nkv, d), BF, sk), P.fill((tk, nkv, d), BF, sk)
+    kq, vq = P.empty((tk, nkv, d), I8, sk), P.empty((tk, nkv, d), I8, sk)
+    ks, vs = P.empty((tk, nkv), F32, sk), P.empty((tk, nkv), F32, sk)
+    for j in range(sk):
+        O.kv_append_int8_pair(kq[j], ks[j], vq[j], vs[j], kb[j], vb[j], 0)
+    o1 = P.empty((1, nh, d), BF, 1)[0]
+    sc = 1.0 / np.sqrt(d)
+    qo = 2 * nh * d * 2
+    ops = [
+        ("decode INT8 KV [32768, 2, 128], 12 q heads", "bytes", tk * nkv * (d + 4) * 2 + qo,
+         lambda i: O.self_attention_int8kv(o1, q1[i % sk], kq[i % sk], ks[i % sk], vq[i % sk], vs[i % sk], sc)),
+        ("decode bf16 KV [32768, 2, 128], 12 q heads", "bytes", tk * nkv * d * 2 * 2 + qo,
+         lambda i: O.self_attention(o1, q1[i % sk], kb[i % sk], vb[i % sk], sc)),
+    ]
+    tp = 2048
+    qp = P.fill((tp, nh, d), BF, 1)[0]
+    kp, vp = P.fill((tp, nkv, d), BF, 1)[0], P.fill((tp, nkv, d), BF, 1)[0]
+    op_ = P.empty((tp, nh, d), BF, 1)[0]
+    ops.append(("prefill 2048 tokens causal, 12 q / 2 kv heads, bf16", "flops",
+                4 * nh * d * tp * (tp + 1) // 2,
+                lambda i: O.self_attention(op_, qp, kp, vp, sc)))
+    return ops, P
+
+
 def cpu_baseline(seconds):
     """Reference CPU ops (oracle/_ref, else the oracle port) on a row sample of config 1,
     single thread pinned to one core; GB/s with the same bytes formula as the GPU."""
@@ -441,6 +478,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-chain", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip configs 0, 2 and 3")
+    ap.add_argument("--no-attention", action="store_true", help="skip the self-attention lines")
     ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain (profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="3 dispatches of a 256 MiB device copy (counter calibration), then 3 of "
@@ -574,6 +612,33 @@ def main():
         del cases, pool
         print("bench: configs " + json.dumps(configs), file=sys.stderr, flush=True)
 
+    attention = None
+    if not args.no_attention:
+        print("bench: building attention buffers", file=sys.stderr, flush=True)
+        aops, apool = attention_ops(L, np.random.default_rng(11))
+        attention = {}
+        for name, kind, amount, fn in aops:
+            for i in range(3):
+                fn(i)
+            reps = max(args.steps // 2, 10)
+            hip.record(e0, stream)
+            for i in range(reps):
+                fn(i)
+            hip.record(e1, stream)
+            us = hip.elapsed_ms(e0, e1) / reps * 1e3
+            if kind == "bytes":
+                gbs = amount / (us * 1e-6) / 1e9
+                attention[name] = {"us": round(us, 3), "bytes": amount, "GB_s": round(gbs, 1),
+                                   "frac_peak": round(gbs / PEAK_GBS, 4), "bound": "hbm"}
+            else:
+                tf = amount / (us * 1e-6) / 1e12
+                attention[name] = {"us": round(us, 3), "flops": amount, "TFLOP_s": round(tf, 2),
+                                   "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                                   "bound": "mfma (bf16 dense peak)"}
+        assert L.take_device_error() == 0
+        del aops, apool
+        print("bench: attention " + json.dumps(attention), file=sys.stderr, flush=True)
+
     dom = per_op["swiglu"]
     roof = {"kernel": "swiglu binaryVec<BF16> [8192, 8960]", "bound": "hbm",
             "achieved": dom["GB_s"], "peak": PEAK_GBS, "unit": "GB/s",
@@ -593,7 +658,8 @@ def main():
         "frac_peak": round(value / PEAK_GBS, 4),
         "tokens_per_s": round(T / (ms_step * 1e-3)),
         "wall_s_timed": round(wall, 3),
-        "per_op": per_op, "chain": chain, "configs": configs, "roofline": roof,
+        "per_op": per_op, "chain": chain, "configs": configs, "attention": attention,
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace llaisys::kernels {
 
@@ -374,6 +375,155 @@ __global__ void __launch_bounds__(kWave)
     for (int e = lane; e < dv; e += kWave) Fmt<T>::put(a.out, ih * dv + e, acc[e] * inv);
 }
 
+// ---- prefill on MFMA (bf16, head_dim 128) ---------------------------------------------
+// One block per (16 queries, kv head, slice of W q heads), one wave per q head.  Per tile
+// of 64 keys a wave forms S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A = 16 key rows read
+// straight from memory, B = the wave's 16 queries kept in registers), so each lane holds
+// the scores of one query (column l % 16) for 16 of the keys and the softmax needs only an
+// exchange between the 4 lanes of that column; then O^T += V^T P^T with the same
+// instruction: P^T is the B operand as the lanes already hold it (k-slot 8g + j of a
+// lane group g is key 32p + 16(j / 4) + 4g + j % 4), V^T comes from a transposed copy of the
+// tile in LDS.  P enters as bf16 hi + lo parts (2^-17 relative), so the output keeps f32
+// accuracy.  Operand layouts (measured on MI355X): A[m = l % 16][k = 8(l / 16) + j],
+// B[k = 8(l / 16) + j][n = l % 16], D[m = 4(l / 16) + i][n = l % 16].
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaQ = 16;  // queries per block
+constexpr int kMfmaKT = 64; // keys per tile
+constexpr int kVtLd = 68;   // V^T row stride (bf16 elements; multiple of 4 for 8-byte reads)
+
+__device__ __forceinline__ bf16x8 asBf16x8(const v4u &r) { return __builtin_bit_cast(bf16x8, r); }
+
+template <int W>
+__global__ void __launch_bounds__(kWave * W)
+    attnMfma(AttnArgs a) {
+    constexpr int D = 128, KB = D / 32, DT = D / 16;
+    __shared__ uint16_t vt[D][kVtLd];
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = int(threadIdx.x) % kWave;
+    const int n = lane % 16, g4 = lane / 16;
+
+    const size_t nqb = (a.seq + kMfmaQ - 1) / kMfmaQ;
+    unsigned b = blockIdx.x;
+    const int sl = int(b % unsigned(a.slices));
+    b /= unsigned(a.slices);
+    const int g = int(b % unsigned(a.nkvh));
+    const size_t qb = nqb - 1 - size_t(b / unsigned(a.nkvh)); // latest queries first
+    const int h = g * a.group + sl * W + wave;
+    const size_t q0 = qb * kMfmaQ;
+    const size_t qi = min(q0 + size_t(n), a.seq - 1); // this lane's query (clamped for loads)
+    const size_t vis_q = visibleKeys(a.total, a.seq, qi);
+    const size_t vis_blk = visibleKeys(a.total, a.seq, min(q0 + kMfmaQ - 1, a.seq - 1));
+    const size_t kstride = size_t(a.nkvh) * D; // elements between key rows
+
+    bf16x8 qreg[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        const uint16_t *qp = static_cast<const uint16_t *>(a.q) + (qi * a.nh + h) * D + 32 * kb + 8 * g4;
+        qreg[kb] = asBf16x8(*reinterpret_cast<const v4u *>(qp));
+    }
+    float m = -INFINITY, lsum = 0.0f;
+    f32x4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const uint16_t *kbase = static_cast<const uint16_t *>(a.k) + size_t(g) * D;
+    const uint16_t *vbase = static_cast<const uint16_t *>(a.v) + size_t(g) * D;
+    for (size_t kt0 = 0; kt0 < vis_blk; kt0 += kMfmaKT) {
+        // K operands of the tile: key kt0 + 16t + l % 16, columns 32kb + 8(l / 16) .. + 7
+        v4u kr[4][KB];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const size_t key = min(kt0 + 16 * t + n, a.total - 1);
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+                kr[t][kb] = *reinterpret_cast<const v4u *>(kbase + key * kstride + 32 * kb + 8 * g4);
+        }
+        // V tile -> LDS, transposed (vt[d][key]); keys past the cache are zeros
+        __syncthreads(); // the previous tile's readers are done
+        for (int idx = threadIdx.x; idx < kMfmaKT * (D / 8); idx += kWave * W) {
+            const int dg = idx % (D / 8), kk = idx / (D / 8);
+            const size_t key = kt0 + size_t(kk);
+            v4u r = v4u{0u, 0u, 0u, 0u};
+            if (key < a.total) r = *reinterpret_cast<const v4u *>(vbase + key * kstride + 8 * dg);
+            const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vt[8 * dg + 2 * e][kk] = uint16_t(w[e] & 0xFFFFu);
+                vt[8 * dg + 2 * e + 1][kk] = uint16_t(w[e] >> 16);
+            }
+        }
+        // scores S^T[key kt0 + 16t + 4g + i][query n]
+        float p[4][4];
+        float mx = m;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kr[t][kb]), qreg[kb], acc, 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const size_t key = kt0 + size_t(16 * t + 4 * g4 + i);
+                p[t][i] = key < vis_q ? acc[i] * a.scale : -INFINITY;
+                mx = fmaxf(mx, p[t][i]);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        // key 0 is visible to every query, so m is finite after the first tile
+        const float corr = mx == m ? 1.0f : __expf(m - mx);
+        m = mx;
+        float ps = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                p[t][i] = p[t][i] == -INFINITY ? 0.0f : __expf(p[t][i] - mx);
+                ps += p[t][i];
+            }
+        lsum = lsum * corr + ps;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+        __syncthreads(); // V^T tile written
+#pragma unroll
+        for (int p2 = 0; p2 < 2; ++p2) {
+            bf16x8 bhi, blo;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = p[2 * p2 + j / 4][j % 4];
+                const __bf16 hi = __bf16(x);
+                bhi[j] = hi;
+                blo[j] = __bf16(x - float(hi));
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const uint16_t *row = &vt[16 * dt + n][32 * p2 + 4 * g4];
+                typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+                const v2u lo4 = *reinterpret_cast<const v2u *>(row);
+                const v2u hi4 = *reinterpret_cast<const v2u *>(row + 16);
+                const bf16x8 av = __builtin_bit_cast(bf16x8, v4u{lo4.x, lo4.y, hi4.x, hi4.y});
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo, o[dt], 0, 0, 0);
+            }
+        }
+    }
+    float lt = lsum + __shfl_xor(lsum, 16, kWave);
+    lt += __shfl_xor(lt, 32, kWave);
+    if (q0 + size_t(n) >= a.seq) return;
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    uint16_t *op = static_cast<uint16_t *>(a.out) + (qi * a.nh + h) * D + 4 * g4;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+        // O^T[d = 16dt + 4g + i][query n]; the reference rounding
+        const uint32_t w0 = f32ToBf16(o[dt][0] * inv) | (f32ToBf16(o[dt][1] * inv) << 16);
+        const uint32_t w1 = f32ToBf16(o[dt][2] * inv) | (f32ToBf16(o[dt][3] * inv) << 16);
+        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<v2u *>(op + 16 * dt) = v2u{w0, w1};
+    }
+}
+
 // Heads per wave for a kv group: the largest supported count that divides it.
 int sliceOf(int group) {
     for (int g : {8, 6, 4, 2})
@@ -412,6 +562,21 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
     }
     const int G = sliceOf(a.group);
     a.slices = a.group / G;
+    // bf16 prefill (16 or more queries) goes to the MFMA kernel; decode and the other
+    // types stay on the vector kernel
+    if constexpr (std::is_same_v<T, BF16> && !kInt8) {
+        const size_t mblocks = (a.seq + kMfmaQ - 1) / kMfmaQ * size_t(a.nkvh) * size_t(a.slices);
+        if (d == 128 && a.total > 0 && a.seq >= size_t(kMfmaQ) && mblocks < (size_t(1) << 31)) {
+            a.nchunks = 1;
+            switch (G) {
+            case 8: attnMfma<8><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
+            case 6: attnMfma<6><<<unsigned(mblocks), kWave * 6, 0, s>>>(a); return;
+            case 4: attnMfma<4><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
+            case 2: attnMfma<2><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
+            default: attnMfma<1><<<unsigned(mblocks), kWave, 0, s>>>(a); return;
+            }
+        }
+    }
     // A block's waves each take one step of keys per chunk when the launch is split: about
     // 2048 waves for decode, partials within the workspace and at most 1024 per (query, head).
     const int U = kInt8 ? 8 : 4;

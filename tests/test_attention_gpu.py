@@ -42,6 +42,10 @@ SHAPES = [
     (256, 256, 12, 2, 128), (64, 300, 12, 2, 128),
     (3, 2, 2, 1, 128), (9, 40, 4, 2, 64),
     (1, 2048, 32, 8, 128), (5, 70, 16, 1, 128),
+    # MFMA prefill path (bf16, >= 16 queries): ragged query count over a longer cache, GQA
+    # groups of 8, 4 and 1, a single tile
+    (200, 1000, 12, 2, 128), (33, 33, 16, 2, 128), (48, 48, 32, 8, 128), (17, 17, 4, 4, 128),
+    (16, 16, 12, 2, 128),
 ]
 
 
