@@ -391,15 +391,23 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaQ = 16;  // queries per block
 constexpr int kMfmaKT = 64; // keys per tile
+constexpr int kKtLd = 136;  // K tile row stride (bf16 elements; 16-byte rows, 4-bank skew)
 constexpr int kVtLd = 68;   // V^T row stride (bf16 elements; multiple of 4 for 8-byte reads)
 
 __device__ __forceinline__ bf16x8 asBf16x8(const v4u &r) { return __builtin_bit_cast(bf16x8, r); }
 
+// Tiles move HBM -> registers -> LDS with one tile of lookahead: while the waves compute on
+// tile t (in LDS buffer t % 2), every thread holds its share of tile t + 1 in registers and
+// writes it to the other buffer at the start of the next step, so the loads overlap the
+// MFMA work and a step needs one barrier.  K is stored as loaded (row-major), V transposed.
 template <int W>
 __global__ void __launch_bounds__(kWave * W)
     attnMfma(AttnArgs a) {
     constexpr int D = 128, KB = D / 32, DT = D / 16;
-    __shared__ uint16_t vt[D][kVtLd];
+    constexpr int kItems = kMfmaKT * (D / 8);                  // 16-byte pieces per tile
+    constexpr int kPer = (kItems + kWave * W - 1) / (kWave * W); // per thread
+    __shared__ uint16_t kt[2][kMfmaKT][kKtLd];
+    __shared__ uint16_t vt[2][D][kVtLd];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
     const int n = lane % 16, g4 = lane / 16;
@@ -415,6 +423,7 @@ __global__ void __launch_bounds__(kWave * W)
     const size_t qi = min(q0 + size_t(n), a.seq - 1); // this lane's query (clamped for loads)
     const size_t vis_q = visibleKeys(a.total, a.seq, qi);
     const size_t vis_blk = visibleKeys(a.total, a.seq, min(q0 + kMfmaQ - 1, a.seq - 1));
+    const size_t ntiles = (vis_blk + kMfmaKT - 1) / kMfmaKT;
     const size_t kstride = size_t(a.nkvh) * D; // elements between key rows
 
     bf16x8 qreg[KB];
@@ -430,30 +439,44 @@ __global__ void __launch_bounds__(kWave * W)
 
     const uint16_t *kbase = static_cast<const uint16_t *>(a.k) + size_t(g) * D;
     const uint16_t *vbase = static_cast<const uint16_t *>(a.v) + size_t(g) * D;
-    for (size_t kt0 = 0; kt0 < vis_blk; kt0 += kMfmaKT) {
-        // K operands of the tile: key kt0 + 16t + l % 16, columns 32kb + 8(l / 16) .. + 7
-        v4u kr[4][KB];
+    // this thread's pieces of a tile: piece idx -> key idx / 16, columns 8 (idx % 16) .. + 7
+    v4u kraw[kPer], vraw[kPer];
+    const auto loadTile = [&](size_t t0) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const size_t key = min(kt0 + 16 * t + n, a.total - 1);
-#pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-                kr[t][kb] = *reinterpret_cast<const v4u *>(kbase + key * kstride + 32 * kb + 8 * g4);
-        }
-        // V tile -> LDS, transposed (vt[d][key]); keys past the cache are zeros
-        __syncthreads(); // the previous tile's readers are done
-        for (int idx = threadIdx.x; idx < kMfmaKT * (D / 8); idx += kWave * W) {
-            const int dg = idx % (D / 8), kk = idx / (D / 8);
-            const size_t key = kt0 + size_t(kk);
-            v4u r = v4u{0u, 0u, 0u, 0u};
-            if (key < a.total) r = *reinterpret_cast<const v4u *>(vbase + key * kstride + 8 * dg);
-            const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vt[8 * dg + 2 * e][kk] = uint16_t(w[e] & 0xFFFFu);
-                vt[8 * dg + 2 * e + 1][kk] = uint16_t(w[e] >> 16);
+        for (int r = 0; r < kPer; ++r) {
+            const int idx = int(threadIdx.x) + r * kWave * W;
+            const size_t key = t0 + size_t(idx / (D / 8));
+            const int col = 8 * (idx % (D / 8));
+            kraw[r] = vraw[r] = v4u{0u, 0u, 0u, 0u}; // keys past the cache: zeros
+            if (idx < kItems && key < a.total) {
+                kraw[r] = *reinterpret_cast<const v4u *>(kbase + key * kstride + col);
+                vraw[r] = *reinterpret_cast<const v4u *>(vbase + key * kstride + col);
             }
         }
+    };
+    const auto storeTile = [&](int buf) {
+#pragma unroll
+        for (int r = 0; r < kPer; ++r) {
+            const int idx = int(threadIdx.x) + r * kWave * W;
+            if (idx >= kItems) continue;
+            const int kk = idx / (D / 8), col = 8 * (idx % (D / 8));
+            *reinterpret_cast<v4u *>(&kt[buf][kk][col]) = kraw[r];
+            const uint32_t w[4] = {vraw[r].x, vraw[r].y, vraw[r].z, vraw[r].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vt[buf][col + 2 * e][kk] = uint16_t(w[e] & 0xFFFFu);
+                vt[buf][col + 2 * e + 1][kk] = uint16_t(w[e] >> 16);
+            }
+        }
+    };
+
+    loadTile(0);
+    for (size_t ti = 0; ti < ntiles; ++ti) {
+        const int buf = int(ti & 1);
+        const size_t kt0 = ti * kMfmaKT;
+        storeTile(buf);
+        if (ti + 1 < ntiles) loadTile(kt0 + kMfmaKT); // in flight during this step's math
+        __syncthreads(); // tile ti in LDS; every wave is past the step that read buf last
         // scores S^T[key kt0 + 16t + 4g + i][query n]
         float p[4][4];
         float mx = m;
@@ -461,8 +484,10 @@ __global__ void __launch_bounds__(kWave * W)
         for (int t = 0; t < 4; ++t) {
             f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb)
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kr[t][kb]), qreg[kb], acc, 0, 0, 0);
+            for (int kb = 0; kb < KB; ++kb) {
+                const v4u kv = *reinterpret_cast<const v4u *>(&kt[buf][16 * t + n][32 * kb + 8 * g4]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kv), qreg[kb], acc, 0, 0, 0);
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const size_t key = kt0 + size_t(16 * t + 4 * g4 + i);
@@ -486,7 +511,6 @@ __global__ void __launch_bounds__(kWave * W)
         lsum = lsum * corr + ps;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
-        __syncthreads(); // V^T tile written
 #pragma unroll
         for (int p2 = 0; p2 < 2; ++p2) {
             bf16x8 bhi, blo;
@@ -499,7 +523,7 @@ __global__ void __launch_bounds__(kWave * W)
             }
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const uint16_t *row = &vt[16 * dt + n][32 * p2 + 4 * g4];
+                const uint16_t *row = &vt[buf][16 * dt + n][32 * p2 + 4 * g4];
                 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
                 const v2u lo4 = *reinterpret_cast<const v2u *>(row);
                 const v2u hi4 = *reinterpret_cast<const v2u *>(row + 16);
