@@ -377,35 +377,41 @@ __global__ void __launch_bounds__(kWave)
 
 // ---- prefill on MFMA (bf16, head_dim 128) ---------------------------------------------
 // One block per (16 queries, kv head, slice of W q heads), one wave per q head.  Per tile
-// of 64 keys a wave forms S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A = 16 key rows read
-// straight from memory, B = the wave's 16 queries kept in registers), so each lane holds
-// the scores of one query (column l % 16) for 16 of the keys and the softmax needs only an
-// exchange between the 4 lanes of that column; then O^T += V^T P^T with the same
-// instruction: P^T is the B operand as the lanes already hold it (k-slot 8g + j of a
-// lane group g is key 32p + 16(j / 4) + 4g + j % 4), V^T comes from a transposed copy of the
-// tile in LDS.  P enters as bf16 hi + lo parts (2^-17 relative), so the output keeps f32
-// accuracy.  Operand layouts (measured on MI355X): A[m = l % 16][k = 8(l / 16) + j],
+// of 64 keys a wave forms S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A = 16 key rows of
+// the tile, B = the wave's 16 queries kept in registers), so each lane holds the scores of
+// one query (column l % 16) for 16 of the keys and the softmax needs only an exchange
+// between the 4 lanes of that column; then O^T += V^T P^T with the same instruction.
+// Operand layouts (measured on MI355X): A[m = l % 16][k = 8(l / 16) + j],
 // B[k = 8(l / 16) + j][n = l % 16], D[m = 4(l / 16) + i][n = l % 16].
+// Key order: row m of score tile t (of 4) is key 32(t / 2) + 8(m / 4) + 4(t % 2) + m % 4,
+// so lane group g holds keys 32p + 8g .. + 7 of tiles 2p and 2p + 1 -- exactly the 8
+// consecutive k-slots 8g + j of the P V product for keys 32p .. 32p + 31, and the V^T
+// operand of those slots is one 16-byte LDS read.  P enters as bf16 hi + lo parts (2^-17
+// relative), so the output keeps f32 accuracy.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaQ = 16;  // queries per block
 constexpr int kMfmaKT = 64; // keys per tile
-constexpr int kKtLd = 136;  // K tile row stride (bf16 elements; 16-byte rows, 4-bank skew)
-constexpr int kVtLd = 68;   // V^T row stride (bf16 elements; multiple of 4 for 8-byte reads)
+constexpr int kKtLd = 136;  // K tile row stride (bf16): 16-byte rows, rows 4 banks apart
+constexpr int kVtLd = 72;   // V^T row stride (bf16): 16-byte reads; rows 8 apart 32 banks apart
 
 __device__ __forceinline__ bf16x8 asBf16x8(const v4u &r) { return __builtin_bit_cast(bf16x8, r); }
 
 // Tiles move HBM -> registers -> LDS with one tile of lookahead: while the waves compute on
 // tile t (in LDS buffer t % 2), every thread holds its share of tile t + 1 in registers and
 // writes it to the other buffer at the start of the next step, so the loads overlap the
-// MFMA work and a step needs one barrier.  K is stored as loaded (row-major), V transposed.
+// MFMA work and a step needs one barrier.  K is stored as loaded (row-major); V is stored
+// transposed from pairs of consecutive keys, one 4-byte write per column and pair (the 32
+// lanes of a pair of rows write 32 consecutive words, the other 32 lanes rows 32 banks on).
 template <int W>
 __global__ void __launch_bounds__(kWave * W)
     attnMfma(AttnArgs a) {
     constexpr int D = 128, KB = D / 32, DT = D / 16;
-    constexpr int kItems = kMfmaKT * (D / 8);                  // 16-byte pieces per tile
-    constexpr int kPer = (kItems + kWave * W - 1) / (kWave * W); // per thread
+    constexpr int kKItems = kMfmaKT * (D / 8);           // 16-byte K pieces per tile
+    constexpr int kVItems = (kMfmaKT / 2) * (D / 8);     // V pieces: 2 keys x 8 columns
+    constexpr int kKPer = (kKItems + kWave * W - 1) / (kWave * W);
+    constexpr int kVPer = (kVItems + kWave * W - 1) / (kWave * W);
     __shared__ uint16_t kt[2][kMfmaKT][kKtLd];
     __shared__ uint16_t vt[2][D][kVtLd];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
@@ -425,6 +431,7 @@ __global__ void __launch_bounds__(kWave * W)
     const size_t vis_blk = visibleKeys(a.total, a.seq, min(q0 + kMfmaQ - 1, a.seq - 1));
     const size_t ntiles = (vis_blk + kMfmaKT - 1) / kMfmaKT;
     const size_t kstride = size_t(a.nkvh) * D; // elements between key rows
+    const float c2 = a.scale * 1.4426950408889634f; // scores to base-2 exponents
 
     bf16x8 qreg[KB];
 #pragma unroll
@@ -432,40 +439,57 @@ __global__ void __launch_bounds__(kWave * W)
         const uint16_t *qp = static_cast<const uint16_t *>(a.q) + (qi * a.nh + h) * D + 32 * kb + 8 * g4;
         qreg[kb] = asBf16x8(*reinterpret_cast<const v4u *>(qp));
     }
-    float m = -INFINITY, lsum = 0.0f;
+    float m = -INFINITY, lsum = 0.0f; // m: running max of the raw dots (scaled by c2 in use)
     f32x4 o[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     const uint16_t *kbase = static_cast<const uint16_t *>(a.k) + size_t(g) * D;
     const uint16_t *vbase = static_cast<const uint16_t *>(a.v) + size_t(g) * D;
-    // this thread's pieces of a tile: piece idx -> key idx / 16, columns 8 (idx % 16) .. + 7
-    v4u kraw[kPer], vraw[kPer];
+    v4u kraw[kKPer], vraw[kVPer][2];
     const auto loadTile = [&](size_t t0) {
+        const size_t left = a.total - t0; // keys of the cache from t0 on (> 0)
 #pragma unroll
-        for (int r = 0; r < kPer; ++r) {
+        for (int r = 0; r < kKPer; ++r) {
             const int idx = int(threadIdx.x) + r * kWave * W;
-            const size_t key = t0 + size_t(idx / (D / 8));
-            const int col = 8 * (idx % (D / 8));
-            kraw[r] = vraw[r] = v4u{0u, 0u, 0u, 0u}; // keys past the cache: zeros
-            if (idx < kItems && key < a.total) {
-                kraw[r] = *reinterpret_cast<const v4u *>(kbase + key * kstride + col);
-                vraw[r] = *reinterpret_cast<const v4u *>(vbase + key * kstride + col);
+            const int kk = idx / (D / 8), col = 8 * (idx % (D / 8));
+            kraw[r] = v4u{0u, 0u, 0u, 0u}; // keys past the cache: zeros
+            if (idx < kKItems && size_t(kk) < left)
+                kraw[r] = *reinterpret_cast<const v4u *>(kbase + (t0 + kk) * kstride + col);
+        }
+#pragma unroll
+        for (int r = 0; r < kVPer; ++r) {
+            const int idx = int(threadIdx.x) + r * kWave * W;
+            const int kp = idx % (kMfmaKT / 2), col = 8 * (idx / (kMfmaKT / 2));
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                vraw[r][e] = v4u{0u, 0u, 0u, 0u};
+                if (idx < kVItems && size_t(2 * kp + e) < left)
+                    vraw[r][e] = *reinterpret_cast<const v4u *>(vbase + (t0 + 2 * kp + e) * kstride + col);
             }
         }
     };
     const auto storeTile = [&](int buf) {
 #pragma unroll
-        for (int r = 0; r < kPer; ++r) {
+        for (int r = 0; r < kKPer; ++r) {
             const int idx = int(threadIdx.x) + r * kWave * W;
-            if (idx >= kItems) continue;
-            const int kk = idx / (D / 8), col = 8 * (idx % (D / 8));
-            *reinterpret_cast<v4u *>(&kt[buf][kk][col]) = kraw[r];
-            const uint32_t w[4] = {vraw[r].x, vraw[r].y, vraw[r].z, vraw[r].w};
+            if (idx < kKItems)
+                *reinterpret_cast<v4u *>(&kt[buf][idx / (D / 8)][8 * (idx % (D / 8))]) = kraw[r];
+        }
+#pragma unroll
+        for (int r = 0; r < kVPer; ++r) {
+            const int idx = int(threadIdx.x) + r * kWave * W;
+            if (idx >= kVItems) continue;
+            const int kp = idx % (kMfmaKT / 2), col = 8 * (idx / (kMfmaKT / 2));
+            const uint32_t w0[4] = {vraw[r][0].x, vraw[r][0].y, vraw[r][0].z, vraw[r][0].w};
+            const uint32_t w1[4] = {vraw[r][1].x, vraw[r][1].y, vraw[r][1].z, vraw[r][1].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                vt[buf][col + 2 * e][kk] = uint16_t(w[e] & 0xFFFFu);
-                vt[buf][col + 2 * e + 1][kk] = uint16_t(w[e] >> 16);
+                // columns col + 2e (low halves) and col + 2e + 1 (high halves) of keys 2kp, 2kp + 1
+                *reinterpret_cast<uint32_t *>(&vt[buf][col + 2 * e][2 * kp]) =
+                    __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
+                *reinterpret_cast<uint32_t *>(&vt[buf][col + 2 * e + 1][2 * kp]) =
+                    __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
             }
         }
     };
@@ -477,59 +501,62 @@ __global__ void __launch_bounds__(kWave * W)
         storeTile(buf);
         if (ti + 1 < ntiles) loadTile(kt0 + kMfmaKT); // in flight during this step's math
         __syncthreads(); // tile ti in LDS; every wave is past the step that read buf last
-        // scores S^T[key kt0 + 16t + 4g + i][query n]
+        // keys of this lane's query visible in the tile: offsets < nvis
+        const int nvis = int(min(vis_q - min(vis_q, kt0), size_t(kMfmaKT)));
         float p[4][4];
         float mx = m;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
+            const int krow = 32 * (t / 2) + 8 * (n / 4) + 4 * (t % 2) + n % 4; // A row n
             f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) {
-                const v4u kv = *reinterpret_cast<const v4u *>(&kt[buf][16 * t + n][32 * kb + 8 * g4]);
+                const v4u kv = *reinterpret_cast<const v4u *>(&kt[buf][krow][32 * kb + 8 * g4]);
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kv), qreg[kb], acc, 0, 0, 0);
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const size_t key = kt0 + size_t(16 * t + 4 * g4 + i);
-                p[t][i] = key < vis_q ? acc[i] * a.scale : -INFINITY;
+                const int off = 32 * (t / 2) + 8 * g4 + 4 * (t % 2) + i; // key of D row 4g + i
+                p[t][i] = off < nvis ? acc[i] : -INFINITY;
                 mx = fmaxf(mx, p[t][i]);
             }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
         // key 0 is visible to every query, so m is finite after the first tile
-        const float corr = mx == m ? 1.0f : __expf(m - mx);
-        m = mx;
+        const float mc = mx * c2;
         float ps = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                p[t][i] = p[t][i] == -INFINITY ? 0.0f : __expf(p[t][i] - mx);
+                // exp(scale * (s - max)) as 2^(s * c2 - max * c2); a masked key is weight 0
+                p[t][i] = p[t][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][i], c2, -mc));
                 ps += p[t][i];
             }
-        lsum = lsum * corr + ps;
+        if (__builtin_expect(__any(mx != m), 0)) { // rescale only when a max moved
+            const float corr = mx == m ? 1.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m, c2, -mc));
+            lsum *= corr;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+        }
+        m = mx;
+        lsum += ps;
 #pragma unroll
         for (int p2 = 0; p2 < 2; ++p2) {
             bf16x8 bhi, blo;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float x = p[2 * p2 + j / 4][j % 4];
+                const float x = p[2 * p2 + j / 4][j % 4]; // key 32 p2 + 8g + j
                 const __bf16 hi = __bf16(x);
                 bhi[j] = hi;
                 blo[j] = __bf16(x - float(hi));
             }
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const uint16_t *row = &vt[buf][16 * dt + n][32 * p2 + 4 * g4];
-                typedef uint32_t v2u __attribute__((ext_vector_type(2)));
-                const v2u lo4 = *reinterpret_cast<const v2u *>(row);
-                const v2u hi4 = *reinterpret_cast<const v2u *>(row + 16);
-                const bf16x8 av = __builtin_bit_cast(bf16x8, v4u{lo4.x, lo4.y, hi4.x, hi4.y});
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bhi, o[dt], 0, 0, 0);
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, blo, o[dt], 0, 0, 0);
+                const v4u vv = *reinterpret_cast<const v4u *>(&vt[buf][16 * dt + n][32 * p2 + 8 * g4]);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vv), bhi, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vv), blo, o[dt], 0, 0, 0);
             }
         }
     }
@@ -590,7 +617,9 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
     // types stay on the vector kernel
     if constexpr (std::is_same_v<T, BF16> && !kInt8) {
         const size_t mblocks = (a.seq + kMfmaQ - 1) / kMfmaQ * size_t(a.nkvh) * size_t(a.slices);
-        if (d == 128 && a.total > 0 && a.seq >= size_t(kMfmaQ) && mblocks < (size_t(1) << 31)) {
+        // (the MFMA kernel tracks the max of the raw dot products: valid for a positive scale)
+        if (d == 128 && a.total > 0 && a.seq >= size_t(kMfmaQ) && mblocks < (size_t(1) << 31) &&
+            a.scale > 0.0f && std::isfinite(a.scale)) {
             a.nchunks = 1;
             switch (G) {
             case 8: attnMfma<8><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;

@@ -70,6 +70,16 @@ def test_self_attention_golden_on_gpu(golden):
     assert n == 18
 
 
+@pytest.mark.parametrize("scale", [-0.2, 0.0, 3.0])
+def test_self_attention_unusual_scales(scale):
+    """Any scale the reference accepts (negative flips the softmax, 0 gives the mean of the
+    visible values); prefill shape, so a positive one takes the MFMA kernel."""
+    rng = np.random.default_rng(77)
+    q, k, v = sample(rng, (40, 12, 128), "bf16"), sample(rng, (40, 2, 128), "bf16"), sample(rng, (40, 2, 128), "bf16")
+    got = attend(q, k, v, scale, "bf16")
+    assert_attention_close(got, oracle.self_attention(q, k, v, scale), v, f"scale {scale}")
+
+
 def test_self_attention_empty_cache_gives_zeros():
     q = f32_to_bf16(np.ones((2, 4, 128), np.float32))
     out = L.Tensor((2, 4, 128), L.DataType.BF16, **AMD)
