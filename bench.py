@@ -371,6 +371,35 @@ def attention_ops(L, rng):
     return ops, P
 
 
+def measure_attention(L, hip, stream, e0, e1, steps):
+    """Times the attention_ops cases (HIP events on the library stream)."""
+    print("bench: building attention buffers", file=sys.stderr, flush=True)
+    aops, apool = attention_ops(L, np.random.default_rng(11))
+    res = {}
+    for name, kind, amount, fn in aops:
+        for i in range(3):
+            fn(i)
+        reps = max(steps // 2, 10)
+        hip.record(e0, stream)
+        for i in range(reps):
+            fn(i)
+        hip.record(e1, stream)
+        us = hip.elapsed_ms(e0, e1) / reps * 1e3
+        if kind == "bytes":
+            gbs = amount / (us * 1e-6) / 1e9
+            res[name] = {"us": round(us, 3), "bytes": amount, "GB_s": round(gbs, 1),
+                         "frac_peak": round(gbs / PEAK_GBS, 4), "bound": "hbm"}
+        else:
+            tf = amount / (us * 1e-6) / 1e12
+            res[name] = {"us": round(us, 3), "flops": amount, "TFLOP_s": round(tf, 2),
+                         "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                         "bound": "mfma (bf16 dense peak)"}
+    assert L.take_device_error() == 0
+    del aops, apool
+    print("bench: attention " + json.dumps(res), file=sys.stderr, flush=True)
+    return res
+
+
 def cpu_baseline(seconds):
     """Reference CPU ops (oracle/_ref, else the oracle port) on a row sample of config 1,
     single thread pinned to one core; GB/s with the same bytes formula as the GPU."""
@@ -479,6 +508,8 @@ def main():
     ap.add_argument("--no-chain", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip configs 0, 2 and 3")
     ap.add_argument("--no-attention", action="store_true", help="skip the self-attention lines")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the self-attention lines (profiling); prints their JSON")
     ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain (profiling)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="3 dispatches of a 256 MiB device copy (counter calibration), then 3 of "
@@ -502,6 +533,10 @@ def main():
         for _ in range(args.steps):
             graph.launch()
         api.device_synchronize()
+        return
+    if args.attention_only:
+        print(json.dumps({"attention": measure_attention(L, hip, stream, e0=hip.event(), e1=hip.event(),
+                                                         steps=args.steps)}), flush=True)
         return
     print("bench: building config-1 buffers", file=sys.stderr, flush=True)
     wl = Workload(L)
@@ -614,30 +649,7 @@ def main():
 
     attention = None
     if not args.no_attention:
-        print("bench: building attention buffers", file=sys.stderr, flush=True)
-        aops, apool = attention_ops(L, np.random.default_rng(11))
-        attention = {}
-        for name, kind, amount, fn in aops:
-            for i in range(3):
-                fn(i)
-            reps = max(args.steps // 2, 10)
-            hip.record(e0, stream)
-            for i in range(reps):
-                fn(i)
-            hip.record(e1, stream)
-            us = hip.elapsed_ms(e0, e1) / reps * 1e3
-            if kind == "bytes":
-                gbs = amount / (us * 1e-6) / 1e9
-                attention[name] = {"us": round(us, 3), "bytes": amount, "GB_s": round(gbs, 1),
-                                   "frac_peak": round(gbs / PEAK_GBS, 4), "bound": "hbm"}
-            else:
-                tf = amount / (us * 1e-6) / 1e12
-                attention[name] = {"us": round(us, 3), "flops": amount, "TFLOP_s": round(tf, 2),
-                                   "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4),
-                                   "bound": "mfma (bf16 dense peak)"}
-        assert L.take_device_error() == 0
-        del aops, apool
-        print("bench: attention " + json.dumps(attention), file=sys.stderr, flush=True)
+        attention = measure_attention(L, hip, stream, e0, e1, args.steps)
 
     dom = per_op["swiglu"]
     roof = {"kernel": "swiglu binaryVec<BF16> [8192, 8960]", "bound": "hbm",

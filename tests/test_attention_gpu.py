@@ -80,6 +80,23 @@ def test_self_attention_unusual_scales(scale):
     assert_attention_close(got, oracle.self_attention(q, k, v, scale), v, f"scale {scale}")
 
 
+def test_prefill_is_deterministic():
+    """Repeated prefill launches, interleaved with other attention shapes (which reuse the
+    library workspace), give bit-identical outputs."""
+    rng = np.random.default_rng(8)
+    q, k, v = sample(rng, (512, 12, 128), "bf16"), sample(rng, (512, 2, 128), "bf16"), sample(rng, (512, 2, 128), "bf16")
+    tq, tk, tv = dev(q, L.DataType.BF16), dev(k, L.DataType.BF16), dev(v, L.DataType.BF16)
+    outs = []
+    for rep in range(4):
+        out = L.Tensor((512, 12, 128), L.DataType.BF16, **AMD)
+        L.Ops.self_attention(out, tq, tk, tv, 0.088)
+        outs.append(out.numpy())
+        attend(q[:64], k[:300], v[:300], 0.1, "bf16")  # another shape in between
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    assert_attention_close(outs[0], oracle.self_attention(q, k, v, 0.088), v, "prefill 512")
+
+
 def test_self_attention_empty_cache_gives_zeros():
     q = f32_to_bf16(np.ones((2, 4, 128), np.float32))
     out = L.Tensor((2, 4, 128), L.DataType.BF16, **AMD)

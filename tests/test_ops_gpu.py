@@ -16,7 +16,7 @@ import pytest
 import llaisys_amd as L
 import oracle
 from llaisys_amd.hostfmt import bf16_to_f32, f32_to_bf16
-from numerics import assert_close, assert_exact
+from numerics import assert_attention_close, assert_close, assert_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -83,6 +83,11 @@ def test_golden_vectors_on_gpu(golden):
             L.Ops.argmax(i, v, dev(c["vals"], DTS[dt]))
             assert_exact(i.numpy(), c["idx"], what)
             assert_exact(v.numpy(), c["val"], what)
+        elif op == "self_attention":
+            out = empty(c["out"].shape, DTS[dt])
+            L.Ops.self_attention(out, dev(c["q"], DTS[dt]), dev(c["k"], DTS[dt]), dev(c["v"], DTS[dt]),
+                                 float(c["scale"]))
+            assert_attention_close(out.numpy(), c["out"], c["v"], what)
         else:
             continue
         checked += 1
