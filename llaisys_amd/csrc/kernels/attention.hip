@@ -285,32 +285,16 @@ __global__ void __launch_bounds__(kCombineThreads)
     attnCombine(void *out, const float *part, int nchunks, int D) {
     __shared__ float w[1024];  // per-chunk factor exp(m_c - M), nchunks <= 1024
     __shared__ float red[kCombineThreads];
-    __shared__ float MM, LL;
+    __shared__ float wred[kCombineThreads / kWave];
     const size_t ih = blockIdx.x; // i * nh + h
     const float *pp = part + ih * size_t(nchunks) * (D + 2);
     const int t = threadIdx.x;
-    float mc = -INFINITY;
-    if (t < nchunks) mc = pp[size_t(t) * (D + 2) + D];
-    red[t] = mc;
-    __syncthreads();
-    if (t == 0) {
-        float M = -INFINITY;
-        for (int k = 0; k < nchunks; ++k) M = fmaxf(M, red[k]);
-        MM = M;
-    }
-    __syncthreads();
-    const float M = MM;
-    if (t < nchunks) {
-        const float f = mc == M ? 1.0f : __expf(mc - M); // mc = -inf: l = o = 0
-        w[t] = f;
-        red[t] = pp[size_t(t) * (D + 2) + D + 1] * f;
-    }
-    __syncthreads();
-    if (t == 0) {
-        float L = 0.0f;
-        for (int k = 0; k < nchunks; ++k) L += red[k];
-        LL = L;
-    }
+    const float mc = t < nchunks ? pp[size_t(t) * (D + 2) + D] : -INFINITY;
+    const float lc = t < nchunks ? pp[size_t(t) * (D + 2) + D + 1] : 0.0f;
+    const float M = groupReduce<kCombineThreads, MaxOp>(mc, wred); // every thread gets it
+    const float f = mc == M ? 1.0f : __expf(mc - M);                // mc = -inf: l = o = 0
+    if (t < nchunks) w[t] = f;
+    const float L = groupReduce<kCombineThreads, SumOp>(t < nchunks ? lc * f : 0.0f, wred);
     __syncthreads();
     const int parts = kCombineThreads / D;
     const int e = t % D, pidx = t / D;
@@ -324,7 +308,6 @@ __global__ void __launch_bounds__(kCombineThreads)
     if (t < D) {
         float O = 0.0f;
         for (int k = 0; k < parts; ++k) O += red[k * D + t];
-        const float L = LL;
         Fmt<T>::put(out, ih * D + t, L > 0.0f ? O / L : 0.0f);
     }
 }
@@ -575,6 +558,234 @@ __global__ void __launch_bounds__(kWave * W)
     }
 }
 
+// ---- decode on MFMA (bf16 q / out, head_dim 128, cache in bf16 or INT8) ---------------
+// Few queries, long cache.  Block = (query, kv head, key chunk), 4 waves; each wave takes
+// 32-key steps of the chunk on its own.  The MFMA columns are the G (<= 16) q heads of the
+// kv head (columns past G hold zero queries and are never written): S^T = K Q^T over 2
+// tiles of 16 keys (row m of tile t is key 8(m / 4) + 4t + m % 4, so lane group g holds keys
+// 8g .. 8g + 7 and P^T is the B operand of one 32-key P V product as the lanes hold it),
+// then O^T += V^T P^T with V^T staged through the wave's own LDS slice (no block barrier
+// inside the loop).  K enters the A operand straight from memory: bf16 rows, or INT8 codes
+// turned into bf16(code * scale) (codesToBf16) with the step's scales shared by shuffles.  The waves merge in LDS; a split launch writes chunk partials in
+// the layout attnCombine merges (max in scaled units).
+constexpr int kDecWaves = 4;
+constexpr int kDecKT = 32;   // keys per wave step
+constexpr int kDecVtLd = 40; // V^T row stride (bf16): 16-byte reads of rows 16 apart hit distinct banks
+
+// 8 consecutive elements of a cache row (128 per row) as raw bits: bf16 (16 bytes) or INT8
+// codes (8 bytes, in .x / .y).
+template <bool kInt8>
+__device__ __forceinline__ v4u loadRow8(const void *base, size_t row, int col) {
+    if constexpr (kInt8) {
+        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+        const v2u c = *reinterpret_cast<const v2u *>(static_cast<const int8_t *>(base) + row * 128 + col);
+        return v4u{c.x, c.y, 0u, 0u};
+    } else {
+        return *reinterpret_cast<const v4u *>(static_cast<const uint16_t *>(base) + row * 128 + col);
+    }
+}
+
+// 8 INT8 codes -> bf16(code * sc) as 4 packed words.  code = u - 128 for the unsigned byte
+// u of code ^ 0x80, and fma(u, sc, -128 sc) rounds u * sc - 128 sc = code * sc once (-128 sc
+// is exact), i.e. exactly float(code) * sc; the pair conversion then rounds to bf16 as the
+// reference does for every non-NaN value.
+__device__ __forceinline__ v4u codesToBf16(const v4u &raw, float sc) {
+    const uint32_t ux = raw.x ^ 0x80808080u, uy = raw.y ^ 0x80808080u;
+    const float off = -128.0f * sc;
+    const auto cv = [&](uint32_t u, int k) {
+        const float b = float((u >> (8 * k)) & 0xFFu); // v_cvt_f32_ubyte{k}
+        return __builtin_fmaf(b, sc, off);
+    };
+    return v4u{Bf16Cvt::narrow2Q(cv(ux, 0), cv(ux, 1)), Bf16Cvt::narrow2Q(cv(ux, 2), cv(ux, 3)),
+               Bf16Cvt::narrow2Q(cv(uy, 0), cv(uy, 1)), Bf16Cvt::narrow2Q(cv(uy, 2), cv(uy, 3))};
+}
+
+template <bool kInt8>
+__global__ void __launch_bounds__(kWave * kDecWaves)
+    attnDecodeMfma(AttnArgs a) {
+    constexpr int D = 128, KB = D / 32, DT = D / 16;
+    __shared__ uint16_t vt[kDecWaves][D][kDecVtLd];
+    __shared__ float st[kDecWaves][16][D + 2];
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = int(threadIdx.x) % kWave;
+    const int n = lane % 16, g4 = lane / 16;
+
+    unsigned b = blockIdx.x;
+    const int c = int(b % unsigned(a.nchunks));
+    b /= unsigned(a.nchunks);
+    const int g = int(b % unsigned(a.nkvh));
+    const size_t i = a.seq - 1 - size_t(b / unsigned(a.nkvh));
+    const size_t vis = visibleKeys(a.total, a.seq, i);
+    const size_t k0 = size_t(c) * size_t(a.chunk);
+    const size_t k1 = min(vis, k0 + size_t(a.chunk));
+    const bool col_ok = n < a.group;
+    const int hq = g * a.group + (col_ok ? n : 0); // this column's q head (clamped)
+    const float c2 = a.scale * 1.4426950408889634f;
+    const size_t rstride = size_t(a.nkvh);          // rows between keys
+
+    bf16x8 qreg[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        v4u r = v4u{0u, 0u, 0u, 0u};
+        if (col_ok)
+            r = *reinterpret_cast<const v4u *>(static_cast<const uint16_t *>(a.q) + (i * a.nh + hq) * D + 32 * kb + 8 * g4);
+        qreg[kb] = asBf16x8(r);
+    }
+    float m = -INFINITY, lsum = 0.0f; // m: max of the raw dots
+    f32x4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (size_t kt0 = k0 + size_t(wave) * kDecKT; kt0 < k1; kt0 += size_t(kDecWaves) * kDecKT) {
+        const int nk = int(min(k1 - kt0, size_t(kDecKT)));
+        // V pieces: lane takes pairs (2kp, 2kp + 1) x 8 columns dc .. dc + 7, 4 per lane
+        v4u vr[4][2];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int idx = lane + kWave * r, kp = idx % 16, dc = 8 * (idx / 16);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                vr[r][e] = v4u{0u, 0u, 0u, 0u}; // keys past the step: zeros
+                if (2 * kp + e < nk) vr[r][e] = loadRow8<kInt8>(a.v, (kt0 + 2 * kp + e) * rstride + g, dc);
+            }
+        }
+        // K operands: tile t, row n -> key 8(n / 4) + 4t + n % 4
+        v4u ka[2][KB];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int off = 8 * (n / 4) + 4 * t + n % 4;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                ka[t][kb] = v4u{0u, 0u, 0u, 0u};
+                if (off < nk) ka[t][kb] = loadRow8<kInt8>(a.k, (kt0 + off) * rstride + g, 32 * kb + 8 * g4);
+            }
+        }
+        if constexpr (kInt8) {
+            // the step's scales, one load per lane (K for lanes 0-31, V for 32-63), handed
+            // to the lanes that convert a row by lane shuffles
+            const int sk = lane % kDecKT;
+            float sreg = 0.0f;
+            if (sk < nk) sreg = (lane < kDecKT ? a.ks : a.vs)[(kt0 + sk) * rstride + g];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float sc = __shfl(sreg, 8 * (n / 4) + 4 * t + n % 4, kWave);
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb) ka[t][kb] = codesToBf16(ka[t][kb], sc);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kp = (lane + kWave * r) % 16;
+#pragma unroll
+                for (int e = 0; e < 2; ++e) vr[r][e] = codesToBf16(vr[r][e], __shfl(sreg, kDecKT + 2 * kp + e, kWave));
+            }
+        }
+        float p[2][4];
+        float mx = m;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(ka[t][kb]), qreg[kb], acc, 0, 0, 0);
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                p[t][ii] = 8 * g4 + 4 * t + ii < nk ? acc[ii] : -INFINITY; // key of D row 4g + ii
+                mx = fmaxf(mx, p[t][ii]);
+            }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float mc = mx * c2;
+        float ps = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                p[t][ii] = p[t][ii] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][ii], c2, -mc));
+                ps += p[t][ii];
+            }
+        if (__builtin_expect(__any(mx != m), 0)) {
+            const float corr = mx == m ? 1.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m, c2, -mc));
+            lsum *= corr;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+        }
+        m = mx;
+        lsum += ps;
+        // V^T into this wave's slice (the previous step's reads of it are done: one wave,
+        // in order; the fences keep the compiler from moving accesses across)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int idx = lane + kWave * r, kp = idx % 16, dc = 8 * (idx / 16);
+            const uint32_t w0[4] = {vr[r][0].x, vr[r][0].y, vr[r][0].z, vr[r][0].w};
+            const uint32_t w1[4] = {vr[r][1].x, vr[r][1].y, vr[r][1].z, vr[r][1].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                *reinterpret_cast<uint32_t *>(&vt[wave][dc + 2 * e][2 * kp]) = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
+                *reinterpret_cast<uint32_t *>(&vt[wave][dc + 2 * e + 1][2 * kp]) = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        bf16x8 bhi, blo;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float x = p[j / 4][j % 4]; // key 8g + j
+            const __bf16 hi = __bf16(x);
+            bhi[j] = hi;
+            blo[j] = __bf16(x - float(hi));
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const v4u vv = *reinterpret_cast<const v4u *>(&vt[wave][16 * dt + n][8 * g4]);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vv), bhi, o[dt], 0, 0, 0);
+            o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vv), blo, o[dt], 0, 0, 0);
+        }
+    }
+    float lt = lsum + __shfl_xor(lsum, 16, kWave);
+    lt += __shfl_xor(lt, 32, kWave);
+    if (col_ok) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) st[wave][n][16 * dt + 4 * g4 + ii] = o[dt][ii];
+        if (g4 == 0) {
+            st[wave][n][D] = m;
+            st[wave][n][D + 1] = lt;
+        }
+    }
+    __syncthreads();
+    for (int pi = threadIdx.x; pi < a.group * D; pi += kWave * kDecWaves) {
+        const int j = pi / D, e = pi % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, st[w][j][D]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDecWaves; ++w) {
+            const float mw = st[w][j][D];
+            const float f = mw == M ? 1.0f : __builtin_amdgcn_exp2f((mw - M) * c2); // 1 for M = -inf, where l = o = 0
+            L += st[w][j][D + 1] * f;
+            O += st[w][j][e] * f;
+        }
+        const size_t ih = i * a.nh + size_t(g * a.group + j);
+        if (a.nchunks == 1) {
+            Fmt<BF16>::put(a.out, ih * D + e, L > 0.0f ? O / L : 0.0f);
+        } else {
+            float *pp = a.part + (ih * size_t(a.nchunks) + c) * (D + 2);
+            pp[e] = O;
+            if (e == 0) {
+                pp[D] = M * a.scale; // the scaled units attnCombine works in
+                pp[D + 1] = L;
+            }
+        }
+    }
+}
+
 // Heads per wave for a kv group: the largest supported count that divides it.
 int sliceOf(int group) {
     for (int g : {8, 6, 4, 2})
@@ -628,6 +839,25 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
             case 2: attnMfma<2><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
             default: attnMfma<1><<<unsigned(mblocks), kWave, 0, s>>>(a); return;
             }
+        }
+    }
+    // bf16 decode (fewer than 16 queries): the MFMA decode kernel, one 32-key step per wave
+    // when the chunks allow (up to 1024 per (query, head), partials within the workspace)
+    if constexpr (std::is_same_v<T, BF16>) {
+        if (d == 128 && a.total > 0 && a.seq < size_t(kMfmaQ) && a.group <= 16 && a.scale > 0.0f &&
+            std::isfinite(a.scale)) {
+            const size_t bk = size_t(kDecWaves) * kDecKT; // keys per block step
+            const size_t pairs = a.seq * size_t(a.nh);
+            size_t nchunks = std::min<size_t>((a.total + bk - 1) / bk, 1024);
+            nchunks = std::max<size_t>(1, std::min(nchunks, ws_bytes / (size_t(d + 2) * sizeof(float) * pairs)));
+            a.nchunks = int(nchunks);
+            a.chunk = int(std::min<size_t>((a.total + nchunks - 1) / nchunks, size_t(INT32_MAX)));
+            a.part = static_cast<float *>(ws);
+            const unsigned blocks = unsigned(a.seq * size_t(a.nkvh) * nchunks);
+            attnDecodeMfma<kInt8><<<blocks, kWave * kDecWaves, 0, s>>>(a);
+            if (nchunks > 1)
+                attnCombine<T><<<unsigned(pairs), kCombineThreads, 0, s>>>(a.out, a.part, a.nchunks, d);
+            return;
         }
     }
     // A block's waves each take one step of keys per chunk when the launch is split: about
