@@ -45,6 +45,8 @@ def lib():
             "orc_kv_append_int8": [P, P, c_size_t, P, c_size_t, c_size_t, c_size_t, c_size_t, c_int],
             "orc_self_attention": [P, P, P, P, c_size_t, c_size_t, c_size_t, c_size_t, c_size_t,
                                    c_size_t, c_float, c_int],
+            "orc_linear": [P, P, P, P, c_size_t, c_size_t, c_size_t, c_int],
+            "orc_linear_w8a16": [P, P, P, P, P, c_size_t, c_size_t, c_size_t, c_int],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -191,3 +193,28 @@ def self_attention_int8kv(q, k_codes, k_scale, v_codes, v_scale, scale):
     k = dequantize_int8(k_codes, k_scale, q.dtype)
     v = dequantize_int8(v_codes, v_scale, q.dtype)
     return self_attention(q, k, v, scale)
+
+
+def linear(x, w, bias=None):
+    """Reference linear (linear_cpu.cpp:11-41): x [rows, in], w [out, in], bias [out]."""
+    x, w = _c(x), _c(w)
+    rows, in_f = x.shape
+    out_f = w.shape[0]
+    assert w.shape == (out_f, in_f) and x.dtype == w.dtype
+    b = None if bias is None else _c(bias)
+    out = np.empty((rows, out_f), dtype=x.dtype)
+    lib().orc_linear(_p(out), _p(x), _p(w), None if b is None else _p(b), rows, in_f, out_f, _code(x))
+    return out
+
+
+def linear_w8a16(x, codes, scale, bias=None):
+    """W8A16 rule: T(scale[n] * sum_k x[m, k] * codes[n, k] + bias[n])."""
+    x, codes = _c(x), np.ascontiguousarray(codes, dtype=np.int8)
+    scale = np.ascontiguousarray(scale, dtype=np.float32)
+    rows, in_f = x.shape
+    out_f = codes.shape[0]
+    b = None if bias is None else _c(bias)
+    out = np.empty((rows, out_f), dtype=x.dtype)
+    lib().orc_linear_w8a16(_p(out), _p(x), _p(codes), _p(scale), None if b is None else _p(b), rows,
+                           in_f, out_f, _code(x))
+    return out

@@ -344,3 +344,32 @@ int orc_self_attention(void *out, const void *q, const void *k, const void *v, s
     free(scores);
     return 0;
 }
+
+/* ---- linear: src/ops/linear/cpu/linear_cpu.cpp:11-41 -------------------------------
+ * out[m][n] = T(sum_k x[m][k] * w[n][k] (left to right, f32) + bias[n]) for x [rows, in],
+ * w [out, in], bias [out] or NULL. */
+void orc_linear(void *out, const void *x, const void *w, const void *bias, size_t rows,
+                size_t in_f, size_t out_f, int dt) {
+    for (size_t m = 0; m < rows; m++)
+        for (size_t n = 0; n < out_f; n++) {
+            float sum = 0.0f;
+            for (size_t k = 0; k < in_f; k++) sum += ld(x, m * in_f + k, dt) * ld(w, n * in_f + k, dt);
+            if (bias) sum += ld(bias, n, dt);
+            st(out, m * out_f + n, dt, sum);
+        }
+}
+
+/* W8A16 linear over INT8 weights (no reference kernel; the rule of llaisysLinearW8A16):
+ * out[m][n] = T(scale[n] * (sum_k x[m][k] * code[n][k], left to right in f32) + bias[n]).
+ * Each product of a bf16 / f16 activation and an INT8 code is exact in f32. */
+void orc_linear_w8a16(void *out, const void *x, const int8_t *code, const float *scale,
+                      const void *bias, size_t rows, size_t in_f, size_t out_f, int dt) {
+    for (size_t m = 0; m < rows; m++)
+        for (size_t n = 0; n < out_f; n++) {
+            float sum = 0.0f;
+            for (size_t k = 0; k < in_f; k++) sum += ld(x, m * in_f + k, dt) * (float)code[n * in_f + k];
+            sum = scale[n] * sum;
+            if (bias) sum += ld(bias, n, dt);
+            st(out, m * out_f + n, dt, sum);
+        }
+}

@@ -54,4 +54,12 @@ int orc_self_attention(void *out, const void *q, const void *k, const void *v, s
                        size_t total, size_t nh, size_t nkvh, size_t d, size_t dv, float scale,
                        int dtype);
 
+/* linear_cpu.cpp:11-41 (bias may be NULL) */
+void orc_linear(void *out, const void *x, const void *w, const void *bias, size_t rows,
+                size_t in_features, size_t out_features, int dtype);
+/* W8A16 rule: T(scale[n] * sum_k x * code + bias[n]) */
+void orc_linear_w8a16(void *out, const void *x, const int8_t *code, const float *scale,
+                      const void *bias, size_t rows, size_t in_features, size_t out_features,
+                      int dtype);
+
 #endif

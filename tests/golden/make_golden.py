@@ -173,6 +173,27 @@ def main():
             g.update({f"{key}/q": q, f"{key}/k": k, f"{key}/v": v, f"{key}/scale": scale,
                       f"{key}/out": out.numpy()})
 
+    # linear: the reference test's small shape (x scale 0.1, w scale 0.01, bias N(0, 1)),
+    # a Qwen2 row block with and without bias (the reference's "no bias" is a bias tensor
+    # with no elements, op.cpp:22), and an odd in_features.  Own seed sequence.
+    li_seed = [0]
+
+    def li_rng():
+        li_seed[0] += 1
+        return np.random.default_rng(7000 + li_seed[0])
+
+    for dt in ("f32", "bf16", "f16"):
+        for rows, in_f, out_f, use_bias in ((2, 4, 3, True), (16, 1536, 64, True), (5, 96, 40, False),
+                                            (3, 77, 9, True)):
+            r = li_rng()
+            x = sample(r, (rows, in_f), dt, 0.1)
+            w = sample(r, (out_f, in_f), dt, 0.01)
+            b = sample(r, (out_f,), dt) if use_bias else sample(r, (0,), dt)
+            out = R.empty((rows, out_f), DT[dt])
+            lib.llaisysLinear(out.lib_tensor(), R.h(x, DT[dt]), R.h(w, DT[dt]), R.h(b, DT[dt]))
+            key = f"linear/{dt}/{rows}x{in_f}x{out_f}{'b' if use_bias else ''}"
+            g.update({f"{key}/x": x, f"{key}/w": w, f"{key}/bias": b, f"{key}/out": out.numpy()})
+
     np.savez_compressed(OUT, **g)
     print(f"wrote {OUT} ({OUT.stat().st_size / 1e6:.2f} MB, {len(g)} arrays)")
 

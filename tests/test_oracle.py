@@ -398,3 +398,51 @@ def test_self_attention_int8kv_is_the_composition():
     exp = oracle.self_attention(q, oracle.dequantize_int8(kq, ks, np.uint16),
                                 oracle.dequantize_int8(vq, vs, np.uint16), 0.25)
     assert_exact(got, exp)
+
+
+# ---- linear and the W8A16 rule -----------------------------------------------------------
+
+def test_golden_linear(golden):
+    n = 0
+    for (op, dt, case), c in golden.items():
+        if op == "linear":
+            b = c["bias"] if c["bias"].size else None
+            assert_exact(oracle.linear(c["x"], c["w"], b), c["out"], f"{dt} {case}")
+            n += 1
+    assert n == 12
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_linear_random_shapes_match_reference(ref, seed):
+    from llaisys_amd.libllaisys import DataType
+    rng = np.random.default_rng(100 + seed)
+    for dt, conv in ((DataType.F32, lambda a: a), (DataType.BF16, f32_to_bf16),
+                     (DataType.F16, lambda a: a.astype(np.float16))):
+        rows, in_f, out_f = int(rng.integers(1, 9)), int(rng.integers(1, 300)), int(rng.integers(1, 40))
+        x = conv(rng.standard_normal((rows, in_f)).astype(np.float32))
+        w = conv((0.05 * rng.standard_normal((out_f, in_f))).astype(np.float32))
+        b = conv(rng.standard_normal(out_f).astype(np.float32))
+        (y,) = _ref_call(ref, "llaisysLinear", [((rows, out_f), dt)], [(x, dt), (w, dt), (b, dt)])
+        assert_exact(oracle.linear(x, w, b), y, "linear")
+
+
+def test_linear_w8a16_closed_forms():
+    rng = np.random.default_rng(12)
+    x = f32_to_bf16(rng.standard_normal((6, 200)).astype(np.float32))
+    codes = rng.integers(-127, 128, size=(30, 200)).astype(np.int8)
+    bias = f32_to_bf16(rng.standard_normal(30).astype(np.float32))
+    # scale 1: exactly the reference linear with the codes as weights (codes are exact in bf16)
+    w = f32_to_bf16(codes.astype(np.float32))
+    ones = np.ones(30, np.float32)
+    assert_exact(oracle.linear_w8a16(x, codes, ones, bias), oracle.linear(x, w, bias))
+    # power-of-two scales only shift the exponent of the f32 sum: scale 2^k, no bias, f32 out
+    xf = bf16_to_f32(x)
+    base = oracle.linear_w8a16(xf, codes, ones)
+    for k in (-7, 3):
+        sc = np.full(30, 2.0 ** k, np.float32)
+        assert np.array_equal(oracle.linear_w8a16(xf, codes, sc), base * np.float32(2.0 ** k))
+    # against f64: the products are exact, so the sum is within f32 accumulation error
+    sc = (0.01 * rng.random(30) + 1e-3).astype(np.float32)
+    got = oracle.linear_w8a16(xf, codes, sc, bias=None)
+    exp = (xf.astype(np.float64) @ codes.T.astype(np.float64)) * sc.astype(np.float64)
+    assert np.abs(got - exp).max() <= 1e-5 * np.abs(exp).max()
