@@ -8,9 +8,10 @@
  * HIP kernel launches on the context stream (llaisysGetContextStream).
  *
  * Scope of this library: the bandwidth-bound per-layer ops and the attention that reads
- * their INT8 KV cache.  llaisysLinear and llaisysRearrange are exported so that the
- * reference's ctypes loader binds, and raise "Unimplemented function" (the reference's own
- * rearrange is a stub, src/ops/rearrange/op.cpp:4-6).  Ops on CPU tensors raise "Unsupported device":
+ * their INT8 KV cache, and the linear layers (dense, and over INT8 weights).
+ * llaisysRearrange is exported so that the reference's ctypes loader binds, and raises
+ * "Unimplemented function" (the reference's own rearrange is a stub,
+ * src/ops/rearrange/op.cpp:4-6).  Ops on CPU tensors raise "Unsupported device":
  * this library has no CPU compute path.
  */
 #ifndef LLAISYS_OPS_H
@@ -28,7 +29,9 @@ __C {
     /* reference ops.h:9 -- out[i,:] = weight[index[i],:]; index I32/I64 */
     __export void llaisysEmbedding(llaisysTensor_t out, llaisysTensor_t index,
                                    llaisysTensor_t weight);
-    /* reference ops.h:10 -- out of scope here: raises "Unimplemented function" */
+    /* reference ops.h:10 -- out = in . weight^T + bias (src/ops/linear/op.cpp:10-42,
+     * cpu/linear_cpu.cpp:11-41): in [.., K], weight [N, K], out [.., N], bias [N], one
+     * dtype, f32 accumulation; a NULL or zero-element bias means no bias. */
     __export void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight,
                                 llaisysTensor_t bias);
     /* reference ops.h:11 -- out of scope here: raises "Unimplemented function" */
@@ -121,6 +124,14 @@ __C {
                                              llaisysTensor_t k_codes, llaisysTensor_t k_scale,
                                              llaisysTensor_t v_codes, llaisysTensor_t v_scale,
                                              float scale);
+    /* llaisysLinear with INT8 weights (no reference counterpart; the decoder's projections,
+     * src/models/qwen2/components.hpp:114, with weights quantized by llaisysQuantizeInt8 per output row):
+     * w_codes [N, K] I8, w_scale [N] F32, in / out / bias of one float dtype;
+     * out[m][n] = T(w_scale[n] * sum_k in[m][k] * code[n][k] + bias[n]), f32 accumulation.
+     * Bias NULL or zero-element means no bias. */
+    __export void llaisysLinearW8A16(llaisysTensor_t out, llaisysTensor_t in,
+                                     llaisysTensor_t w_codes, llaisysTensor_t w_scale,
+                                     llaisysTensor_t bias);
 }
 
 #endif /* LLAISYS_OPS_H */

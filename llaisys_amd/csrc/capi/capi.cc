@@ -121,8 +121,9 @@ __C {
     void llaisysEmbedding(llaisysTensor_t out, llaisysTensor_t index, llaisysTensor_t weight) {
         llaisys::ops::embedding(out->tensor, index->tensor, weight->tensor);
     }
-    void llaisysLinear(llaisysTensor_t, llaisysTensor_t, llaisysTensor_t, llaisysTensor_t) {
-        TO_BE_IMPLEMENTED();
+    void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight,
+                       llaisysTensor_t bias) {
+        llaisys::ops::linear(out->tensor, in->tensor, weight->tensor, bias ? bias->tensor : nullptr);
     }
     void llaisysRearrange(llaisysTensor_t, llaisysTensor_t) { TO_BE_IMPLEMENTED(); }
     void llaisysRmsNorm(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, float eps) {
@@ -185,6 +186,12 @@ __C {
                                    llaisysTensor_t out1, llaisysTensor_t q1, llaisysTensor_t scale1) {
         llaisys::ops::dequantizeInt8Pair(out0->tensor, q0->tensor, scale0->tensor, out1->tensor,
                                          q1->tensor, scale1->tensor);
+    }
+
+    void llaisysLinearW8A16(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t w_codes,
+                            llaisysTensor_t w_scale, llaisysTensor_t bias) {
+        llaisys::ops::linearW8A16(out->tensor, in->tensor, w_codes->tensor, w_scale->tensor,
+                                  bias ? bias->tensor : nullptr);
     }
 
     // ---- model API: out of scope, exported so the reference ctypes loader binds --------

@@ -95,4 +95,11 @@ void selfAttention(void *out, const void *q, const void *k, const void *v, const
                    size_t d, size_t dv, float scale, llaisysDataType_t dt, void *ws,
                    size_t ws_bytes, hipStream_t stream);
 
+// out [rows, N] = x [rows, K] w^T (+ bias [N]); with w_scale non-null w is INT8 codes
+// [N, K] and the sum of each output channel n is multiplied by w_scale[n] (W8A16).  rows,
+// K and N below 2^31.
+void linear(void *out, const void *x, const void *w, const float *w_scale, const void *bias,
+            size_t rows, size_t in_features, size_t out_features, llaisysDataType_t dt,
+            hipStream_t stream);
+
 } // namespace llaisys::kernels

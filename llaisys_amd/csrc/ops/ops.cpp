@@ -386,6 +386,73 @@ void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor
                     reinterpret_cast<const float *>(v_scale->data()), scale);
 }
 
+
+namespace {
+// Shape checks of reference src/ops/linear/op.cpp:10-42 (messages kept); a bias that is
+// null or has no elements means no bias.  Returns the row count.
+size_t checkLinear(const tensor_t &out, const tensor_t &in, const tensor_t &weight,
+                   const tensor_t &bias, bool has_bias) {
+    ASSERT(weight->ndim() == 2, "Linear: weight must be 2D");
+    const size_t in_features = weight->shape()[1], out_features = weight->shape()[0];
+    ASSERT(lastDim(in) == in_features, "Linear: input feature dim mismatch");
+    ASSERT(lastDim(out) == out_features, "Linear: output feature dim mismatch");
+    ASSERT(in_features > 0 && out_features > 0, "Linear: empty weight");
+    const size_t rows = in->numel() / in_features;
+    ASSERT(out->numel() / out_features == rows, "Linear: input/output rows mismatch");
+    if (has_bias) ASSERT(bias->numel() == out_features, "Linear: bias shape mismatch");
+    ASSERT(out->isContiguous() && in->isContiguous() && weight->isContiguous(),
+           "Linear inputs must be contiguous");
+    if (has_bias) ASSERT(bias->isContiguous(), "Linear bias must be contiguous");
+    ASSERT(rows < (size_t(1) << 31) && in_features < (size_t(1) << 31) &&
+               out_features < (size_t(1) << 31),
+           "Linear: dimensions must be below 2^31");
+    return rows;
+}
+} // namespace
+
+// reference src/ops/linear/op.cpp:10-42
+void linear(tensor_t out, tensor_t in, tensor_t weight, tensor_t bias) {
+    const bool has_bias = bias != nullptr && bias->numel() > 0;
+    if (has_bias) {
+        CHECK_SAME_DEVICE(out, in, weight, bias);
+        CHECK_SAME_DTYPE(out->dtype(), in->dtype(), weight->dtype(), bias->dtype());
+    } else {
+        CHECK_SAME_DEVICE(out, in, weight);
+        CHECK_SAME_DTYPE(out->dtype(), in->dtype(), weight->dtype());
+    }
+    const size_t rows = checkLinear(out, in, weight, bias, has_bias);
+    requireFloat(in->dtype());
+    auto s = streamFor(in);
+    kernels::linear(out->data(), in->data(), weight->data(), nullptr,
+                    has_bias ? bias->data() : nullptr, rows, weight->shape()[1],
+                    weight->shape()[0], in->dtype(), s);
+    launched("linear");
+}
+
+// linear with INT8 weight codes [N, K] and one F32 scale per output channel:
+// out = T(w_scale[n] * sum_k in[m][k] * code[n][k] + bias[n]).
+void linearW8A16(tensor_t out, tensor_t in, tensor_t w_codes, tensor_t w_scale, tensor_t bias) {
+    const bool has_bias = bias != nullptr && bias->numel() > 0;
+    CHECK_SAME_DEVICE(out, in, w_codes, w_scale);
+    CHECK_SAME_DTYPE(out->dtype(), in->dtype());
+    if (has_bias) {
+        CHECK_SAME_DEVICE(out, bias);
+        CHECK_SAME_DTYPE(out->dtype(), bias->dtype());
+    }
+    ASSERT(w_codes->dtype() == LLAISYS_DTYPE_I8, "LinearW8A16: weight codes must be INT8");
+    ASSERT(w_scale->dtype() == LLAISYS_DTYPE_F32, "LinearW8A16: weight scales must be F32");
+    const size_t rows = checkLinear(out, in, w_codes, bias, has_bias);
+    ASSERT(w_scale->isContiguous() && w_scale->numel() == w_codes->shape()[0],
+           "LinearW8A16: one contiguous scale per output feature");
+    requireFloat(in->dtype());
+    auto s = streamFor(in);
+    kernels::linear(out->data(), in->data(), w_codes->data(),
+                    reinterpret_cast<const float *>(w_scale->data()),
+                    has_bias ? bias->data() : nullptr, rows, w_codes->shape()[1],
+                    w_codes->shape()[0], in->dtype(), s);
+    launched("linearW8A16");
+}
+
 } // namespace llaisys::ops
 
 namespace llaisys::ops {

@@ -1,7 +1,7 @@
 """Ops: the LLAISYS operators as static methods.
 
-The nine reference methods match python/llaisys/ops.py:6-55 (linear and rearrange raise
-in this library: out of scope); the rest wrap the additive entry points of
+The nine reference methods match python/llaisys/ops.py:6-55 (rearrange raises in this
+library, as the reference's own C++ rearrange does); the rest wrap the additive entry points of
 include/llaisys/ops.h.
 """
 from ctypes import c_float, c_size_t
@@ -24,9 +24,9 @@ class Ops:
         LIB_LLAISYS.llaisysEmbedding(out.lib_tensor(), index.lib_tensor(), weight.lib_tensor())
 
     @staticmethod
-    def linear(out: Tensor, inp: Tensor, weight: Tensor, bias: Tensor):
+    def linear(out: Tensor, inp: Tensor, weight: Tensor, bias: Tensor = None):
         LIB_LLAISYS.llaisysLinear(out.lib_tensor(), inp.lib_tensor(), weight.lib_tensor(),
-                                  bias.lib_tensor())
+                                  None if bias is None else bias.lib_tensor())
 
     @staticmethod
     def rearrange(out: Tensor, inp: Tensor):
@@ -113,3 +113,10 @@ class Ops:
         LIB_LLAISYS.llaisysDequantizeInt8Pair(out0.lib_tensor(), q0.lib_tensor(),
                                               scale0.lib_tensor(), out1.lib_tensor(),
                                               q1.lib_tensor(), scale1.lib_tensor())
+
+    @staticmethod
+    def linear_w8a16(out: Tensor, inp: Tensor, w_codes: Tensor, w_scale: Tensor,
+                     bias: Tensor = None):
+        LIB_LLAISYS.llaisysLinearW8A16(out.lib_tensor(), inp.lib_tensor(), w_codes.lib_tensor(),
+                                       w_scale.lib_tensor(),
+                                       None if bias is None else bias.lib_tensor())

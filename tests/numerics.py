@@ -83,3 +83,33 @@ def assert_attention_close(got, exp, v, what=""):
     ok |= absd <= floor
     assert ok.all(), (f"{what}: {(~ok).sum()} of {ok.size} outputs beyond tolerance "
                       f"(max abs diff {absd.max():.3g}, floor {floor:.3g})")
+
+
+def assert_linear_close(got, exp, x, w, what="", w_scale=None):
+    """Linear outputs against the oracle.  Each output is a K-term dot product that the
+    reference sums left to right in f32; the GPU sums the same exact products in another
+    order, so the two f32 sums differ by at most about K * 2^-24 * sum_k |x_k w_k| (much less
+    in practice).  Bound: the op's usual tolerance (2 ulps bf16 / f16, 1e-5 relative f32) OR
+    an absolute floor of 2^-16 * sum_k |x_k w_k| (times w_scale[n] for INT8 weights), which
+    covers outputs that cancel to near 0."""
+    got, exp = np.asarray(got), np.asarray(exp)
+    assert got.shape == exp.shape and got.dtype == exp.dtype, (what, got.shape, exp.shape)
+    g, e = _as_f32(got).astype(np.float64), _as_f32(exp).astype(np.float64)
+    assert np.array_equal(np.isnan(g), np.isnan(e)), f"{what}: NaN pattern differs"
+    wf = w.astype(np.float64) if w.dtype == np.int8 else _as_f32(w).astype(np.float64)
+    mag = np.abs(_as_f32(x).astype(np.float64)) @ np.abs(wf).T
+    if w_scale is not None:
+        mag = mag * np.abs(np.asarray(w_scale, dtype=np.float64))[None, :]
+    floor = 2.0 ** -16 * mag
+    fin = np.isfinite(e)
+    absd = np.abs(g - e)
+    if exp.dtype == np.float32:
+        ok = absd <= F32_RTOL * np.abs(e)
+    elif exp.dtype == np.uint16:
+        ok = bf16_ulp_distance(got, exp) <= HALF_ULPS
+    else:
+        ok = _f16_ulps(got, exp) <= HALF_ULPS
+    ok = (ok | (absd <= floor))[fin]
+    assert np.array_equal(got[~fin], exp[~fin]), f"{what}: non-finite outputs differ"
+    assert ok.all(), (f"{what}: {(~ok).sum()} of {ok.size} outputs beyond tolerance "
+                      f"(max abs diff {absd[fin].max():.3g})")

@@ -139,7 +139,11 @@ def _run(code):
     ("L.Ops.rope(t((2,1,3)), t((2,1,3)), t((2,), L.DataType.I64), 1e4)", "Head dimension must be even"),
     ("L.Ops.embedding(t((2,4)), t((2,), L.DataType.F32), t((8,4)))", "index data type must be INT32 or INT64"),
     ("L.Ops.argmax(t((1,), L.DataType.F32), t((1,)), t((8,)))", "max_idx must be INT32 or INT64"),
-    ("L.Ops.linear(t((2,2)), t((2,2)), t((2,2)), t((2,)))", "Unimplemented function"),
+    ("L.Ops.rearrange(t((2,2)), t((2,2)))", "Unimplemented function"),
+    ("L.Ops.linear(t((2,2)), t((2,2)), t((2,2)), t((3,)))", "Linear: bias shape mismatch"),
+    ("L.Ops.linear(t((2,3)), t((2,2)), t((2,2)), t((2,)))", "Linear: output feature dim mismatch"),
+    ("L.Ops.linear(t((2,2)), t((2,2)), t((2,2)))", "Unsupported device"),
+    ("L.Ops.linear_w8a16(t((2,2)), t((2,2)), t((2,2)), t((2,)))", "weight codes must be INT8"),
     ("L.Ops.kv_append_int8(t((4,2,8), L.DataType.I8), t((4,2)), t((3,2,8)), 2)", "append past the cache end"),
     ("L.Ops.quantize_int8(t((4,8), L.DataType.I8), t((3,)), t((4,8)))", "one scale per last-dim row"),
     ("L.Tensor((2,), L.DataType.F32, L.DeviceType.AMD, 0)", "invalid device id"),

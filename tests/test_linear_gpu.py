@@ -1,0 +1,130 @@
+"""Linear layers on the GPU (llaisysLinear, llaisysLinearW8A16) against the oracle's
+restatement of the reference kernel (linear_cpu.cpp:11-41) and of the W8A16 rule, which
+tests/test_oracle.py pins to the compiled reference and to closed forms.  Tolerance:
+numerics.assert_linear_close."""
+import zlib
+
+import numpy as np
+import pytest
+
+import llaisys_amd as L
+import oracle
+from llaisys_amd.hostfmt import f32_to_bf16
+from numerics import assert_exact, assert_linear_close
+
+pytestmark = pytest.mark.gpu
+
+AMD = dict(device=L.DeviceType.AMD, device_id=0)
+DTS = {"f32": L.DataType.F32, "bf16": L.DataType.BF16, "f16": L.DataType.F16}
+
+
+def sample(rng, shape, dt, s=1.0):
+    x = (s * rng.standard_normal(shape)).astype(np.float32)
+    return {"f32": x, "bf16": f32_to_bf16(x), "f16": x.astype(np.float16)}[dt]
+
+
+def dev(a, dt=None):
+    return L.Tensor.from_numpy(a, dt, **AMD)
+
+
+def linear(x, w, b, dt):
+    out = L.Tensor((x.shape[0], w.shape[0]), DTS[dt], **AMD)
+    L.Ops.linear(out, dev(x, DTS[dt]), dev(w, DTS[dt]), None if b is None else dev(b, DTS[dt]))
+    return out.numpy()
+
+
+def linear_w8a16(x, codes, scale, b, dt):
+    out = L.Tensor((x.shape[0], codes.shape[0]), DTS[dt], **AMD)
+    L.Ops.linear_w8a16(out, dev(x, DTS[dt]), dev(codes), dev(scale),
+                       None if b is None else dev(b, DTS[dt]))
+    return out.numpy()
+
+
+def int8_weights(rng, out_f, in_f):
+    codes = rng.integers(-127, 128, size=(out_f, in_f), dtype=np.int8)
+    scale = (0.01 * (0.5 + rng.random(out_f))).astype(np.float32) / 127
+    return codes, scale
+
+
+SHAPES = [
+    # rows, in_features, out_features -- reference test shape, decode rows of Qwen2-1.5B's
+    # projections (q, kv, gate/up, down), a prefill block, ragged edges of the 128 x 128
+    # block tile, in_features not a multiple of 8 (scalar path), one output
+    (2, 4, 3), (1, 1536, 1536), (1, 1536, 256), (1, 1536, 8960), (1, 8960, 1536),
+    (256, 1536, 1536), (129, 264, 200), (17, 40, 130), (3, 77, 9), (64, 1536, 1), (1, 8, 1),
+]
+
+
+@pytest.mark.parametrize("bias", [True, False], ids=["bias", "nobias"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_linear_matches_oracle(shape, dt, bias):
+    rows, in_f, out_f = shape
+    rng = np.random.default_rng(zlib.crc32(repr((shape, dt, bias)).encode()))
+    x, w = sample(rng, (rows, in_f), dt), sample(rng, (out_f, in_f), dt, 0.05)
+    b = sample(rng, (out_f,), dt) if bias else None
+    assert_linear_close(linear(x, w, b, dt), oracle.linear(x, w, b), x, w, f"{dt} {shape}")
+
+
+def test_linear_golden_on_gpu(golden):
+    n = 0
+    for (op, dt, case), c in golden.items():
+        if op == "linear":
+            got = linear(c["x"], c["w"], c["bias"], dt)  # zero-element bias = no bias
+            assert_linear_close(got, c["out"], c["x"], c["w"], f"golden {dt} {case}")
+            n += 1
+    assert n == 12
+
+
+def test_linear_prefill_block_is_deterministic():
+    rng = np.random.default_rng(3)
+    x, w = sample(rng, (512, 1536, ), "bf16"), sample(rng, (2048, 1536), "bf16", 0.05)
+    first = linear(x, w, None, "bf16")
+    assert_exact(linear(x, w, None, "bf16"), first, "second run")
+
+
+def test_linear_empty_rows():
+    rng = np.random.default_rng(4)
+    w = sample(rng, (16, 32), "bf16")
+    assert linear(np.zeros((0, 32), np.uint16), w, None, "bf16").shape == (0, 16)
+
+
+@pytest.mark.parametrize("bias", [True, False], ids=["bias", "nobias"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_linear_w8a16_matches_oracle(shape, dt, bias):
+    rows, in_f, out_f = shape
+    rng = np.random.default_rng(zlib.crc32(repr(("w8", shape, dt, bias)).encode()))
+    x = sample(rng, (rows, in_f), dt)
+    codes, scale = int8_weights(rng, out_f, in_f)
+    b = sample(rng, (out_f,), dt) if bias else None
+    assert_linear_close(linear_w8a16(x, codes, scale, b, dt), oracle.linear_w8a16(x, codes, scale, b),
+                        x, codes, f"w8a16 {dt} {shape}", w_scale=scale)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_w8a16_with_unit_scales_equals_dense_linear(dt):
+    # codes are exact in bf16 / f16, and a scale of 1 multiplies exactly: the two entry
+    # points must agree bit for bit on the same sums
+    rng = np.random.default_rng(6)
+    x = sample(rng, (100, 520), dt, 0.1)
+    codes = rng.integers(-127, 128, size=(300, 520), dtype=np.int8)
+    w = {"bf16": f32_to_bf16(codes.astype(np.float32)), "f16": codes.astype(np.float16)}[dt]
+    b = sample(rng, (300,), dt)
+    got = linear_w8a16(x, codes, np.ones(300, np.float32), b, dt)
+    assert_exact(got, linear(x, w, b, dt), dt)
+
+
+def test_w8a16_of_quantized_weights_tracks_dense_linear():
+    # weights quantized by the library's own llaisysQuantizeInt8 (one scale per output row)
+    rng = np.random.default_rng(7)
+    x, w = sample(rng, (32, 1536), "bf16"), sample(rng, (256, 1536), "bf16", 0.02)
+    q, s = L.Tensor((256, 1536), L.DataType.I8, **AMD), L.Tensor((256,), L.DataType.F32, **AMD)
+    L.Ops.quantize_int8(q, s, dev(w, L.DataType.BF16))
+    codes, scale = q.numpy(), s.numpy()
+    got = linear_w8a16(x, codes, scale, None, "bf16")
+    assert_linear_close(got, oracle.linear_w8a16(x, codes, scale), x, codes, "quantized", w_scale=scale)
+    dense = linear(x, w, None, "bf16")
+    gf = (got.astype(np.uint32) << 16).view(np.float32)
+    df = (dense.astype(np.uint32) << 16).view(np.float32)
+    assert np.abs(gf - df).max() < 0.02 * np.abs(df).max()

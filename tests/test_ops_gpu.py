@@ -16,7 +16,7 @@ import pytest
 import llaisys_amd as L
 import oracle
 from llaisys_amd.hostfmt import bf16_to_f32, f32_to_bf16
-from numerics import assert_attention_close, assert_close, assert_exact
+from numerics import assert_attention_close, assert_close, assert_exact, assert_linear_close
 
 pytestmark = pytest.mark.gpu
 
@@ -88,6 +88,10 @@ def test_golden_vectors_on_gpu(golden):
             L.Ops.self_attention(out, dev(c["q"], DTS[dt]), dev(c["k"], DTS[dt]), dev(c["v"], DTS[dt]),
                                  float(c["scale"]))
             assert_attention_close(out.numpy(), c["out"], c["v"], what)
+        elif op == "linear":
+            out = empty(c["out"].shape, DTS[dt])
+            L.Ops.linear(out, dev(c["x"], DTS[dt]), dev(c["w"], DTS[dt]), dev(c["bias"], DTS[dt]))
+            assert_linear_close(out.numpy(), c["out"], c["x"], c["w"], what)
         else:
             continue
         checked += 1
