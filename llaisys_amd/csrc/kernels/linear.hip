@@ -30,6 +30,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 struct LinearArgs {
@@ -49,6 +50,16 @@ __device__ __forceinline__ f32x4 mfma(const v4u &a, const v4u &b, f32x4 c) {
         return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// 32 x 32 x 16: A[m = l % 32][k = 8 (l / 32) + j], B[k = 8 (l / 32) + j][n = l % 32],
+// D[m = 8 (i / 4) + 4 (l / 32) + i % 4][n = l % 32]; twice the sustained rate of 16 x 16 x 32
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32(const v4u &a, const v4u &b, const f32x16 &c) {
+    if constexpr (std::is_same_v<T, BF16>)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
 // 8 INT8 codes as 8 elements of T (exact: |code| <= 127 fits both 8- and 11-bit mantissas)
 template <typename T>
 __device__ __forceinline__ v4u codesToT(const v2u &c) {
@@ -66,90 +77,172 @@ __device__ __forceinline__ v4u codesToT(const v2u &c) {
     return v4u{w[0], w[1], w[2], w[3]};
 }
 
-constexpr int kWM = 64, kWN = 64;        // wave tile
-constexpr int kBM = 128, kBN = 128;      // block tile (2 x 2 waves)
-constexpr int kKS = 32;                  // K per step
+// Many rows (prefill): MFMA-bound.  A block of 4 waves owns BW output channels x BX rows;
+// per stage of 64 k it stages both tiles in LDS (row-contiguous global loads, 144-byte row
+// pitch: the MFMA-operand reads and the tile writes are bank-conflict-free), double-buffered
+// with the next stage's global loads in flight during the MFMAs.  The MFMA computes
+// out^T = w x^T: weight rows are the A operand and activation rows the B operand, so each
+// lane ends with 4 consecutive output channels of one row (one 8-byte store).  INT8 codes
+// are converted to exact bf16 / f16 values on their way into LDS.
+constexpr int kTK = 64;               // k per stage
+constexpr int kXcds = 8;              // accelerator complex dies of an MI355X
 
-template <typename T, bool kInt8>
-__global__ void __launch_bounds__(256)
-    linearMfma(LinearArgs a) {
-    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
-    const int lane = int(threadIdx.x) % kWave;
-    const int r16 = lane % 16, g4 = lane / 16;
-    // block tiles: N-major order so that consecutive blocks share the x rows of an M tile
-    const int nbn = (a.N + kBN - 1) / kBN;
-    const int bm = int(blockIdx.x) / nbn, bn = int(blockIdx.x) % nbn;
-    const int m0 = bm * kBM + (wave / 2) * kWM, n0 = bn * kBN + (wave % 2) * kWN;
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS accesses, not for its
+// global loads (__syncthreads' fence would also drain the prefetches in flight).  The
+// memory clobber keeps the compiler from moving accesses across it.
+__device__ __forceinline__ void ldsBarrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+constexpr int kTPitch = 2 * kTK + 16; // LDS row pitch (bytes)
+
+template <typename T, bool kInt8, int BW, int BX, int NWW, int NWX, int P>
+__global__ void __launch_bounds__(NWW * NWX * 64)
+    linearTiled(LinearArgs a) {
+    constexpr int NT = NWW * NWX * kWave;         // threads
+    constexpr int WW = BW / NWW, WX = BX / NWX;   // wave tile (NWW x NWX waves)
+    constexpr int TW = WW / 32, TX = WX / 32;     // 32 x 32 MFMA tiles per wave
+    constexpr int kXRows = NT / 8;                // 16-bit rows: 8 lanes x 16 B
+    constexpr int kXLoads = BX / kXRows;
+    constexpr int kWRows = kInt8 ? NT / 4 : NT / 8; // INT8 rows: 4 lanes x 16 codes
+    constexpr int kWLoads = BW / kWRows;
+    static_assert(kXLoads >= 1 && kWLoads >= 1 && TW >= 1 && TX >= 1, "tile too small for the block");
+    __shared__ __align__(16) char lds[2][(BW + BX) * kTPitch];
+    const int tid = int(threadIdx.x);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int lane = tid % kWave, r16 = lane % 16, g4 = lane / 16;
+    // Blocks are dispatched to the 8 XCDs round-robin, each XCD with its own L2: give each
+    // XCD a contiguous range of weight tiles and walk the activation tiles fastest inside it,
+    // so that a weight tile stays in that L2 while every row tile passes over it.
+    const int nbx = (a.M + BX - 1) / BX;
+    const int nb = int(gridDim.x), b = int(blockIdx.x);
+    const int v = nb % kXcds == 0 ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
+    const int bx = v % nbx, bw = v / nbx;
+    const int w0 = bw * BW, x0 = bx * BX;
+    const int ww0 = (wave % NWW) * WW, wx0 = (wave / NWW) * WX;
     const char *xb = static_cast<const char *>(a.x);
     const char *wb = static_cast<const char *>(a.w);
-    constexpr int wbytes = kInt8 ? 1 : 2;
-    // rows this lane loads (clamped into range; results of clamped rows are not stored)
-    int xr[4], wr[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        xr[t] = min(m0 + 16 * t + r16, a.M - 1);
-        wr[t] = min(n0 + 16 * t + r16, a.N - 1);
-    }
-    f32x4 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int nk = (a.K + kTK - 1) / kTK;
 
-    const auto load = [&](int k0, v4u (&xa)[4], v4u (&wa)[4]) {
-        const int kk = k0 + 8 * g4;
-        const bool in = kk < a.K; // K % 8 == 0 on this path: a group is all in or all out
+    // global loads of stage kt: activation rows (t / 8 + 32 i, chunk t % 8) and weight rows
+    const int xr = tid / 8, xc = tid % 8;
+    const int wr = tid / (NT / kWRows), wc = tid % (NT / kWRows);
+    // global loads of stage kt into ring slot r; past the last stage: the last stage again
+    // (loads stay unconditional, so that the compiler keeps them where they are issued)
+    v4u gx[P][kXLoads], gw[P][kWLoads];
+    const auto loadGlobal = [&](int kt, v4u(&rx)[kXLoads], v4u(&rw)[kWLoads]) {
+        kt = min(kt, nk - 1);
+        const int kx = kt * kTK + 8 * xc;
+        const bool xin = kx < a.K; // K % 8 == 0
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            xa[t] = in ? *reinterpret_cast<const v4u *>(xb + (size_t(xr[t]) * a.K + kk) * 2) : v4u{0u, 0u, 0u, 0u};
+        for (int i = 0; i < kXLoads; ++i) {
+            const int row = min(x0 + xr + kXRows * i, a.M - 1);
+            rx[i] = *reinterpret_cast<const v4u *>(xb + (size_t(row) * a.K + (xin ? kx : 0)) * 2);
+            if (!xin) rx[i] = v4u{0u, 0u, 0u, 0u};
+        }
+        const int kw = kt * kTK + (kInt8 ? 16 : 8) * wc;
+        const bool win = kw < a.K; // K % 8 == 0 (16-bit) / K % 16 == 0 (INT8)
+#pragma unroll
+        for (int i = 0; i < kWLoads; ++i) {
+            const int row = min(w0 + wr + kWRows * i, a.N - 1);
+            rw[i] = *reinterpret_cast<const v4u *>(wb + (size_t(row) * a.K + (win ? kw : 0)) * (kInt8 ? 1 : 2));
+            if (!win) rw[i] = v4u{0u, 0u, 0u, 0u};
+        }
+    };
+    const auto storeLds = [&](int buf, const v4u(&rx)[kXLoads], const v4u(&rw)[kWLoads]) {
+        char *base = lds[buf];
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i)
+            *reinterpret_cast<v4u *>(base + (BW + xr + kXRows * i) * kTPitch + 16 * xc) = rx[i];
+#pragma unroll
+        for (int i = 0; i < kWLoads; ++i) {
+            char *dst = base + (wr + kWRows * i) * kTPitch;
             if constexpr (kInt8) {
-                const v2u c = in ? *reinterpret_cast<const v2u *>(wb + size_t(wr[t]) * a.K + kk) : v2u{0u, 0u};
-                wa[t] = v4u{c.x, c.y, 0u, 0u};
+                *reinterpret_cast<v4u *>(dst + 32 * wc) = codesToT<T>(v2u{rw[i].x, rw[i].y});
+                *reinterpret_cast<v4u *>(dst + 32 * wc + 16) = codesToT<T>(v2u{rw[i].z, rw[i].w});
             } else {
-                wa[t] = in ? *reinterpret_cast<const v4u *>(wb + (size_t(wr[t]) * a.K + kk) * wbytes) : v4u{0u, 0u, 0u, 0u};
+                *reinterpret_cast<v4u *>(dst + 16 * wc) = rw[i];
             }
         }
     };
-    v4u xa[4], wa[4], xn[4], wn[4];
-    load(0, xa, wa);
-    for (int k0 = 0; k0 < a.K; k0 += kKS) {
-        if (k0 + kKS < a.K) load(k0 + kKS, xn, wn);
-        v4u wt[4];
+
+    f32x16 acc[TW][TX];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            if constexpr (kInt8)
-                wt[t] = codesToT<T>(v2u{wa[t].x, wa[t].y});
-            else
-                wt[t] = wa[t];
-        }
+    for (int i = 0; i < TW; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < TX; ++j)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = mfma<T>(xa[i], wt[j], acc[i][j]);
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    const int r32 = lane % 32, h2 = lane / 32;
+
+    // stage 0 to LDS, stages 1..P in flight
+    loadGlobal(0, gx[0], gw[0]);
+    storeLds(0, gx[0], gw[0]);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            xa[t] = xn[t];
-            wa[t] = wn[t];
+    for (int r = 0; r < P; ++r) loadGlobal(1 + r, gx[r], gw[r]);
+    ldsBarrier();
+    for (int base = 0; base < nk; base += P) {
+#pragma unroll
+        for (int r = 0; r < P; ++r) {
+            const int kt = base + r; // stage in LDS; ring slot r holds stage kt + 1
+            if (kt >= nk) break;
+            const char *tile = lds[kt & 1];
+#pragma unroll
+            for (int st = 0; st < kTK / 16; ++st) {
+                v4u fa[TW], fb[TX];
+#pragma unroll
+                for (int i = 0; i < TW; ++i)
+                    fa[i] = *reinterpret_cast<const v4u *>(tile + (ww0 + 32 * i + r32) * kTPitch + 32 * st + 16 * h2);
+#pragma unroll
+                for (int j = 0; j < TX; ++j)
+                    fb[j] = *reinterpret_cast<const v4u *>(tile + (BW + wx0 + 32 * j + r32) * kTPitch + 32 * st + 16 * h2);
+#pragma unroll
+                for (int i = 0; i < TW; ++i)
+#pragma unroll
+                    for (int j = 0; j < TX; ++j) acc[i][j] = mfma32<T>(fa[i], fb[j], acc[i][j]);
+            }
+            // stage kt + 1 (past the end: harmless, nothing reads it) into the other buffer,
+            // whose last readers finished before the previous barrier; then refill the slot
+            storeLds((kt + 1) & 1, gx[r], gw[r]);
+            loadGlobal(kt + 1 + P, gx[r], gw[r]);
+            ldsBarrier();
         }
     }
-    // D[m = 4g + e][n = r16] of tile (i, j)
+
+    // D[8 q + 4 h + e][r32] of tile (i, j), q < 4, e < 4 = out[row x0 + wx0 + 32 j + r32]
+    // [channel w0 + ww0 + 32 i + 8 q + 4 h + e]: 4 consecutive channels per (q, lane)
+    const bool vec = a.N % 4 == 0;
+    using C = std::conditional_t<std::is_same_v<T, BF16>, Bf16Cvt, F16Cvt>;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int n = n0 + 16 * j + r16;
-        if (n >= a.N) continue;
-        const float sc = kInt8 ? a.scale[n] : 1.0f;
-        const float bv = a.bias ? Fmt<T>::get(a.bias, n) : 0.0f;
+    for (int i = 0; i < TW; ++i)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int q = 0; q < 4; ++q) {
+            const int n = w0 + ww0 + 32 * i + 8 * q + 4 * h2;
+            float sc[4], bv[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int m = m0 + 16 * i + 4 * g4 + e;
-                if (m < a.M) {
-                    const float s = kInt8 ? sc * acc[i][j][e] : acc[i][j][e];
-                    Fmt<T>::put(a.out, size_t(m) * a.N + n, a.bias ? s + bv : s);
+                const int ne = min(n + e, a.N - 1);
+                sc[e] = kInt8 ? a.scale[ne] : 1.0f;
+                bv[e] = a.bias ? Fmt<T>::get(a.bias, ne) : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < TX; ++j) {
+                const int m = x0 + wx0 + 32 * j + r32;
+                if (m >= a.M) continue;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float sum = kInt8 ? sc[e] * acc[i][j][4 * q + e] : acc[i][j][4 * q + e];
+                    v[e] = a.bias ? sum + bv[e] : sum;
+                }
+                if (vec && n + 3 < a.N) {
+                    const uint32_t lo = C::narrow(v[0]) | (C::narrow(v[1]) << 16);
+                    const uint32_t hi = C::narrow(v[2]) | (C::narrow(v[3]) << 16);
+                    *reinterpret_cast<v2u *>(static_cast<char *>(a.out) + (size_t(m) * a.N + n) * 2) = v2u{lo, hi};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < a.N) Fmt<T>::put(a.out, size_t(m) * a.N + n + e, v[e]);
                 }
             }
-    }
+        }
 }
 
 // Few rows (M <= 16, decode): HBM-bound on the weights.  A block owns 16 output channels
@@ -274,18 +367,28 @@ void launch(const LinearArgs &a, hipStream_t s) {
     if (a.M == 0 || a.N == 0) return;
     const auto al = [](const void *p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; };
     constexpr bool kMfmaType = std::is_same_v<T, BF16> || std::is_same_v<T, F16>;
-    if (kMfmaType && a.K % 8 == 0 && a.K > 0 && al(a.x, 16) && al(a.w, kInt8 ? 8 : 16)) {
-        if (a.M <= 16 && (!kInt8 || a.K % 16 == 0) && al(a.w, 16)) {
-            // waves per block: enough blocks x waves to fill the chip, at most one wave per
-            // group of 128 k
-            const int tiles = (a.N + 15) / 16, ng = (a.K + kSkK - 1) / kSkK;
-            const int nw = std::max(1, std::min({16, ng, std::max(2, 2048 / tiles)}));
-            const size_t lds = size_t(nw) * (16 * skinnyPitch(kInt8) + 256 * sizeof(float));
-            if constexpr (kMfmaType) linearSkinny<T, kInt8><<<unsigned(tiles), unsigned(nw * kWave), lds, s>>>(a);
-            return;
+    // MFMA paths: 16-bit activations, 16-byte aligned rows (K % 8 == 0; INT8 codes K % 16 == 0)
+    if (kMfmaType && a.K > 0 && a.K % (kInt8 ? 16 : 8) == 0 && al(a.x, 16) && al(a.w, 16)) {
+        if constexpr (kMfmaType) {
+            if (a.M <= 16) {
+                // waves per block: enough blocks x waves to fill the chip, at most one wave
+                // per group of 128 k
+                const int tiles = (a.N + 15) / 16, ng = (a.K + kSkK - 1) / kSkK;
+                const int nw = std::max(1, std::min({16, ng, std::max(2, 2048 / tiles)}));
+                const size_t lds = size_t(nw) * (16 * skinnyPitch(kInt8) + 256 * sizeof(float));
+                linearSkinny<T, kInt8><<<unsigned(tiles), unsigned(nw * kWave), lds, s>>>(a);
+                return;
+            }
+            // tile shape: 128 x 128 (8 waves, 2 stages of loads in flight) while that still
+            // gives most CUs a block, else 64 x 64
+            const auto blocks = [&](int bw, int bx) {
+                return unsigned((a.N + bw - 1) / bw) * unsigned((a.M + bx - 1) / bx);
+            };
+            if (blocks(128, 128) >= 192)
+                linearTiled<T, kInt8, 128, 128, 4, 2, 2><<<blocks(128, 128), 512, 0, s>>>(a);
+            else
+                linearTiled<T, kInt8, 64, 64, 2, 2, 2><<<blocks(64, 64), 256, 0, s>>>(a);
         }
-        const unsigned blocks = unsigned((a.M + kBM - 1) / kBM) * unsigned((a.N + kBN - 1) / kBN);
-        if constexpr (kMfmaType) linearMfma<T, kInt8><<<blocks, 256, 0, s>>>(a);
         return;
     }
     const size_t n = size_t(a.M) * a.N;

@@ -105,10 +105,11 @@ def test_linear_w8a16_matches_oracle(shape, dt, bias):
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 def test_w8a16_with_unit_scales_equals_dense_linear(dt):
     # codes are exact in bf16 / f16, and a scale of 1 multiplies exactly: the two entry
-    # points must agree bit for bit on the same sums
+    # points must agree bit for bit on the same sums (in_features a multiple of 16, so both
+    # take the MFMA path, which sums in the same order)
     rng = np.random.default_rng(6)
-    x = sample(rng, (100, 520), dt, 0.1)
-    codes = rng.integers(-127, 128, size=(300, 520), dtype=np.int8)
+    x = sample(rng, (100, 528), dt, 0.1)
+    codes = rng.integers(-127, 128, size=(300, 528), dtype=np.int8)
     w = {"bf16": f32_to_bf16(codes.astype(np.float32)), "f16": codes.astype(np.float16)}[dt]
     b = sample(rng, (300,), dt)
     got = linear_w8a16(x, codes, np.ones(300, np.float32), b, dt)
