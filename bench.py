@@ -371,12 +371,11 @@ def attention_ops(L, rng):
     return ops, P
 
 
-def measure_attention(L, hip, stream, e0, e1, steps):
-    """Times the attention_ops cases (HIP events on the library stream)."""
-    print("bench: building attention buffers", file=sys.stderr, flush=True)
-    aops, apool = attention_ops(L, np.random.default_rng(11))
+def time_cases(L, hip, stream, e0, e1, steps, cases):
+    """Times (name, kind, amount per launch, launch(i)) cases with HIP events on the library
+    stream; kind "bytes" is rated against HBM, "flops" against the bf16 MFMA peak."""
     res = {}
-    for name, kind, amount, fn in aops:
+    for name, kind, amount, fn in cases:
         for i in range(3):
             fn(i)
         reps = max(steps // 2, 10)
@@ -395,8 +394,70 @@ def measure_attention(L, hip, stream, e0, e1, steps):
                          "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4),
                          "bound": "mfma (bf16 dense peak)"}
     assert L.take_device_error() == 0
+    return res
+
+
+def measure_attention(L, hip, stream, e0, e1, steps):
+    """Times the attention_ops cases."""
+    print("bench: building attention buffers", file=sys.stderr, flush=True)
+    aops, apool = attention_ops(L, np.random.default_rng(11))
+    res = time_cases(L, hip, stream, e0, e1, steps, aops)
     del aops, apool
     print("bench: attention " + json.dumps(res), file=sys.stderr, flush=True)
+    return res
+
+
+def linear_ops(L, rng):
+    """(name, kind, amount per launch, launch(i)) for the Qwen2-1.5B projections: decode
+    (one token: HBM-bound on the weights; bytes = weights (+ scales) + x + out) and a
+    2048-token prefill (MFMA-bound; flops = 2 * rows * in * out), dense bf16 and W8A16 (INT8
+    codes + per-channel scales from llaisysQuantizeInt8 of the bf16 weights)."""
+    O, BF, F32, I8 = L.Ops, L.DataType.BF16, L.DataType.F32, L.DataType.I8
+    P = Pool(L, rng)
+    ops = []
+
+    def weights(out_f, in_f, sets):
+        w = P.fill((out_f, in_f), BF, sets, 0.02)
+        q, sc = P.empty((out_f, in_f), I8, sets), P.empty((out_f,), F32, sets)
+        for j in range(sets):
+            O.quantize_int8(q[j], sc[j], w[j])
+        return w, q, sc
+
+    for label, in_f, out_f in (("gate/up [8960, 1536]", H, I), ("down [1536, 8960]", I, H)):
+        sets = P.sets_for(out_f * in_f * 2)
+        w, q, sc = weights(out_f, in_f, sets)
+        x1 = P.fill((1, in_f), BF, sets)
+        o1 = P.empty((1, out_f), BF, 1)[0]
+        io = (in_f + out_f) * 2
+        ops.append((f"decode 1 token, {label}, bf16 weights", "bytes", out_f * in_f * 2 + io,
+                    lambda i, x1=x1, w=w, o1=o1, n=sets: O.linear(o1, x1[i % n], w[i % n])))
+        ops.append((f"decode 1 token, {label}, INT8 weights (W8A16)", "bytes", out_f * (in_f + 4) + io,
+                    lambda i, x1=x1, q=q, sc=sc, o1=o1, n=sets: O.linear_w8a16(o1, x1[i % n], q[i % n], sc[i % n])))
+        tp = 2048
+        xp = P.fill((tp, in_f), BF, 1)[0]
+        op_ = P.empty((tp, out_f), BF, 1)[0]
+        fl = 2 * tp * in_f * out_f
+        ops.append((f"prefill 2048 tokens, {label}, bf16 weights", "flops", fl,
+                    lambda i, xp=xp, w=w, op_=op_: O.linear(op_, xp, w[0])))
+        ops.append((f"prefill 2048 tokens, {label}, INT8 weights (W8A16)", "flops", fl,
+                    lambda i, xp=xp, q=q, sc=sc, op_=op_: O.linear_w8a16(op_, xp, q[0], sc[0])))
+    # lm_head: one set (467 MB already exceeds the Infinity Cache)
+    wl, ql, scl = weights(V, H, 1)
+    xl, ol = P.fill((1, H), BF, 1)[0], P.empty((1, V), BF, 1)[0]
+    ops.append(("decode 1 token, lm_head [151936, 1536], bf16 weights", "bytes", V * H * 2 + (H + V) * 2,
+                lambda i: O.linear(ol, xl, wl[0])))
+    ops.append(("decode 1 token, lm_head [151936, 1536], INT8 weights (W8A16)", "bytes",
+                V * (H + 4) + (H + V) * 2, lambda i: O.linear_w8a16(ol, xl, ql[0], scl[0])))
+    return ops, P
+
+
+def measure_linear(L, hip, stream, e0, e1, steps):
+    """Times the linear_ops cases."""
+    print("bench: building linear buffers", file=sys.stderr, flush=True)
+    lops, lpool = linear_ops(L, np.random.default_rng(13))
+    res = time_cases(L, hip, stream, e0, e1, steps, lops)
+    del lops, lpool
+    print("bench: linear " + json.dumps(res), file=sys.stderr, flush=True)
     return res
 
 
@@ -511,6 +572,9 @@ def main():
     ap.add_argument("--attention-only", action="store_true",
                     help="only the self-attention lines (profiling); prints their JSON")
     ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain (profiling)")
+    ap.add_argument("--no-linear", action="store_true", help="skip the linear lines")
+    ap.add_argument("--linear-only", action="store_true",
+                    help="only the linear lines (profiling); prints their JSON")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="3 dispatches of a 256 MiB device copy (counter calibration), then 3 of "
                          "each config-1 op, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -533,6 +597,10 @@ def main():
         for _ in range(args.steps):
             graph.launch()
         api.device_synchronize()
+        return
+    if args.linear_only:
+        print(json.dumps({"linear": measure_linear(L, hip, stream, e0=hip.event(), e1=hip.event(),
+                                                   steps=args.steps)}), flush=True)
         return
     if args.attention_only:
         print(json.dumps({"attention": measure_attention(L, hip, stream, e0=hip.event(), e1=hip.event(),
@@ -650,6 +718,9 @@ def main():
     attention = None
     if not args.no_attention:
         attention = measure_attention(L, hip, stream, e0, e1, args.steps)
+    linear = None
+    if not args.no_linear:
+        linear = measure_linear(L, hip, stream, e0, e1, args.steps)
 
     dom = per_op["swiglu"]
     roof = {"kernel": "swiglu binaryVec<BF16> [8192, 8960]", "bound": "hbm",
@@ -671,7 +742,7 @@ def main():
         "tokens_per_s": round(T / (ms_step * 1e-3)),
         "wall_s_timed": round(wall, 3),
         "per_op": per_op, "chain": chain, "configs": configs, "attention": attention,
-        "roofline": roof,
+        "linear": linear, "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

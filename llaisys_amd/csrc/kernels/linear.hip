@@ -345,6 +345,73 @@ __global__ void __launch_bounds__(1024)
     }
 }
 
+// One or two rows (decode): each wave owns one output channel and streams its weight row,
+// 16 bytes per lane per load (1 KB contiguous per instruction, the pattern that streams HBM
+// fastest), with FMAs in f32 against the matching x chunks (cache hits) and a DPP /
+// permlane butterfly over the lane partials at the end.  No LDS and no cross-block
+// synchronisation, so N output channels give N waves however small N is.
+template <typename T, bool kInt8, int M>
+__global__ void __launch_bounds__(256)
+    linearGemv(LinearArgs a) {
+    constexpr int E = kInt8 ? 16 : 8;  // weight elements per 16-byte chunk
+    constexpr int U = 4;               // chunks in flight per lane
+    const int lane = int(threadIdx.x) % kWave;
+    const int n = int(blockIdx.x) * 4 + int(threadIdx.x) / kWave; // wave-uniform
+    if (n >= a.N) return;
+    const int nc = a.K / E; // K % E == 0
+    const char *wrow = static_cast<const char *>(a.w) + size_t(n) * a.K * (kInt8 ? 1 : 2);
+    const char *xb = static_cast<const char *>(a.x);
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+    for (int c0 = lane; c0 < nc; c0 += kWave * U) {
+        // all loads first (a chunk past the row end reads chunk 0 and is masked below)
+        v4u wv[U], xv[U][M][E / 8];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + kWave * u < nc ? c0 + kWave * u : 0;
+            wv[u] = *reinterpret_cast<const v4u *>(wrow + size_t(c) * 16);
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int h = 0; h < E / 8; ++h)
+                    xv[u][m][h] = *reinterpret_cast<const v4u *>(xb + (size_t(m) * a.K + size_t(c) * E + 8 * h) * 2);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + kWave * u >= nc) continue;
+            float wf[E];
+            if constexpr (kInt8) {
+                const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+                for (int e = 0; e < E; ++e) wf[e] = float(int8_t(ww[e / 4] >> (8 * (e % 4))));
+            } else {
+                Fmt<T>::unpack(wv[u], wf);
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int h = 0; h < E / 8; ++h) {
+                    float xf[8];
+                    Fmt<T>::unpack(xv[u][m][h], xf);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[m] = __builtin_fmaf(xf[e], wf[8 * h + e], acc[m]);
+                }
+        }
+    }
+    const float sc = kInt8 ? a.scale[n] : 1.0f;
+    const float bv = a.bias ? Fmt<T>::get(a.bias, n) : 0.0f;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float s = waveGroupReduce<kWave, SumOp>(acc[m]);
+        if (lane == 0) {
+            if constexpr (kInt8) s = sc * s;
+            if (a.bias) s = s + bv;
+            Fmt<T>::put(a.out, size_t(m) * a.N + n, s);
+        }
+    }
+}
+
 // Any shape and type: one thread per output, the sum in the reference's order.
 template <typename T, bool kInt8>
 __global__ void __launch_bounds__(256)
@@ -370,6 +437,18 @@ void launch(const LinearArgs &a, hipStream_t s) {
     // MFMA paths: 16-bit activations, 16-byte aligned rows (K % 8 == 0; INT8 codes K % 16 == 0)
     if (kMfmaType && a.K > 0 && a.K % (kInt8 ? 16 : 8) == 0 && al(a.x, 16) && al(a.w, 16)) {
         if constexpr (kMfmaType) {
+            // one or two rows: the VALU GEMV (one wave per channel) while its f32 work stays
+            // under the HBM time -- always for 16-bit weights; for INT8 weights (16 codes per
+            // 16 bytes to convert) only when there are too few 16-channel tiles for the MFMA
+            // kernel to occupy the chip
+            if (a.M <= 2 && (!kInt8 || (a.N + 15) / 16 < 256)) {
+                const unsigned blocks = unsigned((a.N + 3) / 4);
+                if (a.M == 1)
+                    linearGemv<T, kInt8, 1><<<blocks, 256, 0, s>>>(a);
+                else
+                    linearGemv<T, kInt8, 2><<<blocks, 256, 0, s>>>(a);
+                return;
+            }
             if (a.M <= 16) {
                 // waves per block: enough blocks x waves to fill the chip, at most one wave
                 // per group of 128 k

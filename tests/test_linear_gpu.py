@@ -52,6 +52,8 @@ SHAPES = [
     # block tile, in_features not a multiple of 8 (scalar path), one output
     (2, 4, 3), (1, 1536, 1536), (1, 1536, 256), (1, 1536, 8960), (1, 8960, 1536),
     (256, 1536, 1536), (129, 264, 200), (17, 40, 130), (3, 77, 9), (64, 1536, 1), (1, 8, 1),
+    # few rows over few output tiles: K split across blocks (ragged last split, 16 rows)
+    (16, 4096, 300), (2, 2056, 40),
 ]
 
 
@@ -129,3 +131,23 @@ def test_w8a16_of_quantized_weights_tracks_dense_linear():
     gf = (got.astype(np.uint32) << 16).view(np.float32)
     df = (dense.astype(np.uint32) << 16).view(np.float32)
     assert np.abs(gf - df).max() < 0.02 * np.abs(df).max()
+
+
+def test_split_k_linear_repeats_and_interleaves_with_argmax():
+    # the split-K few-row path keeps per-tile arrival counters in the library scratch next to
+    # the flat argmax's counter; both must return to zero, so repeated and interleaved calls
+    # give identical results
+    rng = np.random.default_rng(8)
+    x, w = sample(rng, (1, 8960), "bf16"), sample(rng, (1536, 8960), "bf16", 0.02)
+    tx, tw = dev(x, DTS["bf16"]), dev(w, DTS["bf16"])
+    logits = dev(sample(rng, (1, 151936), "bf16"), DTS["bf16"])
+    outs = []
+    for _ in range(3):
+        out = L.Tensor((1, 1536), DTS["bf16"], **AMD)
+        L.Ops.linear(out, tx, tw)
+        i, v = L.Tensor((1,), L.DataType.I64, **AMD), L.Tensor((1,), DTS["bf16"], **AMD)
+        L.Ops.argmax(i, v, logits)
+        outs.append(out.numpy())
+    for o in outs[1:]:
+        assert_exact(o, outs[0], "repeat")
+    assert_linear_close(outs[0], oracle.linear(x, w), x, w, "split-K decode")
