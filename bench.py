@@ -461,6 +461,33 @@ def measure_linear(L, hip, stream, e0, e1, steps):
     return res
 
 
+def rearrange_ops(L, rng):
+    """(name, "bytes", bytes per launch, launch(i)) for the strided copy behind
+    Tensor::contiguous: q [2048, 12, 128] bf16 to head-major (rows of 256 B) and a
+    [8192, 8192] bf16 transpose (LDS tiles); bytes = read + write."""
+    O, BF = L.Ops, L.DataType.BF16
+    P = Pool(L, rng)
+    ops = []
+    for label, shape, perm in (("q [2048, 12, 128] -> [12, 2048, 128] bf16", (2048, 12, 128), (1, 0, 2)),
+                               ("transpose [8192, 8192] bf16", (8192, 8192), (1, 0))):
+        n = int(np.prod(shape))
+        sets = P.sets_for(2 * n * 2)
+        src = [t.permute(*perm) for t in P.fill(shape, BF, sets)]
+        dst = P.empty(src[0].shape(), BF, sets)
+        ops.append((f"rearrange {label}", "bytes", 2 * n * 2,
+                    lambda i, src=src, dst=dst, k=sets: O.rearrange(dst[i % k], src[i % k])))
+    return ops, P
+
+
+def measure_rearrange(L, hip, stream, e0, e1, steps):
+    print("bench: building rearrange buffers", file=sys.stderr, flush=True)
+    rops, rpool = rearrange_ops(L, np.random.default_rng(17))
+    res = time_cases(L, hip, stream, e0, e1, steps, rops)
+    del rops, rpool
+    print("bench: rearrange " + json.dumps(res), file=sys.stderr, flush=True)
+    return res
+
+
 def cpu_baseline(seconds):
     """Reference CPU ops (oracle/_ref, else the oracle port) on a row sample of config 1,
     single thread pinned to one core; GB/s with the same bytes formula as the GPU."""
@@ -572,9 +599,9 @@ def main():
     ap.add_argument("--attention-only", action="store_true",
                     help="only the self-attention lines (profiling); prints their JSON")
     ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain (profiling)")
-    ap.add_argument("--no-linear", action="store_true", help="skip the linear lines")
+    ap.add_argument("--no-linear", action="store_true", help="skip the linear and rearrange lines")
     ap.add_argument("--linear-only", action="store_true",
-                    help="only the linear lines (profiling); prints their JSON")
+                    help="only the linear and rearrange lines (profiling); prints their JSON")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="3 dispatches of a 256 MiB device copy (counter calibration), then 3 of "
                          "each config-1 op, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
@@ -599,8 +626,9 @@ def main():
         api.device_synchronize()
         return
     if args.linear_only:
-        print(json.dumps({"linear": measure_linear(L, hip, stream, e0=hip.event(), e1=hip.event(),
-                                                   steps=args.steps)}), flush=True)
+        res = measure_linear(L, hip, stream, e0=hip.event(), e1=hip.event(), steps=args.steps)
+        res.update(measure_rearrange(L, hip, stream, e0=hip.event(), e1=hip.event(), steps=args.steps))
+        print(json.dumps({"linear": res}), flush=True)
         return
     if args.attention_only:
         print(json.dumps({"attention": measure_attention(L, hip, stream, e0=hip.event(), e1=hip.event(),
@@ -721,6 +749,7 @@ def main():
     linear = None
     if not args.no_linear:
         linear = measure_linear(L, hip, stream, e0, e1, args.steps)
+        linear.update(measure_rearrange(L, hip, stream, e0, e1, args.steps))
 
     dom = per_op["swiglu"]
     roof = {"kernel": "swiglu binaryVec<BF16> [8192, 8960]", "bound": "hbm",

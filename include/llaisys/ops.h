@@ -8,11 +8,9 @@
  * HIP kernel launches on the context stream (llaisysGetContextStream).
  *
  * Scope of this library: the bandwidth-bound per-layer ops and the attention that reads
- * their INT8 KV cache, and the linear layers (dense, and over INT8 weights).
- * llaisysRearrange is exported so that the reference's ctypes loader binds, and raises
- * "Unimplemented function" (the reference's own rearrange is a stub,
- * src/ops/rearrange/op.cpp:4-6).  Ops on CPU tensors raise "Unsupported device":
- * this library has no CPU compute path.
+ * their INT8 KV cache, the linear layers (dense, and over INT8 weights) and the strided
+ * copy (rearrange) behind the tensor plumbing.  Ops on CPU tensors raise "Unsupported
+ * device": this library has no CPU compute path.
  */
 #ifndef LLAISYS_OPS_H
 #define LLAISYS_OPS_H
@@ -34,7 +32,9 @@ __C {
      * dtype, f32 accumulation; a NULL or zero-element bias means no bias. */
     __export void llaisysLinear(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight,
                                 llaisysTensor_t bias);
-    /* reference ops.h:11 -- out of scope here: raises "Unimplemented function" */
+    /* reference ops.h:11 (a stub there, src/ops/rearrange/op.cpp:4-6) -- out[i] = in[i] for
+     * every multi-index i: same shape, dtype and device, any strides, at most 8 dims;
+     * bit-exact copy. */
     __export void llaisysRearrange(llaisysTensor_t out, llaisysTensor_t in);
     /* reference ops.h:12 -- per last-dim row: y = x * w / sqrt(mean(x^2) + eps) */
     __export void llaisysRmsNorm(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight,

@@ -47,6 +47,18 @@ __C {
     /* reference tensor.h:61-64 -- [start, end) along dim */
     __export llaisysTensor_t tensorSlice(llaisysTensor_t tensor, size_t dim, size_t start,
                                          size_t end);
+    /* reference Tensor::contiguous (src/tensor/tensor.hpp:55, a stub at tensor.cpp:344-347;
+     * no C entry point there) -- the tensor itself when contiguous (shared storage), else a
+     * contiguous copy on the same device (llaisysRearrange on AMD devices) */
+    __export llaisysTensor_t tensorContiguous(llaisysTensor_t tensor);
+    /* reference Tensor::reshape (tensor.hpp:56, a stub at tensor.cpp:349-352) -- a view
+     * when contiguous, else a view of tensorContiguous */
+    __export llaisysTensor_t tensorReshape(llaisysTensor_t tensor, size_t *shape, size_t ndim);
+    /* reference Tensor::to (tensor.hpp:57, a stub at tensor.cpp:354-357) -- the tensor itself
+     * when already there, else a contiguous copy on (device_type, device); device < 0 keeps
+     * the id for the same device type, else 0.  Synchronous. */
+    __export llaisysTensor_t tensorTo(llaisysTensor_t tensor, llaisysDeviceType_t device_type,
+                                      int device);
 }
 
 #endif /* LLAISYS_TENSOR_H */

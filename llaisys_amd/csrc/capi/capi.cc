@@ -111,6 +111,17 @@ __C {
         return wrap(t->tensor->slice(dim, start, end));
     }
 
+    // reference src/tensor/tensor.hpp:55-57 (C++ only there)
+    llaisysTensor_t tensorContiguous(llaisysTensor_t t) { return wrap(t->tensor->contiguous()); }
+
+    llaisysTensor_t tensorReshape(llaisysTensor_t t, size_t * shape, size_t ndim) {
+        return wrap(t->tensor->reshape(std::vector<size_t>(shape, shape + ndim)));
+    }
+
+    llaisysTensor_t tensorTo(llaisysTensor_t t, llaisysDeviceType_t device_type, int device) {
+        return wrap(t->tensor->to(device_type, device));
+    }
+
     // ---- ops (reference src/llaisys/ops.cc:19-45) --------------------------------------
     void llaisysAdd(llaisysTensor_t c, llaisysTensor_t a, llaisysTensor_t b) {
         llaisys::ops::add(c->tensor, a->tensor, b->tensor);
@@ -125,7 +136,9 @@ __C {
                        llaisysTensor_t bias) {
         llaisys::ops::linear(out->tensor, in->tensor, weight->tensor, bias ? bias->tensor : nullptr);
     }
-    void llaisysRearrange(llaisysTensor_t, llaisysTensor_t) { TO_BE_IMPLEMENTED(); }
+    void llaisysRearrange(llaisysTensor_t out, llaisysTensor_t in) {
+        llaisys::ops::rearrange(out->tensor, in->tensor);
+    }
     void llaisysRmsNorm(llaisysTensor_t out, llaisysTensor_t in, llaisysTensor_t weight, float eps) {
         llaisys::ops::rmsNorm(out->tensor, in->tensor, weight->tensor, eps);
     }

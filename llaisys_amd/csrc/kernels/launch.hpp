@@ -102,4 +102,9 @@ void linear(void *out, const void *x, const void *w, const float *w_scale, const
             size_t rows, size_t in_features, size_t out_features, llaisysDataType_t dt,
             hipStream_t stream);
 
+// out[i] = in[i] for every multi-index i of `shape` (ndim <= 8), element strides per layout,
+// elements of esize (1, 2, 4 or 8) bytes.
+void rearrange(void *out, const void *in, size_t ndim, const size_t *shape, const ptrdiff_t *in_strides,
+               const ptrdiff_t *out_strides, size_t esize, hipStream_t stream);
+
 } // namespace llaisys::kernels

@@ -1,0 +1,195 @@
+// Strided copy between two layouts of one shape: out[i] = in[i] for every multi-index i.
+//
+// The reference's rearrange is a stub (src/ops/rearrange/op.cpp:4-6); its meaning is fixed by
+// its signature and by Tensor::contiguous / Tensor::to (src/tensor/tensor.hpp:55-57), which
+// need exactly this copy.  Bytes only -- no arithmetic -- so results are bit-exact.
+//
+// Host side: size-1 dimensions are dropped and neighbours that are contiguous in both
+// layouts are merged, so most copies reach one of three kernels:
+//  - rowCopy:   the innermost dimension is contiguous in both layouts: rows of R bytes are
+//               copied in the widest unit (16 / 8 / 4 / 2 / 1 B) that divides R and the
+//               base addresses; HBM-bound, 1 read + 1 write per byte.
+//  - tileCopy:  the output's contiguous dimension is strided in the input, and another
+//               dimension is contiguous there (a transpose): 32 x 32 element tiles through LDS,
+//               both sides coalesced; HBM-bound.
+//  - gatherCopy: anything else, one thread per element.
+#include "common.hpp"
+#include "launch.hpp"
+
+#include <algorithm>
+#include <cstring>
+
+namespace llaisys::kernels {
+
+namespace {
+
+constexpr int kMaxDims = 8;
+
+struct Dims {
+    int nd;
+    int64_t shape[kMaxDims];
+    int64_t sin[kMaxDims];  // element strides
+    int64_t sout[kMaxDims];
+};
+
+// offsets of linear index `idx` over the first nd dims (row-major over `shape`)
+__device__ __forceinline__ void offsets(const Dims &d, int nd, int64_t idx, int64_t &oi, int64_t &oo) {
+    oi = 0;
+    oo = 0;
+    for (int k = nd - 1; k >= 0; --k) {
+        const int64_t c = idx % d.shape[k];
+        idx /= d.shape[k];
+        oi += c * d.sin[k];
+        oo += c * d.sout[k];
+    }
+}
+
+template <typename U>
+__global__ void __launch_bounds__(256)
+    rowCopy(char *out, const char *in, Dims d, int64_t rows, int64_t units, int esize) {
+    // d covers the outer dims (the row index); a row is `units` units of U, contiguous in both
+    const int64_t total = rows * units;
+    for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < total; t += int64_t(gridDim.x) * 256) {
+        const int64_t r = t / units, u = t % units;
+        int64_t oi, oo;
+        offsets(d, d.nd, r, oi, oo);
+        reinterpret_cast<U *>(out + oo * esize)[u] = reinterpret_cast<const U *>(in + oi * esize)[u];
+    }
+}
+
+// dims p (input-contiguous) and q (output-contiguous) tiled 32 x 32; the other dims of d
+// (without p and q) index blockIdx.z
+template <typename E>
+__global__ void __launch_bounds__(256)
+    tileCopy(E *out, const E *in, Dims rest, int64_t np, int64_t nq, int64_t sp_out, int64_t sq_in) {
+    __shared__ E tile[32][33];
+    int64_t oi, oo;
+    offsets(rest, rest.nd, blockIdx.z, oi, oo);
+    const int64_t p0 = int64_t(blockIdx.x) * 32, q0 = int64_t(blockIdx.y) * 32;
+    const int tx = threadIdx.x % 32, ty = threadIdx.x / 32;
+    // read: consecutive threads walk p (contiguous in the input)
+#pragma unroll
+    for (int k = 0; k < 32; k += 8) {
+        const int64_t p = p0 + tx, q = q0 + ty + k;
+        if (p < np && q < nq) tile[ty + k][tx] = in[oi + p + q * sq_in];
+    }
+    __syncthreads();
+    // write: consecutive threads walk q (contiguous in the output)
+#pragma unroll
+    for (int k = 0; k < 32; k += 8) {
+        const int64_t q = q0 + tx, p = p0 + ty + k;
+        if (p < np && q < nq) out[oo + q + p * sp_out] = tile[tx][ty + k];
+    }
+}
+
+template <typename E>
+__global__ void __launch_bounds__(256)
+    gatherCopy(E *out, const E *in, Dims d, int64_t n) {
+    for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < n; t += int64_t(gridDim.x) * 256) {
+        int64_t oi, oo;
+        offsets(d, d.nd, t, oi, oo);
+        out[oo] = in[oi];
+    }
+}
+
+unsigned gridFor(int64_t work) {
+    return unsigned(std::min<int64_t>((work + 255) / 256, int64_t(256) * 64));
+}
+
+} // namespace
+
+void rearrange(void *out, const void *in, size_t ndim, const size_t *shape, const ptrdiff_t *in_strides,
+               const ptrdiff_t *out_strides, size_t esize, hipStream_t s) {
+    // drop size-1 dims, then merge neighbours contiguous in both layouts
+    Dims d{};
+    int64_t n = 1;
+    for (size_t k = 0; k < ndim; ++k) {
+        n *= int64_t(shape[k]);
+        if (shape[k] == 1) continue;
+        const int64_t sh = int64_t(shape[k]), si = in_strides[k], so = out_strides[k];
+        if (d.nd > 0 && d.sin[d.nd - 1] == sh * si && d.sout[d.nd - 1] == sh * so) {
+            d.shape[d.nd - 1] *= sh;
+            d.sin[d.nd - 1] = si;
+            d.sout[d.nd - 1] = so;
+        } else {
+            d.shape[d.nd] = sh;
+            d.sin[d.nd] = si;
+            d.sout[d.nd] = so;
+            ++d.nd;
+        }
+    }
+    if (n == 0) return;
+    char *o = static_cast<char *>(out);
+    const char *i = static_cast<const char *>(in);
+    if (d.nd == 0) { // one element
+        d.nd = 1;
+        d.shape[0] = 1;
+        d.sin[0] = d.sout[0] = 1;
+    }
+    const int last = d.nd - 1;
+    if (d.sin[last] == 1 && d.sout[last] == 1) {
+        // rows: the innermost dim is contiguous in both
+        const int64_t rowBytes = d.shape[last] * int64_t(esize);
+        Dims outer = d;
+        outer.nd = last;
+        const int64_t rows = n / d.shape[last];
+        int ub = 16;
+        const auto fits = [&](int b) {
+            if (rowBytes % b) return false;
+            if ((reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(i)) % b) return false;
+            for (int k = 0; k < outer.nd; ++k)
+                if ((outer.sin[k] * int64_t(esize)) % b || (outer.sout[k] * int64_t(esize)) % b) return false;
+            return true;
+        };
+        while (ub > 1 && !fits(ub)) ub /= 2;
+        const int64_t units = rowBytes / ub;
+        const unsigned g = gridFor(rows * units);
+        switch (ub) {
+        case 16: rowCopy<v4u><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+        case 8: rowCopy<uint64_t><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+        case 4: rowCopy<uint32_t><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+        case 2: rowCopy<uint16_t><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+        default: rowCopy<uint8_t><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+        }
+        return;
+    }
+    // transpose: output contiguous in dim q = last, input contiguous in some dim p != q
+    int p = -1;
+    for (int k = 0; k < last; ++k)
+        if (d.sin[k] == 1) p = k;
+    if (d.sout[last] == 1 && p >= 0 && (esize == 1 || esize == 2 || esize == 4 || esize == 8)) {
+        Dims rest{};
+        int64_t nz = 1;
+        for (int k = 0; k < last; ++k) {
+            if (k == p) continue;
+            rest.shape[rest.nd] = d.shape[k];
+            rest.sin[rest.nd] = d.sin[k];
+            rest.sout[rest.nd] = d.sout[k];
+            ++rest.nd;
+            nz *= d.shape[k];
+        }
+        if (nz <= 65535) {
+            const dim3 grid(unsigned((d.shape[p] + 31) / 32), unsigned((d.shape[last] + 31) / 32), unsigned(nz));
+            if (grid.y <= 65535) {
+                const int64_t np = d.shape[p], nq = d.shape[last], spo = d.sout[p], sqi = d.sin[last];
+                switch (esize) {
+                case 1: tileCopy<uint8_t><<<grid, 256, 0, s>>>(reinterpret_cast<uint8_t *>(o), reinterpret_cast<const uint8_t *>(i), rest, np, nq, spo, sqi); break;
+                case 2: tileCopy<uint16_t><<<grid, 256, 0, s>>>(reinterpret_cast<uint16_t *>(o), reinterpret_cast<const uint16_t *>(i), rest, np, nq, spo, sqi); break;
+                case 4: tileCopy<uint32_t><<<grid, 256, 0, s>>>(reinterpret_cast<uint32_t *>(o), reinterpret_cast<const uint32_t *>(i), rest, np, nq, spo, sqi); break;
+                default: tileCopy<uint64_t><<<grid, 256, 0, s>>>(reinterpret_cast<uint64_t *>(o), reinterpret_cast<const uint64_t *>(i), rest, np, nq, spo, sqi); break;
+                }
+                return;
+            }
+        }
+    }
+    const unsigned g = gridFor(n);
+    switch (esize) {
+    case 1: gatherCopy<uint8_t><<<g, 256, 0, s>>>(reinterpret_cast<uint8_t *>(o), reinterpret_cast<const uint8_t *>(i), d, n); break;
+    case 2: gatherCopy<uint16_t><<<g, 256, 0, s>>>(reinterpret_cast<uint16_t *>(o), reinterpret_cast<const uint16_t *>(i), d, n); break;
+    case 4: gatherCopy<uint32_t><<<g, 256, 0, s>>>(reinterpret_cast<uint32_t *>(o), reinterpret_cast<const uint32_t *>(i), d, n); break;
+    case 8: gatherCopy<uint64_t><<<g, 256, 0, s>>>(reinterpret_cast<uint64_t *>(o), reinterpret_cast<const uint64_t *>(i), d, n); break;
+    default: break; // element sizes are 1, 2, 4 or 8 bytes
+    }
+}
+
+} // namespace llaisys::kernels

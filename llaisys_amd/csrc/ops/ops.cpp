@@ -387,6 +387,17 @@ void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor
 }
 
 
+// reference src/ops/rearrange/op.cpp:4-6 (a stub there): out[i] = in[i] for every
+// multi-index, between any two layouts of one shape (Tensor::copyInto on the GPU).
+void rearrange(tensor_t out, tensor_t in) {
+    CHECK_SAME_DEVICE(out, in);
+    CHECK_SAME_SHAPE(out->shape(), in->shape());
+    CHECK_SAME_DTYPE(out->dtype(), in->dtype());
+    ASSERT(in->ndim() <= 8, "Rearrange: at most 8 dimensions");
+    streamFor(out); // AMD tensors only: this library has no CPU compute path
+    in->copyInto(out);
+}
+
 namespace {
 // Shape checks of reference src/ops/linear/op.cpp:10-42 (messages kept); a bias that is
 // null or has no elements means no bias.  Returns the row count.

@@ -1,6 +1,7 @@
 #include "tensor.hpp"
 
 #include "../device/runtime_api.hpp"
+#include "../kernels/launch.hpp"
 #include "../utils/check.hpp"
 #include "../utils/types.hpp"
 
@@ -170,6 +171,79 @@ void Tensor::load(const void *src) {
     const size_t bytes = numel() * elementSize();
     device::getRuntimeAPI(_storage->deviceType())
         ->memcpy_sync(data(), src, bytes, LLAISYS_MEMCPY_H2D);
+}
+
+namespace {
+// host strided copy of one element at a time (host tensors only: data movement, not compute)
+void hostCopy(std::byte *dst, const std::vector<ptrdiff_t> &sdst, const std::byte *src,
+              const std::vector<ptrdiff_t> &ssrc, const std::vector<size_t> &shape, size_t dim,
+              size_t esize) {
+    if (dim == shape.size()) {
+        std::memcpy(dst, src, esize);
+        return;
+    }
+    for (size_t i = 0; i < shape[dim]; i++)
+        hostCopy(dst + ptrdiff_t(i) * sdst[dim] * ptrdiff_t(esize), sdst,
+                 src + ptrdiff_t(i) * ssrc[dim] * ptrdiff_t(esize), ssrc, shape, dim + 1, esize);
+}
+} // namespace
+
+void Tensor::copyInto(const tensor_t &out) const {
+    CHECK_ARGUMENT(out->shape() == _shape, "copy: shapes differ");
+    CHECK_ARGUMENT(out->dtype() == _dtype, "copy: dtypes differ");
+    CHECK_ARGUMENT(out->deviceType() == deviceType() && out->deviceId() == deviceId(),
+                   "copy: tensors on different devices");
+    CHECK_ARGUMENT(_shape.size() <= 8, "copy: at most 8 dimensions");
+    if (numel() == 0) return;
+    if (deviceType() == LLAISYS_DEVICE_CPU) {
+        hostCopy(out->data(), out->strides(), data(), _strides, _shape, 0, elementSize());
+        return;
+    }
+    auto &ctx = core::context();
+    ctx.setDevice(deviceType(), deviceId());
+    auto s = static_cast<hipStream_t>(ctx.runtime().stream());
+    kernels::rearrange(out->data(), data(), _shape.size(), _shape.data(), _strides.data(),
+                       out->strides().data(), elementSize(), s);
+    device::amd::check(hipGetLastError(), "rearrange");
+}
+
+tensor_t Tensor::contiguous() const {
+    if (isContiguous()) return tensor_t(new Tensor(_dtype, _shape, _strides, _storage, _offset));
+    tensor_t out = create(_shape, _dtype, deviceType(), deviceId());
+    copyInto(out);
+    return out;
+}
+
+tensor_t Tensor::reshape(const std::vector<size_t> &shape) const {
+    if (product(shape) != numel())
+        throw std::runtime_error("Reshape shape mismatch: numel must be the same.");
+    return contiguous()->view(shape);
+}
+
+tensor_t Tensor::to(llaisysDeviceType_t device_type, int device) const {
+    if (device < 0) device = device_type == deviceType() ? deviceId() : 0;
+    if (device_type == deviceType() && device == deviceId())
+        return tensor_t(new Tensor(_dtype, _shape, _strides, _storage, _offset));
+    const tensor_t src = contiguous();
+    tensor_t dst = create(_shape, _dtype, device_type, device);
+    const size_t bytes = numel() * elementSize();
+    if (bytes == 0) return dst;
+    auto &ctx = core::context();
+    const bool fromGpu = deviceType() != LLAISYS_DEVICE_CPU, toGpu = device_type != LLAISYS_DEVICE_CPU;
+    if (fromGpu) { // the source may still be written by work queued on its stream
+        ctx.setDevice(deviceType(), deviceId());
+        ctx.runtime().api()->device_synchronize();
+    }
+    if (!fromGpu && !toGpu) {
+        std::memcpy(dst->data(), src->data(), bytes);
+        return dst;
+    }
+    const llaisysMemcpyKind_t kind = fromGpu && toGpu ? LLAISYS_MEMCPY_D2D
+                                     : fromGpu         ? LLAISYS_MEMCPY_D2H
+                                                       : LLAISYS_MEMCPY_H2D;
+    ctx.setDevice(toGpu ? device_type : deviceType(), toGpu ? device : deviceId());
+    ctx.runtime().api()->memcpy_sync(dst->data(), src->data(), bytes, kind);
+    return dst;
 }
 
 } // namespace llaisys

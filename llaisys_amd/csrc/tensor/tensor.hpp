@@ -46,6 +46,18 @@ public:
     // Synchronous copy of numel() * elementSize() bytes from host memory.
     void load(const void *src);
 
+    // Reference tensor.hpp:55-57 (stubs there, tensor.cpp:344-357).
+    // contiguous(): this tensor when already contiguous (shared storage), else a new
+    // contiguous tensor on the same device holding a copy (a GPU rearrange on AMD devices).
+    tensor_t contiguous() const;
+    // reshape(): a view when contiguous, else a view of contiguous().
+    tensor_t reshape(const std::vector<size_t> &shape) const;
+    // to(): this tensor when already on (device_type, device), else a contiguous copy there.
+    // device < 0 means this tensor's device id for the same device type, else 0.
+    tensor_t to(llaisysDeviceType_t device_type, int device = -1) const;
+    // Element-by-element copy into `out` (same shape and dtype, same device).
+    void copyInto(const tensor_t &out) const;
+
 private:
     Tensor(llaisysDataType_t dt, std::vector<size_t> shape, std::vector<ptrdiff_t> strides,
            core::storage_t storage, size_t offset)

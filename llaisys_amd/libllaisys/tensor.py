@@ -32,3 +32,14 @@ def load_tensor(lib):
         fn = getattr(lib, name)
         fn.argtypes = args
         fn.restype = res
+    # additive entry points (bound when present, so the reference library also loads)
+    added = {
+        "tensorContiguous": ([llaisysTensor_t], llaisysTensor_t),
+        "tensorReshape": ([llaisysTensor_t, POINTER(c_size_t), c_size_t], llaisysTensor_t),
+        "tensorTo": ([llaisysTensor_t, llaisysDeviceType_t, c_int], llaisysTensor_t),
+    }
+    for name, (args, res) in added.items():
+        if hasattr(lib, name):
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = res

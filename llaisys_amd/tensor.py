@@ -88,6 +88,22 @@ class Tensor:
         return Tensor(tensor=self._lib.tensorSlice(self._tensor, c_size_t(dim), c_size_t(start),
                                                    c_size_t(end)), lib=self._lib)
 
+    def contiguous(self) -> "Tensor":
+        """This tensor when contiguous (shared storage), else a contiguous copy on the same
+        device (reference Tensor::contiguous, src/tensor/tensor.hpp:55)."""
+        return Tensor(tensor=self._lib.tensorContiguous(self._tensor), lib=self._lib)
+
+    def reshape(self, *shape: int) -> "Tensor":
+        """A view when contiguous, else a view of contiguous() (reference tensor.hpp:56)."""
+        dims = (c_size_t * len(shape))(*shape)
+        return Tensor(tensor=self._lib.tensorReshape(self._tensor, dims, c_size_t(len(shape))),
+                      lib=self._lib)
+
+    def to(self, device: "DeviceType", device_id: int = -1) -> "Tensor":
+        """This tensor when already on (device, device_id), else a contiguous copy there
+        (reference Tensor::to, tensor.hpp:57).  Synchronous."""
+        return Tensor(tensor=self._lib.tensorTo(self._tensor, device, c_int(device_id)), lib=self._lib)
+
     # ---- numpy helpers --------------------------------------------------------------
     def numel(self) -> int:
         return int(np.prod(self.shape(), dtype=np.int64))

@@ -108,6 +108,28 @@ def test_tensor_metadata_like_reference_test_tensor():
     assert s0.data_ptr() == t.data_ptr() + 20 * 4
 
 
+def test_tensor_contiguous_reshape_to_on_host_tensors():
+    # host tensors: contiguous / reshape / to are data movement (reference tensor.hpp:55-57)
+    data = np.arange(3 * 4 * 5, dtype=np.float32).reshape(3, 4, 5)
+    t = L.Tensor.from_numpy(data, device=L.DeviceType.CPU)
+    same = t.contiguous()
+    assert same.data_ptr() == t.data_ptr()  # already contiguous: shared storage
+    p = t.permute(2, 0, 1)
+    c = p.contiguous()
+    assert c.is_contiguous() and c.data_ptr() != t.data_ptr()
+    assert np.array_equal(c.numpy(), np.ascontiguousarray(data.transpose(2, 0, 1)))
+    s = t.slice(2, 1, 4)
+    assert np.array_equal(s.contiguous().numpy(), data[:, :, 1:4])
+    r = p.reshape(5, 12)
+    assert r.shape() == (5, 12) and np.array_equal(r.numpy(), data.transpose(2, 0, 1).reshape(5, 12))
+    assert t.reshape(60).data_ptr() == t.data_ptr()
+    h = p.to(L.DeviceType.CPU)
+    assert h.data_ptr() == p.data_ptr() and not h.is_contiguous()  # already there
+    i8 = L.Tensor.from_numpy(np.arange(24, dtype=np.int8).reshape(2, 3, 4), device=L.DeviceType.CPU)
+    assert np.array_equal(i8.permute(1, 2, 0).contiguous().numpy(),
+                          np.arange(24, dtype=np.int8).reshape(2, 3, 4).transpose(1, 2, 0))
+
+
 def test_tensor_load_and_bf16_roundtrip():
     from llaisys_amd.hostfmt import bf16_to_f32, f32_to_bf16
     x = np.random.default_rng(0).standard_normal((7, 9)).astype(np.float32)
@@ -139,7 +161,8 @@ def _run(code):
     ("L.Ops.rope(t((2,1,3)), t((2,1,3)), t((2,), L.DataType.I64), 1e4)", "Head dimension must be even"),
     ("L.Ops.embedding(t((2,4)), t((2,), L.DataType.F32), t((8,4)))", "index data type must be INT32 or INT64"),
     ("L.Ops.argmax(t((1,), L.DataType.F32), t((1,)), t((8,)))", "max_idx must be INT32 or INT64"),
-    ("L.Ops.rearrange(t((2,2)), t((2,2)))", "Unimplemented function"),
+    ("L.Ops.rearrange(t((2,2)), t((2,2)))", "Unsupported device"),
+    ("L.Ops.rearrange(t((2,3)), t((3,2)))", "Shapes mismatch"),
     ("L.Ops.linear(t((2,2)), t((2,2)), t((2,2)), t((3,)))", "Linear: bias shape mismatch"),
     ("L.Ops.linear(t((2,3)), t((2,2)), t((2,2)), t((2,)))", "Linear: output feature dim mismatch"),
     ("L.Ops.linear(t((2,2)), t((2,2)), t((2,2)))", "Unsupported device"),
