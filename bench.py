@@ -479,11 +479,27 @@ def rearrange_ops(L, rng):
     return ops, P
 
 
+def sample_ops(L, rng):
+    """(name, "bytes", logits bytes per launch, launch(i)) for llaisysRandomSample over one
+    row of the Qwen2 vocabulary (bf16): the reference generate() defaults (T 0.8, top_p 0.8)
+    with top_k 50 and 1024, and the greedy case (argmax).  Latency-bound (one 297 KB row)."""
+    O, BF, I64 = L.Ops, L.DataType.BF16, L.DataType.I64
+    P = Pool(L, rng)
+    sets = 16
+    lg = P.fill((1, V), BF, sets, 3.0)
+    out = P.empty((1,), I64, 1)[0]
+    return [(f"sample 1 x {V} bf16, T 0.8, top_k {k}, top_p 0.8", "bytes", V * 2,
+             lambda i, k=k: O.random_sample(out, lg[i % sets], 0.8, k, 0.8, i)) for k in (50, 1024)] + [
+        (f"sample 1 x {V} bf16, greedy (argmax)", "bytes", V * 2,
+         lambda i: O.random_sample(out, lg[i % sets], 0.0, 50, 0.8, i))], P
+
+
 def measure_rearrange(L, hip, stream, e0, e1, steps):
-    print("bench: building rearrange buffers", file=sys.stderr, flush=True)
+    print("bench: building rearrange and sampling buffers", file=sys.stderr, flush=True)
     rops, rpool = rearrange_ops(L, np.random.default_rng(17))
-    res = time_cases(L, hip, stream, e0, e1, steps, rops)
-    del rops, rpool
+    sops, spool = sample_ops(L, np.random.default_rng(19))
+    res = time_cases(L, hip, stream, e0, e1, steps, rops + sops)
+    del rops, rpool, sops, spool
     print("bench: rearrange " + json.dumps(res), file=sys.stderr, flush=True)
     return res
 

@@ -132,6 +132,19 @@ __C {
     __export void llaisysLinearW8A16(llaisysTensor_t out, llaisysTensor_t in,
                                      llaisysTensor_t w_codes, llaisysTensor_t w_scale,
                                      llaisysTensor_t bias);
+    /* Random sampling after argmax (no reference kernel: README.md:397-399 asks for a random
+     * sample operator with temperature, top-k and top-p; python/llaisys/models/qwen2.py:216-218
+     * takes the three and ignores them).  logits [V] or [rows, V] (F32 / BF16 / F16), out_idx
+     * I64 / I32 with one index per row.  temperature <= 0 or top_k == 1: the row's argmax
+     * (first maximum).  Otherwise top_k in [2, 1024] (clamped to V): z = x * (1/T); the
+     * top_k largest z (ties by lower index); weights w = floor(2^31 * 2^((z - zmax) log2 e))
+     * from a fixed exp2 polynomial; top_p < 1 keeps the shortest (z desc, index asc) prefix
+     * whose weight sum reaches floor(top_p * W) (at least one token); the token is drawn by
+     * inverse CDF over that prefix with the uniform (splitmix64(seed + row) >> 40) / 2^24.
+     * Deterministic: equal inputs and seed give equal indices. */
+    __export void llaisysRandomSample(llaisysTensor_t out_idx, llaisysTensor_t logits,
+                                      float temperature, int64_t top_k, float top_p,
+                                      uint64_t seed);
 }
 
 #endif /* LLAISYS_OPS_H */

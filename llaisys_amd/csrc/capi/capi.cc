@@ -207,6 +207,11 @@ __C {
                                   bias ? bias->tensor : nullptr);
     }
 
+    void llaisysRandomSample(llaisysTensor_t out_idx, llaisysTensor_t logits, float temperature,
+                             int64_t top_k, float top_p, uint64_t seed) {
+        llaisys::ops::randomSample(out_idx->tensor, logits->tensor, temperature, top_k, top_p, seed);
+    }
+
     // ---- model API: out of scope, exported so the reference ctypes loader binds --------
     struct LlaisysQwen2Model *llaisysQwen2ModelCreate(const struct LlaisysQwen2Meta *,
                                                       llaisysDeviceType_t, int *, int) {

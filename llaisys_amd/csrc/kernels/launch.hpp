@@ -55,10 +55,15 @@ void embedding(void *out, const void *index, bool index_i64, size_t n_index, con
 void argmaxRows(void *idx, bool idx_i64, void *val, const void *vals, size_t rows, size_t cols,
                 llaisysDataType_t dt, hipStream_t stream);
 
-// Library scratch layout: the first kScratchReserved bytes hold the flat argmax's
-// completion counter, which must stay zero between launches; other users of the scratch
-// start after it.
-constexpr size_t kScratchReserved = 256;
+// Library scratch layout (zeroed once when allocated): bytes [0, 256) hold the flat argmax's
+// completion counter and [kSampleStateOffset, kScratchReserved) the sampler's per-row
+// histograms and counters; both stay zero between launches.  Other users of the scratch
+// start at kScratchReserved.
+constexpr size_t kSampleRows = 16;            // rows per sampler launch
+constexpr size_t kSampleRowStateBytes = 20496;
+constexpr size_t kSampleStateOffset = 256;
+constexpr size_t kScratchReserved =
+    (kSampleStateOffset + kSampleRows * kSampleRowStateBytes + 255) / 256 * 256;
 
 // Flat argmax over n elements; `workspace` (>= argmaxWorkspaceBytes(n)) holds the
 // completion counter (first kScratchReserved bytes, zero before the first call; the kernel
@@ -106,5 +111,14 @@ void linear(void *out, const void *x, const void *w, const float *w_scale, const
 // elements of esize (1, 2, 4 or 8) bytes.
 void rearrange(void *out, const void *in, size_t ndim, const size_t *shape, const ptrdiff_t *in_strides,
                const ptrdiff_t *out_strides, size_t esize, hipStream_t stream);
+
+// Random sampling of one index per row of logits [rows, V] (rule: temperature <= 0 or
+// top_k == 1 -> argmax; else top_k in [2, 1024] (clamped to V), top_p, splitmix64(seed +
+// row) uniform).  `ws` is the library scratch of at least kScratchReserved +
+// randomSampleWorkspaceBytes(rows, V, dt) bytes.
+size_t randomSampleWorkspaceBytes(size_t rows, size_t V, llaisysDataType_t dt);
+void randomSample(void *out_idx, bool i64, const void *logits, size_t rows, size_t V,
+                  llaisysDataType_t dt, float temperature, int64_t top_k, float top_p,
+                  uint64_t seed, void *ws, hipStream_t stream);
 
 } // namespace llaisys::kernels

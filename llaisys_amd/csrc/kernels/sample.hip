@@ -1,0 +1,466 @@
+// Random sampling after argmax: temperature, top-k and top-p over rows of logits.
+//
+// No reference kernel: README.md:397-399 asks for a random sample operator with
+// temperature, top-k and top-p, and python/llaisys/models/qwen2.py:216-218 takes the three
+// parameters.  The rule (z = x * (1/T); order by (z desc, index asc); keep the top k;
+// integer weights w = floor(2^31 * 2^((z - zmax) log2 e)) from a fixed exp2 polynomial;
+// top-p prefix by integer weight sum; inverse-CDF draw with a splitmix64 uniform) is made of
+// integer work and IEEE single multiplies / adds in a fixed order, so every GPU result is
+// bit-identical to the CPU statement of the rule whatever the thread order.
+//
+// Kernels per launch of up to kSampleRows rows (all on the context stream):
+//   sampleHist<1..3> : top-k radix select over the order-preserving u32 key of z -- each
+//                      level histograms one digit (11 / 11 / 10 bits) of the keys that
+//                      match the digits chosen so far; the choice of every earlier digit is
+//                      recomputed by each block from the previous histograms (integer
+//                      atomics: exact and order-free).  HBM / L2-bound, one read of the row.
+//   sampleGather     : the keys above the k-th largest (< k of them) and the ties at it.
+//   sampleFinish     : one 256-thread block per row: the k candidates (ties by index) sorted by
+//                      (key desc, index asc) in LDS, weights, prefix sums, the top-p cut,
+//                      the draw; then re-zeroes the row's histograms and counters.
+#include "common.hpp"
+#include "launch.hpp"
+
+#include <algorithm>
+
+namespace llaisys::kernels {
+
+namespace {
+
+constexpr int kSmpBlock = 256;
+constexpr int kSmpChunk = kSmpBlock * 8; // elements per histogram block
+constexpr int kMaxK = 1024;
+constexpr int kTieCap = 4096;
+
+__device__ __forceinline__ uint32_t keyOf(float z) {
+    const uint32_t b = __float_as_uint(z);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float unkey(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+// 2^t for t <= 0: degree-7 Taylor polynomial of e^(g ln 2) on g = frac(t) - 1/2, times
+// sqrt(2), scaled by 2^floor(t); each step one IEEE single multiply or add (_rn: never
+// contracted), so CPU and GPU agree bit for bit.
+__device__ __forceinline__ float sampleExp2(float t) {
+    if (!(t > -126.0f)) return 0.0f;
+    const float n = floorf(t);
+    const float g = __fsub_rn(__fsub_rn(t, n), 0.5f);
+    float y = 1.525273380405984e-05f;
+    y = __fadd_rn(__fmul_rn(y, g), 0.00015403530393381608f);
+    y = __fadd_rn(__fmul_rn(y, g), 0.0013333558146428443f);
+    y = __fadd_rn(__fmul_rn(y, g), 0.009618129107628477f);
+    y = __fadd_rn(__fmul_rn(y, g), 0.05550410866482158f);
+    y = __fadd_rn(__fmul_rn(y, g), 0.2402265069591007f);
+    y = __fadd_rn(__fmul_rn(y, g), 0.6931471805599453f);
+    y = __fadd_rn(__fmul_rn(y, g), 1.0f);
+    return ldexpf(__fmul_rn(y, 1.4142135623730951f), int(n));
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+// per-row state in the reserved (zero between launches) scratch
+struct SmpRow {
+    uint32_t h1[2048];
+    uint32_t h2[2048];
+    uint32_t h3[1024];
+    uint32_t nGt, nTie, theta, need; // counters; the threshold key and the ties it takes
+};
+static_assert(sizeof(SmpRow) == kSampleRowStateBytes, "sampler state layout");
+
+struct SmpArgs {
+    const void *x;
+    void *out;
+    bool i64;
+    int V, k, rows;
+    float inv, topP;
+    uint64_t seed;
+    SmpRow *st;      // rows entries, reserved scratch
+    uint32_t *gt;    // rows x kMaxK candidate indices (key above the threshold)
+    uint32_t *ties;  // rows x kTieCap indices with the threshold key
+};
+
+// Largest bin b of h[0..n) whose suffix count reaches `need`; returns b and, in *inside,
+// need minus the count above b.  All kSmpBlock threads of the block call it; the histogram
+// is first staged in `lh` (LDS, n words); `sc` is LDS scratch of kSmpBlock + 1 words.
+__device__ int chooseBin(const uint32_t *h, int n, uint32_t need, uint32_t *inside, uint32_t *lh,
+                         uint32_t *sc) {
+    const int t = int(threadIdx.x);
+    for (int b = t; b < n; b += kSmpBlock) lh[b] = h[b];
+    __syncthreads();
+    const int per = n / kSmpBlock; // thread t owns bins [t*per, (t+1)*per)
+    uint32_t s = 0;
+    for (int j = 0; j < per; ++j) s += lh[t * per + j];
+    sc[t] = s;
+    __syncthreads();
+    // suffix sums over the threads' totals
+    for (int d = 1; d < kSmpBlock; d *= 2) {
+        const uint32_t v = t + d < kSmpBlock ? sc[t + d] : 0u;
+        __syncthreads();
+        sc[t] += v;
+        __syncthreads();
+    }
+    // sc[t] = count in bins >= t*per; the thread whose range holds the crossing resolves it
+    __shared__ int bin;
+    __shared__ uint32_t in;
+    const uint32_t above = t + 1 < kSmpBlock ? sc[t + 1] : 0u;
+    if (above < need && sc[t] >= need) {
+        uint32_t acc = above;
+        for (int j = per - 1; j >= 0; --j) {
+            const uint32_t c = lh[t * per + j];
+            if (acc + c >= need) {
+                bin = t * per + j;
+                in = need - acc;
+                break;
+            }
+            acc += c;
+        }
+    }
+    __syncthreads();
+    *inside = in;
+    return bin;
+}
+
+// the digits chosen after `level` histograms: prefix (the key's top bits) and the count
+// still needed among keys with that prefix
+__device__ void decide(const SmpRow &st, int level, uint32_t k, uint32_t *prefix, uint32_t *need,
+                       uint32_t *lh, uint32_t *sc) {
+    uint32_t nd = k, p = 0;
+    if (level >= 1) p = uint32_t(chooseBin(st.h1, 2048, nd, &nd, lh, sc));
+    if (level >= 2) p = (p << 11) | uint32_t(chooseBin(st.h2, 2048, nd, &nd, lh, sc));
+    if (level >= 3) p = (p << 10) | uint32_t(chooseBin(st.h3, 1024, nd, &nd, lh, sc));
+    *prefix = p;
+    *need = nd;
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t keyAt(const SmpArgs &a, int row, int i) {
+    return keyOf(__fmul_rn(Fmt<T>::get(a.x, size_t(row) * a.V + i), a.inv));
+}
+
+// LEVEL 1..3: histogram of digit LEVEL of the keys matching the chosen prefix
+template <typename T, int LEVEL>
+__global__ void __launch_bounds__(kSmpBlock)
+    sampleHist(SmpArgs a) {
+    __shared__ uint32_t hist[2048];
+    __shared__ uint32_t sc[kSmpBlock + 1];
+    const int row = int(blockIdx.y);
+    SmpRow &st = a.st[row];
+    uint32_t prefix = 0, need = 0;
+    if constexpr (LEVEL > 1) decide(st, LEVEL - 1, uint32_t(a.k), &prefix, &need, hist, sc);
+    constexpr int kBins = LEVEL == 3 ? 1024 : 2048;
+    __syncthreads(); // hist held the staged histograms
+    for (int b = int(threadIdx.x); b < kBins; b += kSmpBlock) hist[b] = 0;
+    __syncthreads();
+    const int base = int(blockIdx.x) * kSmpChunk;
+    constexpr int kPer = kSmpChunk / kSmpBlock;
+    uint32_t keys[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = base + j * kSmpBlock + int(threadIdx.x);
+        keys[j] = keyAt<T>(a, row, i < a.V ? i : a.V - 1);
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = base + j * kSmpBlock + int(threadIdx.x);
+        if (i >= a.V) break;
+        const uint32_t key = keys[j];
+        if constexpr (LEVEL == 1) {
+            atomicAdd(&hist[key >> 21], 1u);
+        } else if constexpr (LEVEL == 2) {
+            if ((key >> 21) == prefix) atomicAdd(&hist[(key >> 10) & 0x7FFu], 1u);
+        } else {
+            if ((key >> 10) == prefix) atomicAdd(&hist[key & 0x3FFu], 1u);
+        }
+    }
+    __syncthreads();
+    uint32_t *g = LEVEL == 1 ? st.h1 : (LEVEL == 2 ? st.h2 : st.h3);
+    for (int b = int(threadIdx.x); b < kBins; b += kSmpBlock)
+        if (hist[b]) atomicAdd(g + b, hist[b]);
+}
+
+// the candidates: keys above the k-th largest key, and the ties at it
+template <typename T>
+__global__ void __launch_bounds__(kSmpBlock)
+    sampleGather(SmpArgs a) {
+    __shared__ uint32_t sc[kSmpBlock + 1];
+    __shared__ uint32_t lh[2048];
+    const int row = int(blockIdx.y);
+    SmpRow &st = a.st[row];
+    uint32_t theta = 0, need = 0;
+    decide(st, 3, uint32_t(a.k), &theta, &need, lh, sc);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        st.theta = theta;
+        st.need = need;
+    }
+    // positions are reserved per block (LDS counters, then one global atomic per list), so a
+    // thousand candidates do not queue on one global counter
+    __shared__ uint32_t nG, nT, baseG, baseT;
+    if (threadIdx.x == 0) nG = nT = 0;
+    __syncthreads();
+    const int base = int(blockIdx.x) * kSmpChunk;
+    constexpr int kPer = kSmpChunk / kSmpBlock;
+    uint32_t slot[kPer]; // bit 31: tie; else candidate; position within the block's list
+    int cls[kPer];       // 0 none, 1 above theta, 2 tie
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = base + j * kSmpBlock + int(threadIdx.x);
+        cls[j] = 0;
+        if (i < a.V) {
+            const uint32_t key = keyAt<T>(a, row, i);
+            if (key > theta) {
+                cls[j] = 1;
+                slot[j] = atomicAdd(&nG, 1u);
+            } else if (key == theta) {
+                cls[j] = 2;
+                slot[j] = atomicAdd(&nT, 1u);
+            }
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        baseG = nG ? atomicAdd(&st.nGt, nG) : 0u;
+        baseT = nT ? atomicAdd(&st.nTie, nT) : 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const uint32_t i = uint32_t(base + j * kSmpBlock + int(threadIdx.x));
+        if (cls[j] == 1) {
+            const uint32_t pos = baseG + slot[j];
+            if (pos < uint32_t(kMaxK)) a.gt[size_t(row) * kMaxK + pos] = i;
+        } else if (cls[j] == 2) {
+            const uint32_t pos = baseT + slot[j];
+            if (pos < uint32_t(kTieCap)) a.ties[size_t(row) * kTieCap + pos] = i;
+        }
+    }
+}
+
+// ascending bitonic sort of n (power of two) 64-bit items in LDS by all threads
+__device__ void bitonic(uint64_t *v, int n) {
+    for (int size = 2; size <= n; size *= 2)
+        for (int stride = size / 2; stride > 0; stride /= 2) {
+            for (int i = int(threadIdx.x); i < n / 2; i += int(blockDim.x)) {
+                const int lo = 2 * i - (i & (stride - 1)), hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const uint64_t x = v[lo], y = v[hi];
+                if ((x > y) == up) {
+                    v[lo] = y;
+                    v[hi] = x;
+                }
+            }
+            __syncthreads();
+        }
+}
+
+constexpr int kFinThreads = 256;
+
+// exclusive prefix sums of v (one value per thread, kFinThreads threads) in `buf`; returns
+// this thread's exclusive sum and, in *total, the block total
+__device__ uint64_t blockExclusive(uint64_t v, uint64_t *buf, uint64_t *total) {
+    const int t = int(threadIdx.x);
+    buf[t] = v;
+    __syncthreads();
+    for (int d = 1; d < kFinThreads; d *= 2) {
+        const uint64_t add = t >= d ? buf[t - d] : 0ull;
+        __syncthreads();
+        buf[t] += add;
+        __syncthreads();
+    }
+    const uint64_t inc = buf[t];
+    *total = buf[kFinThreads - 1];
+    __syncthreads();
+    return inc - v;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kFinThreads)
+    sampleFinish(SmpArgs a) {
+    __shared__ uint64_t item[kTieCap];
+    __shared__ uint64_t cum[kMaxK];
+    __shared__ uint64_t sbuf[kFinThreads];
+    __shared__ uint32_t tieIdx[kMaxK];
+    __shared__ int kept, pick;
+    const int row = int(blockIdx.x);
+    const int t = int(threadIdx.x);
+    SmpRow &st = a.st[row];
+    const uint32_t theta = st.theta, need = st.need, nTie = st.nTie;
+    const uint32_t nGt = min(st.nGt, uint32_t(kMaxK));
+    const int k = a.k; // == nGt + need
+    // 1. the `need` smallest indices whose key equals theta
+    if (nTie <= uint32_t(kTieCap)) {
+        int n2 = 2;
+        while (n2 < int(nTie)) n2 *= 2;
+        for (int i = t; i < n2; i += kFinThreads)
+            item[i] = i < int(nTie) ? uint64_t(a.ties[size_t(row) * kTieCap + i]) : ~0ull;
+        __syncthreads();
+        bitonic(item, n2);
+        for (int i = t; i < int(need); i += kFinThreads) tieIdx[i] = uint32_t(item[i]);
+    } else {
+        // more ties than the list holds: rank them in index order (contiguous segments)
+        const int seg = (a.V + kFinThreads - 1) / kFinThreads, lo = t * seg, hi = min(a.V, lo + seg);
+        uint32_t c = 0;
+        for (int i = lo; i < hi; ++i) c += keyAt<T>(a, row, i) == theta;
+        uint64_t tot;
+        uint32_t r = uint32_t(blockExclusive(c, sbuf, &tot));
+        for (int i = lo; i < hi && r < need; ++i)
+            if (keyAt<T>(a, row, i) == theta) tieIdx[r++] = uint32_t(i);
+    }
+    __syncthreads();
+    // 2. the k candidates sorted by (key desc, index asc): ascending on (~key, index)
+    int nk = 2;
+    while (nk < k) nk *= 2;
+    for (int j = t; j < nk; j += kFinThreads) {
+        uint64_t v = ~0ull;
+        if (j < k) {
+            const uint32_t i = j < int(nGt) ? a.gt[size_t(row) * kMaxK + j] : tieIdx[j - int(nGt)];
+            v = (uint64_t(~keyAt<T>(a, row, int(i))) << 32) | i;
+        }
+        item[j] = v;
+    }
+    __syncthreads();
+    bitonic(item, nk);
+    // 3. integer weights and their running sums (thread t owns elements [4t, 4t + 4))
+    const float zmax = unkey(~uint32_t(item[0] >> 32));
+    uint64_t w4[4], run = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int j = 4 * t + e;
+        w4[e] = 0;
+        if (j < k) {
+            const float z = unkey(~uint32_t(item[j] >> 32));
+            const float p = sampleExp2(__fmul_rn(__fsub_rn(z, zmax), 1.4426950408889634f));
+            w4[e] = uint32_t(__fmul_rn(p, 2147483648.0f));
+        }
+        run += w4[e];
+    }
+    uint64_t tot;
+    uint64_t pre = blockExclusive(run, sbuf, &tot);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        pre += w4[e];
+        cum[4 * t + e] = pre;
+    }
+    __syncthreads();
+    // 4. the top-p cut and the draw
+    const uint64_t W = cum[k - 1];
+    uint64_t target = 0; // 0: no top-p cut
+    if (a.topP < 1.0f) {
+        target = 1;
+        if (a.topP > 0.0f) {
+            target = uint64_t(double(a.topP) * double(W));
+            if (target == 0) target = 1;
+        }
+    }
+    if (t == 0) kept = k;
+    __syncthreads();
+    if (target)
+        for (int j = t; j < k; j += kFinThreads)
+            if (cum[j] >= target && (j == 0 || cum[j - 1] < target)) kept = j + 1;
+    __syncthreads();
+    const uint64_t wk = cum[kept - 1];
+    const uint64_t u24 = splitmix64(a.seed + uint64_t(row)) >> 40;
+    const uint64_t rr = (__umul64hi(u24, wk) << 40) | ((u24 * wk) >> 24);
+    for (int j = t; j < kept; j += kFinThreads)
+        if (cum[j] > rr && (j == 0 || cum[j - 1] <= rr)) pick = j;
+    __syncthreads();
+    if (t == 0) {
+        const int64_t idx = int64_t(uint32_t(item[pick]));
+        if (a.i64)
+            static_cast<int64_t *>(a.out)[row] = idx;
+        else
+            static_cast<int32_t *>(a.out)[row] = int32_t(idx);
+    }
+    // 5. leave the row's state zero for the next launch
+    for (int b = t; b < 2048; b += kFinThreads) {
+        st.h1[b] = 0;
+        st.h2[b] = 0;
+        if (b < 1024) st.h3[b] = 0;
+    }
+    if (t == 0) st.nGt = st.nTie = st.theta = st.need = 0;
+}
+
+} // namespace
+
+} // namespace llaisys::kernels
+
+namespace llaisys::kernels {
+
+// greedy: the flat argmax's partials (after kScratchReserved), then one value per row
+size_t greedyValueOffset(size_t V, llaisysDataType_t dt) {
+    return (argmaxWorkspaceBytes(V, dt) + 15) / 16 * 16;
+}
+
+size_t randomSampleWorkspaceBytes(size_t rows, size_t V, llaisysDataType_t dt) {
+    // sampling: candidate and tie lists of up to kSampleRows rows
+    const size_t lists = kSampleRows * (size_t(kMaxK) + size_t(kTieCap)) * sizeof(uint32_t);
+    const size_t greedy = greedyValueOffset(V, dt) - kScratchReserved + rows * sizeof(float);
+    return std::max(lists, greedy);
+}
+
+void randomSample(void *out_idx, bool i64, const void *logits, size_t rows, size_t V,
+                  llaisysDataType_t dt, float temperature, int64_t top_k, float top_p,
+                  uint64_t seed, void *ws, hipStream_t s) {
+    if (rows == 0 || V == 0) return;
+    char *base = static_cast<char *>(ws);
+    if (!(temperature > 0.0f) || top_k == 1) { // greedy: the row's argmax
+        char *val = base + greedyValueOffset(V, dt); // the argmax kernels want a value output too
+        if (rows == 1) // one row: the multi-block flat argmax (its workspace: base, counter at 0)
+            argmax(out_idx, i64, val, logits, V, dt, base, s);
+        else
+            argmaxRows(out_idx, i64, val, logits, rows, V, dt, s);
+        return;
+    }
+    const float inv = 1.0f / temperature;
+    const int k = int(std::min<int64_t>(top_k, int64_t(V)));
+    const size_t esz = dt == LLAISYS_DTYPE_F32 ? 4 : 2;
+    for (size_t r0 = 0; r0 < rows; r0 += kSampleRows) {
+        const size_t nr = std::min(kSampleRows, rows - r0);
+        SmpArgs a;
+        a.x = static_cast<const char *>(logits) + r0 * V * esz;
+        a.out = static_cast<char *>(out_idx) + r0 * (i64 ? 8 : 4);
+        a.i64 = i64;
+        a.V = int(V);
+        a.k = k;
+        a.rows = int(nr);
+        a.inv = inv;
+        a.topP = top_p;
+        a.seed = seed + r0;
+        a.st = reinterpret_cast<SmpRow *>(base + kSampleStateOffset);
+        a.gt = reinterpret_cast<uint32_t *>(base + kScratchReserved);
+        a.ties = a.gt + kSampleRows * kMaxK;
+        const dim3 grid(unsigned((V + kSmpChunk - 1) / kSmpChunk), unsigned(nr));
+        switch (dt) {
+        case LLAISYS_DTYPE_F32:
+            sampleHist<F32, 1><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleHist<F32, 2><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleHist<F32, 3><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleGather<F32><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleFinish<F32><<<unsigned(nr), kFinThreads, 0, s>>>(a);
+            break;
+        case LLAISYS_DTYPE_BF16:
+            sampleHist<BF16, 1><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleHist<BF16, 2><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleHist<BF16, 3><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleGather<BF16><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleFinish<BF16><<<unsigned(nr), kFinThreads, 0, s>>>(a);
+            break;
+        case LLAISYS_DTYPE_F16:
+            sampleHist<F16, 1><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleHist<F16, 2><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleHist<F16, 3><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleGather<F16><<<grid, kSmpBlock, 0, s>>>(a);
+            sampleFinish<F16><<<unsigned(nr), kFinThreads, 0, s>>>(a);
+            break;
+        default: return;
+        }
+    }
+}
+
+} // namespace llaisys::kernels

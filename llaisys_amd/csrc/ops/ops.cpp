@@ -398,6 +398,33 @@ void rearrange(tensor_t out, tensor_t in) {
     in->copyInto(out);
 }
 
+// Random sampling after argmax (no reference kernel; README.md:397-399 asks for it,
+// python/llaisys/models/qwen2.py:216-218 takes its parameters): one index per row of
+// logits [V] or [rows, V].
+void randomSample(tensor_t out_idx, tensor_t logits, float temperature, int64_t top_k,
+                  float top_p, uint64_t seed) {
+    CHECK_SAME_DEVICE(out_idx, logits);
+    ASSERT(out_idx->isContiguous() && logits->isContiguous(), "RandomSample: tensors must be contiguous");
+    ASSERT(out_idx->dtype() == LLAISYS_DTYPE_I32 || out_idx->dtype() == LLAISYS_DTYPE_I64,
+           "RandomSample: out_idx must be INT32 or INT64");
+    requireFloat(logits->dtype());
+    ASSERT(logits->ndim() == 1 || logits->ndim() == 2, "RandomSample: logits must be [V] or [rows, V]");
+    const size_t rows = logits->ndim() == 2 ? logits->shape()[0] : 1;
+    const size_t V = logits->shape().back();
+    ASSERT(out_idx->numel() == rows, "RandomSample: out_idx must hold one index per row");
+    ASSERT(V > 0 && V < (size_t(1) << 31), "RandomSample: vocabulary size must be in [1, 2^31)");
+    const bool greedy = !(temperature > 0.0f) || top_k == 1;
+    ASSERT(greedy || (top_k >= 2 && top_k <= 1024),
+           "RandomSample: top_k must be 1 or in [2, 1024] when sampling");
+    auto s = streamFor(logits);
+    void *ws = device::amd::workspace(logits->deviceId(),
+                                      kernels::kScratchReserved +
+                                          kernels::randomSampleWorkspaceBytes(rows, V, logits->dtype()));
+    kernels::randomSample(out_idx->data(), out_idx->dtype() == LLAISYS_DTYPE_I64, logits->data(), rows,
+                          V, logits->dtype(), temperature, top_k, top_p, seed, ws, s);
+    launched("randomSample");
+}
+
 namespace {
 // Shape checks of reference src/ops/linear/op.cpp:10-42 (messages kept); a bias that is
 // null or has no elements means no bias.  Returns the row count.

@@ -4,7 +4,7 @@ The nine reference methods match python/llaisys/ops.py:6-55 (rearrange raises in
 library, as the reference's own C++ rearrange does); the rest wrap the additive entry points of
 include/llaisys/ops.h.
 """
-from ctypes import c_float, c_size_t
+from ctypes import c_float, c_int64, c_size_t, c_uint64
 
 from .libllaisys import LIB_LLAISYS
 from .tensor import Tensor
@@ -120,3 +120,9 @@ class Ops:
         LIB_LLAISYS.llaisysLinearW8A16(out.lib_tensor(), inp.lib_tensor(), w_codes.lib_tensor(),
                                        w_scale.lib_tensor(),
                                        None if bias is None else bias.lib_tensor())
+
+    @staticmethod
+    def random_sample(out_idx: Tensor, logits: Tensor, temperature: float, top_k: int, top_p: float,
+                      seed: int):
+        LIB_LLAISYS.llaisysRandomSample(out_idx.lib_tensor(), logits.lib_tensor(), c_float(temperature),
+                                        c_int64(top_k), c_float(top_p), c_uint64(seed & (2 ** 64 - 1)))

@@ -47,11 +47,18 @@ def lib():
                                    c_size_t, c_float, c_int],
             "orc_linear": [P, P, P, P, c_size_t, c_size_t, c_size_t, c_int],
             "orc_linear_w8a16": [P, P, P, P, P, c_size_t, c_size_t, c_size_t, c_int],
+            "orc_random_sample": [P, P, c_size_t, c_size_t, c_int, c_float, ctypes.c_int64, c_float,
+                                  ctypes.c_uint64],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = c_int if name in ("orc_embedding", "orc_kv_append_int8", "orc_self_attention") else None
+            fn.restype = c_int if name in ("orc_embedding", "orc_kv_append_int8", "orc_self_attention",
+                                           "orc_random_sample") else None
+        L.orc_sample_exp2.argtypes = [c_float]
+        L.orc_sample_exp2.restype = c_float
+        L.orc_splitmix64.argtypes = [ctypes.c_uint64]
+        L.orc_splitmix64.restype = ctypes.c_uint64
         for name in ("orc_f32_to_bf16", "orc_f32_to_f16"):
             getattr(L, name).argtypes = [c_float]
             getattr(L, name).restype = ctypes.c_uint16
@@ -218,3 +225,23 @@ def linear_w8a16(x, codes, scale, bias=None):
     lib().orc_linear_w8a16(_p(out), _p(x), _p(codes), _p(scale), None if b is None else _p(b), rows,
                            in_f, out_f, _code(x))
     return out
+
+
+def random_sample(logits, temperature, top_k, top_p, seed):
+    """Sampling rule of oracle.h orc_random_sample: logits [V] or [rows, V] -> int64 [rows]."""
+    x = _c(logits)
+    rows, V = (1, x.shape[0]) if x.ndim == 1 else x.shape
+    out = np.empty(rows, dtype=np.int64)
+    rc = lib().orc_random_sample(_p(out), _p(x), rows, V, _code(x), float(temperature), int(top_k),
+                                 float(top_p), int(seed) & (2 ** 64 - 1))
+    if rc != 0:
+        raise ValueError("top_k must be 1 or in [2, 1024] when sampling")
+    return out
+
+
+def sample_exp2(t):
+    return float(lib().orc_sample_exp2(float(t)))
+
+
+def splitmix64(x):
+    return int(lib().orc_splitmix64(int(x) & (2 ** 64 - 1)))

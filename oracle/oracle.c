@@ -373,3 +373,113 @@ void orc_linear_w8a16(void *out, const void *x, const int8_t *code, const float 
             st(out, m * out_f + n, dt, sum);
         }
 }
+
+/* ---- random sampling (no reference kernel; rule in oracle.h) ------------------------- */
+
+uint64_t orc_splitmix64(uint64_t x) {
+    /* splitmix64 finaliser (Steele, Lea and Flood, "Fast splittable pseudorandom number
+     * generators", OOPSLA 2014) applied to x + golden gamma */
+    uint64_t z = x + 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+float orc_sample_exp2(float t) {
+    if (!(t > -126.0f)) return 0.0f;
+    const float n = floorf(t);
+    const float g = (t - n) - 0.5f;
+    /* (ln 2)^k / k!, k = 7 .. 1 */
+    float y = 1.525273380405984e-05f;
+    y = y * g + 0.00015403530393381608f;
+    y = y * g + 0.0013333558146428443f;
+    y = y * g + 0.009618129107628477f;
+    y = y * g + 0.05550410866482158f;
+    y = y * g + 0.2402265069591007f;
+    y = y * g + 0.6931471805599453f;
+    y = y * g + 1.0f;
+    return ldexpf(y * 1.4142135623730951f, (int)n);
+}
+
+static uint32_t smp_key(float z) {
+    uint32_t b;
+    memcpy(&b, &z, 4);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+static float smp_unkey(uint32_t k) {
+    const uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+    float z;
+    memcpy(&z, &b, 4);
+    return z;
+}
+
+typedef struct {
+    uint32_t key;
+    uint32_t idx;
+} smp_item;
+
+static int smp_cmp(const void *a, const void *b) {
+    const smp_item *x = a, *y = b;
+    if (x->key != y->key) return x->key > y->key ? -1 : 1;
+    return x->idx < y->idx ? -1 : (x->idx > y->idx);
+}
+
+int orc_random_sample(int64_t *out_idx, const void *logits, size_t rows, size_t V, int dt,
+                      float temperature, int64_t top_k, float top_p, uint64_t seed) {
+    if (!(temperature > 0.0f) || top_k == 1) {
+        for (size_t r = 0; r < rows; r++) {
+            float m = ld(logits, r * V, dt);
+            size_t mi = 0;
+            for (size_t i = 1; i < V; i++) {
+                const float v = ld(logits, r * V + i, dt);
+                if (v > m) { m = v; mi = i; }
+            }
+            out_idx[r] = (int64_t)mi;
+        }
+        return 0;
+    }
+    if (top_k < 2 || top_k > 1024) return -1;
+    const float inv = 1.0f / temperature;
+    const size_t k = (size_t)top_k < V ? (size_t)top_k : V;
+    smp_item *it = malloc(V * sizeof(smp_item));
+    uint64_t *cum = malloc(k * sizeof(uint64_t));
+    uint32_t *w = malloc(k * sizeof(uint32_t));
+    for (size_t r = 0; r < rows; r++) {
+        for (size_t i = 0; i < V; i++) {
+            it[i].key = smp_key(ld(logits, r * V + i, dt) * inv);
+            it[i].idx = (uint32_t)i;
+        }
+        qsort(it, V, sizeof(smp_item), smp_cmp);
+        const float zmax = smp_unkey(it[0].key);
+        uint64_t W = 0;
+        for (size_t j = 0; j < k; j++) {
+            const float p = orc_sample_exp2((smp_unkey(it[j].key) - zmax) * 1.4426950408889634f);
+            w[j] = (uint32_t)(p * 2147483648.0f);
+            W += w[j];
+            cum[j] = W;
+        }
+        size_t kept = k;
+        if (top_p < 1.0f) {
+            uint64_t target = 1;
+            if (top_p > 0.0f) {
+                target = (uint64_t)((double)top_p * (double)W);
+                if (target == 0) target = 1;
+            }
+            kept = 0;
+            while (cum[kept] < target) kept++;
+            kept++;
+        }
+        const uint64_t Wk = cum[kept - 1];
+        const uint64_t u24 = orc_splitmix64(seed + r) >> 40;
+        const unsigned __int128 prod = (unsigned __int128)u24 * Wk;
+        const uint64_t rr = (uint64_t)(prod >> 24);
+        size_t j = 0;
+        while (cum[j] <= rr) j++;
+        out_idx[r] = (int64_t)it[j].idx;
+    }
+    free(it);
+    free(cum);
+    free(w);
+    return 0;
+}

@@ -62,4 +62,23 @@ void orc_linear_w8a16(void *out, const void *x, const int8_t *code, const float 
                       const void *bias, size_t rows, size_t in_features, size_t out_features,
                       int dtype);
 
+/* Random sampling after argmax (no reference kernel: README.md:397-399 asks for
+ * temperature, top-k and top-p; python/llaisys/models/qwen2.py:216-218 takes them and
+ * ignores them).  The rule, per row of `logits` [rows, V]:
+ *   temperature <= 0 or top_k == 1: the row's argmax (first maximum);
+ *   else z = x * (1 / temperature) (1/T rounded to f32 once), order the V elements by
+ *   (key(z) desc, index asc) with key the order-preserving u32 of the f32 bits, keep the
+ *   first min(top_k, V) (top_k must be in [2, 1024]), weights w = floor(p * 2^31) with
+ *   p = orc_sample_exp2((z - zmax) * log2(e)), W = sum of w; top_p < 1 keeps the shortest
+ *   prefix whose w-sum >= max(1, floor(top_p * W)) (top_p <= 0: the first element);
+ *   then with u24 = splitmix64(seed + row) >> 40 and r = floor(u24 * W_kept / 2^24), the
+ *   sample is the first element of the kept prefix whose running w-sum exceeds r.
+ * Returns 0, or -1 for a top_k outside the supported range. */
+int orc_random_sample(int64_t *out_idx, const void *logits, size_t rows, size_t V, int dtype,
+                      float temperature, int64_t top_k, float top_p, uint64_t seed);
+/* 2^t for t <= 0 as the sampler computes it: degree-7 Taylor polynomial of e^(g ln 2) on
+ * g = frac(t) - 1/2, times sqrt(2), scaled by 2^floor(t); 0 below 2^-126. */
+float orc_sample_exp2(float t);
+uint64_t orc_splitmix64(uint64_t x);
+
 #endif

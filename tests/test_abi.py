@@ -163,6 +163,8 @@ def _run(code):
     ("L.Ops.argmax(t((1,), L.DataType.F32), t((1,)), t((8,)))", "max_idx must be INT32 or INT64"),
     ("L.Ops.rearrange(t((2,2)), t((2,2)))", "Unsupported device"),
     ("L.Ops.rearrange(t((2,3)), t((3,2)))", "Shapes mismatch"),
+    ("L.Ops.random_sample(t((1,), L.DataType.I64), t((10,)), 0.8, 2000, 0.9, 1)", "top_k must be 1 or in [2, 1024]"),
+    ("L.Ops.random_sample(t((2,), L.DataType.I64), t((3, 10)), 0.8, 20, 0.9, 1)", "one index per row"),
     ("L.Ops.linear(t((2,2)), t((2,2)), t((2,2)), t((3,)))", "Linear: bias shape mismatch"),
     ("L.Ops.linear(t((2,3)), t((2,2)), t((2,2)), t((2,)))", "Linear: output feature dim mismatch"),
     ("L.Ops.linear(t((2,2)), t((2,2)), t((2,2)))", "Unsupported device"),

@@ -446,3 +446,96 @@ def test_linear_w8a16_closed_forms():
     got = oracle.linear_w8a16(xf, codes, sc, bias=None)
     exp = (xf.astype(np.float64) @ codes.T.astype(np.float64)) * sc.astype(np.float64)
     assert np.abs(got - exp).max() <= 1e-5 * np.abs(exp).max()
+
+
+# ---- random sampling (no reference kernel; rule in oracle/oracle.h) ------------------------
+
+def test_sample_exp2_against_math():
+    ts = np.concatenate([-np.linspace(0, 120, 2000), -np.random.default_rng(3).random(500) * 30])
+    for t in ts.astype(np.float32):
+        got, exp = oracle.sample_exp2(t), 2.0 ** float(t)
+        assert abs(got - exp) <= 2e-7 * exp, (t, got, exp)
+    assert oracle.sample_exp2(-126.5) == 0.0 and oracle.sample_exp2(float("nan")) == 0.0
+
+
+def test_splitmix64_known_answers():
+    # the first three outputs of splitmix64 seeded with 0 (Steele, Lea and Flood 2014)
+    gamma = 0x9E3779B97F4A7C15
+    assert oracle.splitmix64(0) == 0xE220A8397B1DCDAF
+    assert oracle.splitmix64(gamma) == 0x6E789E6AA1B965F4
+    assert oracle.splitmix64(2 * gamma) == 0x06C45D188009454F
+
+
+def _sample_rule(x, temperature, top_k, top_p, seed):
+    """The sampling rule restated with Python integers (independent of oracle.c's loops)."""
+    x = np.asarray(x, np.float32)
+    if temperature <= 0 or top_k == 1:
+        return int(np.argmax(x))
+    inv = np.float32(1.0) / np.float32(temperature)
+    z = (x * inv).astype(np.float32)
+    bits = z.view(np.uint32).astype(np.int64)
+    key = np.where(bits & 0x80000000, (~bits) & 0xFFFFFFFF, bits | 0x80000000)
+    order = sorted(range(len(z)), key=lambda i: (-int(key[i]), i))[:min(top_k, len(z))]
+    zmax = z[order[0]]
+    w = [int(np.float32(oracle.sample_exp2(np.float32(z[i] - zmax) * np.float32(1.4426950408889634)))
+             * np.float32(2 ** 31)) for i in order]
+    cum = np.cumsum(w, dtype=object)
+    W = int(cum[-1])
+    kept = len(order)
+    if top_p < 1:
+        target = max(1, int(float(np.float32(top_p)) * W)) if top_p > 0 else 1
+        kept = next(j for j in range(len(order)) if cum[j] >= target) + 1
+    wk = int(cum[kept - 1])
+    r = ((oracle.splitmix64(seed) >> 40) * wk) >> 24
+    return order[next(j for j in range(kept) if cum[j] > r)]
+
+
+def test_random_sample_matches_the_rule_restated():
+    rng = np.random.default_rng(21)
+    for case in range(60):
+        V = int(rng.integers(2, 400))
+        x = (rng.standard_normal(V) * rng.choice([0.5, 3.0, 10.0])).astype(np.float32)
+        if case % 3 == 0:  # ties
+            x = np.round(x).astype(np.float32)
+        T = float(rng.choice([0.0, 0.3, 0.8, 1.0, 2.5]))
+        k = int(rng.choice([1, 2, 7, 50, 1024]))
+        p = float(rng.choice([0.0, 0.2, 0.8, 0.95, 1.0]))
+        seed = int(rng.integers(0, 2 ** 62))
+        got = oracle.random_sample(x, T, k, p, seed)[0]
+        assert got == _sample_rule(x, T, k, p, seed), (case, V, T, k, p)
+
+
+def test_random_sample_greedy_cases_are_argmax():
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((5, 300)).astype(np.float32)
+    x[2, 17] = x[2, 250] = x[2].max() + 1  # tie: the lower index wins
+    am = np.argmax(x, axis=1)
+    assert np.array_equal(oracle.random_sample(x, 0.0, 50, 0.9, 1), am)
+    assert np.array_equal(oracle.random_sample(x, 0.8, 1, 0.9, 1), am)
+    assert np.array_equal(oracle.random_sample(x, 0.8, 50, 0.0, 1), am)  # top_p <= 0: the top element
+    with pytest.raises(ValueError):
+        oracle.random_sample(x, 0.8, 2000, 0.9, 1)
+
+
+def _chi2_ok(counts, probs, n):
+    exp = np.asarray(probs) * n
+    m = exp > 0
+    assert counts[~m].sum() == 0, "sampled an excluded token"
+    chi2 = float((((counts[m] - exp[m]) ** 2) / exp[m]).sum())
+    dof = int(m.sum()) - 1
+    return chi2 < dof + 6 * np.sqrt(2 * max(dof, 1)) + 10
+
+
+def test_random_sample_distribution():
+    x = np.array([2.0, 1.0, 0.5, 0.0, -1.0, 3.0, 0.2, -0.3], np.float32)
+    n = 20000
+    for T, k, p in ((1.0, 8, 1.0), (0.7, 3, 1.0), (1.0, 8, 0.6), (2.0, 5, 0.9)):
+        z = x.astype(np.float64) / T
+        order = np.argsort(-z, kind="stable")[:k]
+        pr = np.exp(z[order] - z[order].max())
+        pr /= pr.sum()
+        keep = len(order) if p >= 1 else int(np.searchsorted(np.cumsum(pr), p - 1e-12) + 1)
+        probs = np.zeros(len(x))
+        probs[order[:keep]] = pr[:keep] / pr[:keep].sum()
+        counts = np.bincount([oracle.random_sample(x, T, k, p, s)[0] for s in range(n)], minlength=len(x))
+        assert _chi2_ok(counts, probs, n), (T, k, p, counts, probs * n)

@@ -1,0 +1,96 @@
+"""Random sampling on the GPU (llaisysRandomSample) against the oracle's statement of the rule
+(oracle/oracle.h orc_random_sample), which tests/test_oracle.py pins by closed forms (greedy
+cases are argmax), an independent integer restatement and its sampled distribution.  The
+rule is integer work plus IEEE single multiplies / adds in a fixed order, so the indices
+must be equal bit for bit."""
+import numpy as np
+import pytest
+
+import llaisys_amd as L
+import oracle
+from llaisys_amd.hostfmt import f32_to_bf16
+
+pytestmark = pytest.mark.gpu
+
+AMD = dict(device=L.DeviceType.AMD, device_id=0)
+DTS = {"f32": L.DataType.F32, "bf16": L.DataType.BF16, "f16": L.DataType.F16}
+
+
+def conv(x, dt):
+    return {"f32": x.astype(np.float32), "bf16": f32_to_bf16(x.astype(np.float32)), "f16": x.astype(np.float16)}[dt]
+
+
+def gpu_sample(x, dt, T, k, p, seed, i64=True):
+    rows = 1 if x.ndim == 1 else x.shape[0]
+    out = L.Tensor((rows,), L.DataType.I64 if i64 else L.DataType.I32, **AMD)
+    L.Ops.random_sample(out, L.Tensor.from_numpy(x, DTS[dt], **AMD), T, k, p, seed)
+    return out.numpy().astype(np.int64)
+
+
+CASES = [
+    # rows, V, scale, temperature, top_k, top_p
+    (1, 151936, 3.0, 0.8, 50, 0.8),     # Qwen2 vocabulary, the reference generate() defaults + top_k
+    (1, 151936, 3.0, 1.0, 1024, 0.95),
+    (1, 151936, 3.0, 0.7, 40, 1.0),     # top-k only
+    (4, 32000, 1.0, 1.3, 200, 0.9),
+    (20, 5000, 2.0, 0.9, 64, 0.7),      # more than 16 rows: two launches
+    (3, 100, 1.0, 1.0, 500, 0.9),       # k > V
+    (2, 4097, 5.0, 0.5, 2, 0.0),        # top_p <= 0: the top token
+    (1, 151936, 3.0, 0.0, 50, 0.8),     # temperature 0: argmax
+    (5, 3000, 1.0, 0.8, 1, 0.8),        # top_k 1: argmax
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32", "f16"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
+def test_random_sample_matches_oracle(case, dt):
+    rows, V, scale, T, k, p = case
+    rng = np.random.default_rng(hash((case, dt)) % 2 ** 32)
+    x = conv(rng.standard_normal((rows, V)) * scale, dt)
+    for seed in (0, 12345, 2 ** 63 + 7):
+        exp = oracle.random_sample(x, T, k, p, seed)
+        got = gpu_sample(x, dt, T, k, p, seed)
+        assert np.array_equal(got, exp), (case, dt, seed, got, exp)
+
+
+def test_random_sample_ties_and_tie_overflow():
+    rng = np.random.default_rng(4)
+    # many exact ties around the k-th key (rounded logits) and more ties than the list holds
+    x1 = np.round(rng.standard_normal((3, 20000)) * 2).astype(np.float32)
+    x2 = np.zeros((2, 10000), np.float32)
+    x2[1, 9999] = 1.0
+    for x in (x1, x2):
+        for seed in (1, 99):
+            for k, p in ((1024, 0.9), (37, 1.0), (5, 0.5)):
+                exp = oracle.random_sample(x, 1.0, k, p, seed)
+                assert np.array_equal(gpu_sample(x, "f32", 1.0, k, p, seed), exp), (x.shape, k, p, seed)
+
+
+def test_random_sample_repeats_and_int32_output():
+    rng = np.random.default_rng(5)
+    x = conv(rng.standard_normal((2, 151936)) * 3, "bf16")
+    first = gpu_sample(x, "bf16", 0.8, 100, 0.9, 42)
+    for _ in range(3):  # the sampler's scratch state returns to zero after every launch
+        assert np.array_equal(gpu_sample(x, "bf16", 0.8, 100, 0.9, 42), first)
+    assert np.array_equal(gpu_sample(x, "bf16", 0.8, 100, 0.9, 42, i64=False), first)
+
+
+def test_random_sample_distribution_on_gpu():
+    x = np.array([2.0, 1.0, 0.5, 0.0, -1.0, 3.0, 0.2, -0.3], np.float32)
+    T, k, p, n = 1.0, 6, 0.9, 3000
+    z = x.astype(np.float64) / T
+    order = np.argsort(-z, kind="stable")[:k]
+    pr = np.exp(z[order] - z[order].max())
+    pr /= pr.sum()
+    keep = int(np.searchsorted(np.cumsum(pr), p - 1e-12) + 1)
+    probs = np.zeros(len(x))
+    probs[order[:keep]] = pr[:keep] / pr[:keep].sum()
+    rows = np.tile(x, (n, 1))  # one launch: row r draws with splitmix64(seed + r)
+    got = gpu_sample(rows, "f32", T, k, p, 1000)
+    assert np.array_equal(got, oracle.random_sample(rows, T, k, p, 1000))
+    counts = np.bincount(got, minlength=len(x))
+    exp = probs * n
+    assert counts[probs == 0].sum() == 0
+    m = exp > 0
+    chi2 = float((((counts[m] - exp[m]) ** 2) / exp[m]).sum())
+    assert chi2 < 30, (counts, exp)
