@@ -93,6 +93,49 @@ constexpr int kXcds = 8;              // accelerator complex dies of an MI355X
 __device__ __forceinline__ void ldsBarrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 constexpr int kTPitch = 2 * kTK + 16; // LDS row pitch (bytes)
 
+// Epilogue of the tiled kernels: D[8 q + 4 h + e][r32] of 32 x 32 tile (i, j) (q, e < 4) is
+// out[row xr + 32 j + r32][channel wr + 32 i + 8 q + 4 h + e], 4 consecutive channels per
+// (q, lane): scale (INT8), bias, one 8-byte store (or element stores at the edge).
+template <typename T, bool kInt8, int TW, int TX>
+__device__ __forceinline__ void storeTiles(const LinearArgs &a, const f32x16 (&acc)[TW][TX], int wr, int xr, int lane) {
+    const int r32 = lane % 32, h2 = lane / 32;
+    const bool vec = a.N % 4 == 0;
+    using C = std::conditional_t<std::is_same_v<T, BF16>, Bf16Cvt, F16Cvt>;
+#pragma unroll
+    for (int i = 0; i < TW; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = wr + 32 * i + 8 * q + 4 * h2;
+            float sc[4], bv[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int ne = min(n + e, a.N - 1);
+                sc[e] = kInt8 ? a.scale[ne] : 1.0f;
+                bv[e] = a.bias ? Fmt<T>::get(a.bias, ne) : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < TX; ++j) {
+                const int m = xr + 32 * j + r32;
+                if (m >= a.M) continue;
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float sum = kInt8 ? sc[e] * acc[i][j][4 * q + e] : acc[i][j][4 * q + e];
+                    v[e] = a.bias ? sum + bv[e] : sum;
+                }
+                if (vec && n + 3 < a.N) {
+                    const uint32_t lo = C::narrow(v[0]) | (C::narrow(v[1]) << 16);
+                    const uint32_t hi = C::narrow(v[2]) | (C::narrow(v[3]) << 16);
+                    *reinterpret_cast<v2u *>(static_cast<char *>(a.out) + (size_t(m) * a.N + n) * 2) = v2u{lo, hi};
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < a.N) Fmt<T>::put(a.out, size_t(m) * a.N + n + e, v[e]);
+                }
+            }
+        }
+}
+
 template <typename T, bool kInt8, int BW, int BX, int NWW, int NWX, int P>
 __global__ void __launch_bounds__(NWW * NWX * 64)
     linearTiled(LinearArgs a) {
@@ -206,43 +249,97 @@ __global__ void __launch_bounds__(NWW * NWX * 64)
         }
     }
 
-    // D[8 q + 4 h + e][r32] of tile (i, j), q < 4, e < 4 = out[row x0 + wx0 + 32 j + r32]
-    // [channel w0 + ww0 + 32 i + 8 q + 4 h + e]: 4 consecutive channels per (q, lane)
-    const bool vec = a.N % 4 == 0;
-    using C = std::conditional_t<std::is_same_v<T, BF16>, Bf16Cvt, F16Cvt>;
+    storeTiles<T, kInt8, TW, TX>(a, acc, w0 + ww0, x0 + wx0, lane);
+}
+
+// Many rows, 16-bit weights, K a multiple of 64: the tiled kernel's MFMA work with the
+// operands moved HBM -> LDS by global_load_lds_dwordx4 (no register staging, no LDS write
+// instructions) through S stages (S - 1 in flight while the MFMAs run on one).  A load
+// instruction fills 1 KB of LDS contiguously (8 rows x 128 B, one 64-k stage of a row),
+// so rows cannot be padded; instead the lane that fills slot c of row r fetches k-chunk
+// c ^ ((r >> 1) & 7), and the MFMA-operand reads apply the same XOR (bank-conflict-free,
+// measured).  Waits count this wave's loads (vmcnt) and one LDS-only barrier per stage
+// makes every wave's loads visible and frees the stage read two steps ago.
+template <int VM>
+__device__ __forceinline__ void waitVmcnt() {
+    // s_waitcnt fields: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8] (15: no wait)
+    __builtin_amdgcn_s_waitcnt((VM & 0xF) | (0x7 << 4) | (0xF << 8) | ((VM >> 4) << 14));
+}
+
+template <typename T, int BW, int BX, int NWW, int NWX, int S>
+__global__ void __launch_bounds__(NWW * NWX * 64)
+    linearDirect(LinearArgs a) {
+    constexpr int NWV = NWW * NWX;
+    constexpr int WW = BW / NWW, WX = BX / NWX, TW = WW / 32, TX = WX / 32;
+    constexpr int kRowB = 2 * kTK;                 // bytes of a row per stage
+    constexpr int kStageB = (BW + BX) * kRowB;
+    constexpr int kLoads = (BW + BX) / 8 / NWV;    // loads (8 rows each) per wave per stage
+    static_assert((BW + BX) % (8 * NWV) == 0 && kLoads * (S - 2) < 64, "load split");
+    __shared__ __align__(16) char lds[S * kStageB];
+    const int tid = int(threadIdx.x), lane = tid % kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int nbx = (a.M + BX - 1) / BX;
+    const int nb = int(gridDim.x), b = int(blockIdx.x);
+    const int v = nb % kXcds == 0 ? (b % kXcds) * (nb / kXcds) + b / kXcds : b;
+    const int bx = v % nbx, bw = v / nbx;
+    const int w0 = bw * BW, x0 = bx * BX;
+    const int ww0 = (wave % NWW) * WW, wx0 = (wave / NWW) * WX;
+    const char *xb = static_cast<const char *>(a.x), *wb = static_cast<const char *>(a.w);
+    const int nk = a.K / kTK;
+    // tile rows [0, BW) are weight rows, [BW, BW + BX) activation rows (clamped at the edges)
+    const char *src[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int tr = 8 * (wave * kLoads + i) + lane / 8;
+        const int kc = (lane % 8) ^ ((tr >> 1) & 7);
+        src[i] = tr < BW ? wb + (size_t(min(w0 + tr, a.N - 1)) * a.K + 8 * kc) * 2
+                         : xb + (size_t(min(x0 + tr - BW, a.M - 1)) * a.K + 8 * kc) * 2;
+    }
+    const auto issue = [&](int kt) { // past the last stage: the last stage again, never read
+        const int ktc = min(kt, nk - 1);
+        char *dst = lds + (kt % S) * kStageB;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i)
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1))) *)(src[i] + size_t(ktc) * kRowB),
+                (void __attribute__((address_space(3))) *)(dst + 8 * (wave * kLoads + i) * kRowB), 16, 0, 0);
+    };
+    f32x16 acc[TW][TX];
 #pragma unroll
     for (int i = 0; i < TW; ++i)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int n = w0 + ww0 + 32 * i + 8 * q + 4 * h2;
-            float sc[4], bv[4];
+        for (int j = 0; j < TX; ++j)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int ne = min(n + e, a.N - 1);
-                sc[e] = kInt8 ? a.scale[ne] : 1.0f;
-                bv[e] = a.bias ? Fmt<T>::get(a.bias, ne) : 0.0f;
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    const int r32 = lane % 32, h2 = lane / 32;
+#pragma unroll
+    for (int st = 0; st < S - 1; ++st) issue(st);
+    for (int kt = 0; kt < nk; ++kt) {
+        waitVmcnt<kLoads * (S - 2)>(); // this wave's loads of stage kt have landed
+        ldsBarrier();                  // every wave's have; stage kt - 1 is no longer read
+        issue(kt + S - 1);
+        const char *tile = lds + (kt % S) * kStageB;
+#pragma unroll
+        for (int st = 0; st < kTK / 16; ++st) {
+            v4u fa[TW], fb[TX];
+#pragma unroll
+            for (int i = 0; i < TW; ++i) {
+                const int row = ww0 + 32 * i + r32;
+                fa[i] = *reinterpret_cast<const v4u *>(tile + row * kRowB + 16 * ((2 * st + h2) ^ ((row >> 1) & 7)));
             }
 #pragma unroll
             for (int j = 0; j < TX; ++j) {
-                const int m = x0 + wx0 + 32 * j + r32;
-                if (m >= a.M) continue;
-                float v[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float sum = kInt8 ? sc[e] * acc[i][j][4 * q + e] : acc[i][j][4 * q + e];
-                    v[e] = a.bias ? sum + bv[e] : sum;
-                }
-                if (vec && n + 3 < a.N) {
-                    const uint32_t lo = C::narrow(v[0]) | (C::narrow(v[1]) << 16);
-                    const uint32_t hi = C::narrow(v[2]) | (C::narrow(v[3]) << 16);
-                    *reinterpret_cast<v2u *>(static_cast<char *>(a.out) + (size_t(m) * a.N + n) * 2) = v2u{lo, hi};
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n + e < a.N) Fmt<T>::put(a.out, size_t(m) * a.N + n + e, v[e]);
-                }
+                const int row = BW + wx0 + 32 * j + r32;
+                fb[j] = *reinterpret_cast<const v4u *>(tile + row * kRowB + 16 * ((2 * st + h2) ^ ((row >> 1) & 7)));
             }
+#pragma unroll
+            for (int i = 0; i < TW; ++i)
+#pragma unroll
+                for (int j = 0; j < TX; ++j) acc[i][j] = mfma32<T>(fa[i], fb[j], acc[i][j]);
         }
+    }
+    waitVmcnt<0>(); // no LDS write may still be landing when the wave ends
+    storeTiles<T, false, TW, TX>(a, acc, w0 + ww0, x0 + wx0, lane);
 }
 
 // Few rows (M <= 16, decode): HBM-bound on the weights.  A block owns 16 output channels
@@ -463,10 +560,14 @@ void launch(const LinearArgs &a, hipStream_t s) {
             const auto blocks = [&](int bw, int bx) {
                 return unsigned((a.N + bw - 1) / bw) * unsigned((a.M + bx - 1) / bx);
             };
-            if (blocks(128, 128) >= 192)
-                linearTiled<T, kInt8, 128, 128, 4, 2, 2><<<blocks(128, 128), 512, 0, s>>>(a);
-            else
+            if (blocks(128, 128) >= 192) {
+                if (!kInt8 && a.K % kTK == 0)
+                    linearDirect<T, 128, 128, 4, 2, 3><<<blocks(128, 128), 512, 0, s>>>(a);
+                else
+                    linearTiled<T, kInt8, 128, 128, 4, 2, 2><<<blocks(128, 128), 512, 0, s>>>(a);
+            } else {
                 linearTiled<T, kInt8, 64, 64, 2, 2, 2><<<blocks(64, 64), 256, 0, s>>>(a);
+            }
         }
         return;
     }
