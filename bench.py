@@ -190,6 +190,123 @@ class Chain:
         O.argmax_rows(self.tok_idx, self.tok_val, self.logits)
 
 
+class DecodeChain:
+    """One decode step of Qwen2-1.5B built from the library's entry points only (random
+    weights, the reference's layer structure, src/models/qwen2/{layer,attention,mlp}.hpp):
+    embedding; per layer add+rms_norm, q / k / v linear (with bias), fused RoPE + INT8 KV
+    append at position CTX, attention over the CTX + 1 cached tokens (INT8 KV), o linear,
+    add+rms_norm, gate / up linear, swiglu, down linear; then the final norm, the lm_head
+    linear and a sample (T 0.8, top_k 50, top_p 0.8).  Projection weights are INT8 codes +
+    per-channel scales (W8A16) or bf16; every layer has its own copies, so no cache serves
+    them.  Like production Qwen2 decoders, q / k / v are one concatenated [2048, 1536]
+    projection (with its bias) and gate / up one [17920, 1536] projection: one linear launch
+    each, the one-row outputs split by slicing."""
+
+    LAYERS, CTX = 28, 4096
+
+    def __init__(self, L, int8_weights=True, seed=6):
+        BF, I8, F32, I64 = L.DataType.BF16, L.DataType.I8, L.DataType.F32, L.DataType.I64
+        dev = dict(device=L.DeviceType.AMD, device_id=0)
+        rng = np.random.default_rng(seed)
+        api = L.RuntimeAPI(L.DeviceType.AMD)
+        O = L.Ops
+        self.L, self.int8 = L, int8_weights
+        QKV = (NH + 2 * NKV) * D
+        shapes = {"qkv": (QKV, H), "o": (H, NH * D), "gate_up": (2 * I, H), "down": (H, I)}
+
+        def copies(proto, n):
+            out = [proto]
+            for _ in range(n - 1):
+                t = L.Tensor(proto.shape(), proto.dtype(), **dev)
+                api.memcpy_sync(t.data_ptr(), proto.data_ptr(), proto.numel() * (1 if proto.dtype() == I8 else 2 if proto.dtype() == BF else 4), L.MemcpyKind.D2D)
+                out.append(t)
+            return out
+
+        self.w = {}
+        for name, shp in shapes.items():
+            wb = L.Tensor.from_numpy(bf16(rng, shp, 0.02), BF, **dev)
+            if int8_weights:
+                q, sc = L.Tensor(shp, I8, **dev), L.Tensor((shp[0],), F32, **dev)
+                O.quantize_int8(q, sc, wb)
+                self.w[name] = list(zip(copies(q, self.LAYERS), copies(sc, self.LAYERS)))
+            else:
+                self.w[name] = [(t, None) for t in copies(wb, self.LAYERS)]
+        self.bias = copies(L.Tensor.from_numpy(bf16(rng, (QKV,), 0.1), BF, **dev), self.LAYERS)
+        self.norm = [(L.Tensor.from_numpy(bf16(rng, (H,), 0.1, 1.0), BF, **dev),
+                      L.Tensor.from_numpy(bf16(rng, (H,), 0.1, 1.0), BF, **dev)) for _ in range(self.LAYERS)]
+        # INT8 KV caches holding CTX tokens, one row more for the step's append
+        kv0 = [L.Tensor.from_numpy(bf16(rng, (self.CTX, NKV, D)), BF, **dev) for _ in range(2)]
+        self.cache = []
+        for _ in range(self.LAYERS):
+            c = {}
+            for nm, src in (("k", kv0[0]), ("v", kv0[1])):
+                c[nm] = L.Tensor((self.CTX + 1, NKV, D), I8, **dev)
+                c[nm + "s"] = L.Tensor((self.CTX + 1, NKV), F32, **dev)
+                O.kv_append_int8(c[nm], c[nm + "s"], src, 0)
+            c["kview"] = c["k"].slice(0, 0, self.CTX + 1)
+            c["vview"] = c["v"].slice(0, 0, self.CTX + 1)
+            self.cache.append(c)
+        self.table = L.Tensor.from_numpy(bf16(rng, (V, H), 0.02), BF, **dev)
+        if int8_weights:
+            lq, ls = L.Tensor((V, H), I8, **dev), L.Tensor((V,), F32, **dev)
+            O.quantize_int8(lq, ls, L.Tensor.from_numpy(bf16(rng, (V, H), 0.02), BF, **dev))
+            self.lm = (lq, ls)
+        else:
+            self.lm = (L.Tensor.from_numpy(bf16(rng, (V, H), 0.02), BF, **dev), None)
+        self.wf = L.Tensor.from_numpy(bf16(rng, (H,), 0.1, 1.0), BF, **dev)
+        self.ids = L.Tensor.from_numpy(np.array([12345], np.int64), **dev)
+        self.pos = L.Tensor.from_numpy(np.array([self.CTX], np.int64), **dev)
+        t = lambda shp, dt=BF: L.Tensor(shp, dt, **dev)
+        self.x, self.n, self.prev = t((1, H)), t((1, H)), t((1, H))
+        self.qkv = t((1, QKV))
+        flat = self.qkv.view(QKV)
+        self.qv = flat.slice(0, 0, NH * D).view(1, NH, D)
+        self.kv = flat.slice(0, NH * D, (NH + NKV) * D).view(1, NKV, D)
+        self.vv = flat.slice(0, (NH + NKV) * D, QKV).view(1, NKV, D)
+        self.gu = t((1, 2 * I))
+        gflat = self.gu.view(2 * I)
+        self.g, self.u = gflat.slice(0, 0, I).view(1, I), gflat.slice(0, I, 2 * I).view(1, I)
+        self.qr, self.att, self.o = t((1, NH, D)), t((1, NH, D)), t((1, H))
+        self.a, self.d = t((1, I)), t((1, H))
+        self.logits, self.tok = t((1, V)), t((1,), I64)
+        self.zero = L.Tensor.from_numpy(np.zeros((1, H), np.uint16), BF, **dev)
+
+    def _lin(self, out, x, pair, bias=None):
+        O = self.L.Ops
+        w, sc = pair
+        if sc is None:
+            O.linear(out, x, w, bias)
+        else:
+            O.linear_w8a16(out, x, w, sc, bias)
+
+    def weight_bytes(self):
+        per = sum(r * c for r, c in (((NH + 2 * NKV) * D, H), (H, NH * D), (2 * I, H), (H, I)))
+        e = 1 if self.int8 else 2
+        return self.LAYERS * per * e + V * H * e
+
+    def run(self, seed=0):
+        O = self.L.Ops
+        O.embedding(self.prev, self.ids, self.table)
+        api_x = self.zero
+        for l in range(self.LAYERS):
+            c = self.cache[l]
+            # x = prev + x (the first layer adds the embedding to zero); n = rms_norm(x)
+            O.add_rms_norm(self.n, self.x, self.prev, api_x if l == 0 else self.x, self.norm[l][0], 1e-6)
+            self._lin(self.qkv, self.n, self.w["qkv"][l], self.bias[l])
+            O.rope_kv_append_int8(self.qr, self.qv, self.kv, self.vv, self.pos, 1e6,
+                                  c["k"], c["ks"], c["v"], c["vs"], self.CTX)
+            O.self_attention_int8kv(self.att, self.qr, c["kview"], c["ks"], c["vview"], c["vs"],
+                                    1.0 / np.sqrt(D))
+            self._lin(self.o, self.att.view(1, NH * D), self.w["o"][l])
+            O.add_rms_norm(self.n, self.x, self.o, self.x, self.norm[l][1], 1e-6)
+            self._lin(self.gu, self.n, self.w["gate_up"][l])
+            O.swiglu(self.a, self.g, self.u)
+            self._lin(self.prev, self.a, self.w["down"][l])
+        O.add_rms_norm(self.n, self.x, self.prev, self.x, self.wf, 1e-6)
+        self._lin(self.logits, self.n, self.lm)
+        O.random_sample(self.tok, self.logits, 0.8, 50, 0.8, seed)
+
+
 class Pool:
     """Disjoint buffer sets cut from one allocation per tensor (slice + view keep the byte
     offset), filled with seeded normal samples; enough sets that one pass over them moves
@@ -504,6 +621,43 @@ def measure_rearrange(L, hip, stream, e0, e1, steps):
     return res
 
 
+def measure_decode(L, hip, stream, e0, e1, graphs=True, int8_only=False):
+    """One Qwen2-1.5B decode step (DecodeChain) at context 4096, replayed as one HIP graph
+    (graphs=False: eager launches, for kernel tracing), with INT8 and with bf16 projection
+    weights: ms per token, tokens/s, and the weight bytes streamed per token against HBM."""
+    res = {}
+    for int8 in ((True,) if int8_only else (True, False)):
+        label = "INT8 weights (W8A16), INT8 KV" if int8 else "bf16 weights, INT8 KV"
+        print(f"bench: building decode chain ({label})", file=sys.stderr, flush=True)
+        dc = DecodeChain(L, int8)
+        for i in range(2):
+            dc.run(i)
+        graph = None
+        if graphs:
+            graph = L.Graph.capture()
+            dc.run(7)
+            graph.end()
+        step = graph.launch if graphs else dc.run
+        for _ in range(3):
+            step()
+        nrep = 20
+        hip.record(e0, stream)
+        for _ in range(nrep):
+            step()
+        hip.record(e1, stream)
+        ms = hip.elapsed_ms(e0, e1) / nrep
+        wb = dc.weight_bytes()
+        res[label] = {"ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+                      "weight_bytes": wb, "weight_GB_s": round(wb / (ms * 1e-3) / 1e9, 1),
+                      "frac_peak": round(wb / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                      "context": DecodeChain.CTX, "layers": DecodeChain.LAYERS,
+                      "launch": "one HIP graph" if graphs else "eager"}
+        assert L.take_device_error() == 0
+        del graph, dc
+    print("bench: decode " + json.dumps(res), file=sys.stderr, flush=True)
+    return res
+
+
 def cpu_baseline(seconds):
     """Reference CPU ops (oracle/_ref, else the oracle port) on a row sample of config 1,
     single thread pinned to one core; GB/s with the same bytes formula as the GPU."""
@@ -616,6 +770,11 @@ def main():
                     help="only the self-attention lines (profiling); prints their JSON")
     ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain (profiling)")
     ap.add_argument("--no-linear", action="store_true", help="skip the linear and rearrange lines")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode-step chain")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode-step chain; prints its JSON")
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="with --decode-only: INT8 weights only, eager launches (kernel tracing)")
     ap.add_argument("--linear-only", action="store_true",
                     help="only the linear and rearrange lines (profiling); prints their JSON")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -640,6 +799,11 @@ def main():
         for _ in range(args.steps):
             graph.launch()
         api.device_synchronize()
+        return
+    if args.decode_only:
+        print(json.dumps({"decode": measure_decode(L, hip, stream, hip.event(), hip.event(),
+                                                   graphs=not args.decode_eager,
+                                                   int8_only=args.decode_eager)}), flush=True)
         return
     if args.linear_only:
         res = measure_linear(L, hip, stream, e0=hip.event(), e1=hip.event(), steps=args.steps)
@@ -762,6 +926,9 @@ def main():
     attention = None
     if not args.no_attention:
         attention = measure_attention(L, hip, stream, e0, e1, args.steps)
+    decode = None
+    if not args.no_decode:
+        decode = measure_decode(L, hip, stream, e0, e1)
     linear = None
     if not args.no_linear:
         linear = measure_linear(L, hip, stream, e0, e1, args.steps)
@@ -787,7 +954,7 @@ def main():
         "tokens_per_s": round(T / (ms_step * 1e-3)),
         "wall_s_timed": round(wall, 3),
         "per_op": per_op, "chain": chain, "configs": configs, "attention": attention,
-        "linear": linear, "roofline": roof,
+        "linear": linear, "decode": decode, "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
