@@ -10,13 +10,16 @@
 // when that max beats the lane's best, which is rare on real logits), then (value, index)
 // pairs are merged across the wavefront with butterflies and across wavefronts through
 // LDS, ties going to the lower index.  Rows: one 256-thread block per row.  Flat: the
-// vector is cut into segments, one block each; every block stores its partial, and the
-// last block to finish (a device-scope counter) merges them, all in one launch.
+// vector is cut into segments, one block each; every block folds its best into one
+// device-scope 64-bit atomic maximum of (value bits, ~index) and the last block to arrive
+// (a device-scope counter) reads it, all in one launch and with no L2 write-back fence
+// (above 2^32 elements: partials behind a fence, merged by the last block).
 // The final write uses the values the scans already hold (element 0 and the winner), so
 // no input element is re-read after the merge.
 //
-// Latency (MI355X, rocprof, [1, 151936] bf16): 6.6 us, of which a near-empty launch is
-// 1.6 us and one HBM round trip about 1.2 us.  One 1024-thread block issuing all its
+// Latency (MI355X, [1, 151936] bf16): 5.6 us with the atomic maximum (6.6-7.0 us when
+// every block stored a partial behind an agent-scope fence, which writes back the L2);
+// a near-empty launch is 1.6 us and one HBM round trip about 1.2 us.  One 1024-thread block issuing all its
 // loads at once took 17 us: a single CU keeps too few misses in flight to stream 300 KB,
 // so the vector is spread over 19 blocks and the cross-block merge stays.
 #include "common.hpp"
@@ -181,6 +184,59 @@ __global__ void __launch_bounds__(kBlock)
     }
 }
 
+// Flat argmax for n < 2^32 without partials or fences: every block folds its best
+// (value, index) into one device-scope 64-bit atomic maximum of the key
+// (order-preserving bits of the value) << 32 | ~index -- a larger value, then a lower
+// index, makes a larger key; a block with no candidate (all -inf / NaN) skips it.  The
+// atomic returns its old value, and the wait for it orders the maximum before the block's
+// arrival count; the last block to arrive reads the key (and element 0) with device-scope
+// loads, finishes, and leaves key and counter zero.  Device-scope atomics are performed at
+// the device's coherence point, so no L2 write-back fence is needed between blocks.
+struct FlatSlots {
+    unsigned counter; // the launch's arrival count (offset 0 of the scratch)
+    unsigned x0bits;  // element 0, stored by block 0 before it arrives
+    unsigned long long key;
+};
+
+__device__ __forceinline__ uint32_t orderBits(float v) {
+    const uint32_t b = __float_as_uint(v);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kBlock)
+    argmaxFlatAtomic(void *idx, bool i64, void *val, const void *__restrict__ vals, size_t n,
+                     size_t seg, bool vec, FlatSlots *sl) {
+    const size_t begin = size_t(blockIdx.x) * seg;
+    const size_t end = begin + seg < n ? begin + seg : n;
+    float x0 = 0.0f;
+    Best b = blockMerge(scan<T>(vals, begin, end, vec, &x0));
+    if (threadIdx.x != 0) return;
+    unsigned long long seen = 0;
+    if (blockIdx.x == 0)
+        seen += __hip_atomic_exchange(&sl->x0bits, __float_as_uint(x0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (b.i != kNone) {
+        const unsigned long long key = (uint64_t(orderBits(b.v)) << 32) | uint64_t(~uint32_t(b.i));
+        seen += __hip_atomic_fetch_max(&sl->key, key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Consuming the returned values keeps both atomics in their returning form, and the
+    // wait completes them before the arrival is counted.
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(seen)::"memory");
+    if (__hip_atomic_fetch_add(&sl->counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != gridDim.x - 1)
+        return;
+    const unsigned long long key = __hip_atomic_load(&sl->key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float x0_all = __uint_as_float(__hip_atomic_load(&sl->x0bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    Best m{-INFINITY, kNone};
+    if (key != 0) {
+        const uint32_t ob = uint32_t(key >> 32);
+        m.v = __uint_as_float((ob & 0x80000000u) ? (ob & 0x7FFFFFFFu) : ~ob);
+        m.i = int64_t(~uint32_t(key));
+    }
+    finish<T>(m, x0_all, idx, i64, val, 0);
+    __hip_atomic_store(&sl->key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&sl->counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 constexpr size_t kCounterBytes = kScratchReserved;
 
 template <typename T>
@@ -209,6 +265,11 @@ void launchFlat(void *idx, bool i64, void *val, const void *vals, size_t n, void
     if (n == 0) return;
     const size_t seg = segmentOf<T>();
     const unsigned blocks = unsigned((n + seg - 1) / seg);
+    if (n < (size_t(1) << 32)) {
+        argmaxFlatAtomic<T><<<blocks, kBlock, 0, s>>>(idx, i64, val, vals, n, seg, aligned16(vals),
+                                                      static_cast<FlatSlots *>(ws));
+        return;
+    }
     auto *counter = static_cast<unsigned *>(ws);
     auto *part = reinterpret_cast<Partial *>(static_cast<char *>(ws) + kCounterBytes);
     argmaxFlatKernel<T><<<blocks, kBlock, 0, s>>>(idx, i64, val, vals, n, seg, aligned16(vals),

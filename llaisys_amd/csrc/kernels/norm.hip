@@ -24,7 +24,7 @@ namespace llaisys::kernels {
 
 namespace {
 
-template <typename T, int G, int VMAX, bool kFused>
+template <typename T, int G, int VMAX, bool kFused, bool kWPre>
 __global__ void __launch_bounds__(blockFor<G>())
     rmsNormRows(void *__restrict__ out, void *residual_out, const void *__restrict__ in,
                 const void *residual, const void *__restrict__ weight, size_t rows, int cols,
@@ -44,14 +44,19 @@ __global__ void __launch_bounds__(blockFor<G>())
     // the residual) are issued before any store: residual_out may alias residual, so the
     // compiler could not hoist a residual load above an earlier residual store itself, and
     // the loads would turn into a chain of dependent round trips.
+    // kWPre (few rows): the weight vectors are loaded here too -- after the reduction they
+    // would be one more dependent round trip, which a single row (decode) waits on; with
+    // many rows the registers cost more occupancy than the latency they hide.
     v4u raw[VMAX];
     v4u res[kFused ? VMAX : 1];
+    v4u wv[kWPre ? VMAX : 1];
 #pragma unroll
     for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
         if (live && vi < nvec) {
             raw[v] = load16Stream<T>(in, base + size_t(vi) * N);
             if constexpr (kFused) res[v] = load16Stream<T>(residual, base + size_t(vi) * N);
+            if constexpr (kWPre) wv[v] = load16<T>(weight, size_t(vi) * N);
         }
     }
     if constexpr (kFused) {
@@ -89,7 +94,7 @@ __global__ void __launch_bounds__(blockFor<G>())
         if (live && vi < nvec) {
             float x[N], w[N], y[N];
             F::unpack(raw[v], x);
-            F::unpack(load16<T>(weight, size_t(vi) * N), w);
+            F::unpack(kWPre ? wv[kWPre ? v : 0] : load16<T>(weight, size_t(vi) * N), w);
 #pragma unroll
             for (int e = 0; e < N; ++e) y[e] = x[e] * w[e] * inv;
             store16Stream<T>(out, base + size_t(vi) * N, F::packQ(y));
@@ -139,12 +144,19 @@ void launch(void *out, void *res_out, const void *in, const void *res, const voi
         constexpr int G = decltype(g)::value, V = decltype(v)::value; // V: vectors per lane
         constexpr int kBlock = blockFor<G>();
         const unsigned grid = blocksFor(rows, kBlock / G);
-        if (fused)
-            rmsNormRows<T, G, V, true><<<grid, kBlock, 0, s>>>(out, res_out, in, res, w, rows,
-                                                                int(cols), eps);
+        const bool few = rows <= 64;
+        if (fused && few)
+            rmsNormRows<T, G, V, true, true><<<grid, kBlock, 0, s>>>(out, res_out, in, res, w, rows,
+                                                                      int(cols), eps);
+        else if (fused)
+            rmsNormRows<T, G, V, true, false><<<grid, kBlock, 0, s>>>(out, res_out, in, res, w, rows,
+                                                                       int(cols), eps);
+        else if (few)
+            rmsNormRows<T, G, V, false, true><<<grid, kBlock, 0, s>>>(out, nullptr, in, nullptr, w,
+                                                                       rows, int(cols), eps);
         else
-            rmsNormRows<T, G, V, false><<<grid, kBlock, 0, s>>>(out, nullptr, in, nullptr, w,
-                                                                 rows, int(cols), eps);
+            rmsNormRows<T, G, V, false, false><<<grid, kBlock, 0, s>>>(out, nullptr, in, nullptr, w,
+                                                                        rows, int(cols), eps);
         done = true;
     });
     if (done) return;
