@@ -358,7 +358,10 @@ __global__ void __launch_bounds__(kFinThreads)
             if (target == 0) target = 1;
         }
     }
-    if (t == 0) kept = k;
+    if (t == 0) {
+        kept = k;
+        pick = 0; // overwritten below: r < the kept weight sum, so the crossing exists
+    }
     __syncthreads();
     if (target)
         for (int j = t; j < k; j += kFinThreads)
