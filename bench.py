@@ -204,13 +204,13 @@ class DecodeChain:
 
     LAYERS, CTX = 28, 4096
 
-    def __init__(self, L, int8_weights=True, seed=6):
+    def __init__(self, L, int8_weights=True, seed=6, fused=True):
         BF, I8, F32, I64 = L.DataType.BF16, L.DataType.I8, L.DataType.F32, L.DataType.I64
         dev = dict(device=L.DeviceType.AMD, device_id=0)
         rng = np.random.default_rng(seed)
         api = L.RuntimeAPI(L.DeviceType.AMD)
         O = L.Ops
-        self.L, self.int8 = L, int8_weights
+        self.L, self.int8, self.fused = L, int8_weights, fused
         QKV = (NH + 2 * NKV) * D
         shapes = {"qkv": (QKV, H), "o": (H, NH * D), "gate_up": (2 * I, H), "down": (H, I)}
 
@@ -258,6 +258,7 @@ class DecodeChain:
         self.pos = L.Tensor.from_numpy(np.array([self.CTX], np.int64), **dev)
         t = lambda shp, dt=BF: L.Tensor(shp, dt, **dev)
         self.x, self.n, self.prev = t((1, H)), t((1, H)), t((1, H))
+        self.x2 = t((1, H))  # the fused ops write the residual stream ping-pong
         self.qkv = t((1, QKV))
         flat = self.qkv.view(QKV)
         self.qv = flat.slice(0, 0, NH * D).view(1, NH, D)
@@ -285,6 +286,8 @@ class DecodeChain:
         return self.LAYERS * per * e + V * H * e
 
     def run(self, seed=0):
+        if self.fused:
+            return self.run_fused(seed)
         O = self.L.Ops
         O.embedding(self.prev, self.ids, self.table)
         api_x = self.zero
@@ -293,16 +296,42 @@ class DecodeChain:
             # x = prev + x (the first layer adds the embedding to zero); n = rms_norm(x)
             O.add_rms_norm(self.n, self.x, self.prev, api_x if l == 0 else self.x, self.norm[l][0], 1e-6)
             self._lin(self.qkv, self.n, self.w["qkv"][l], self.bias[l])
-            O.rope_kv_append_int8(self.qr, self.qv, self.kv, self.vv, self.pos, 1e6,
-                                  c["k"], c["ks"], c["v"], c["vs"], self.CTX)
-            O.self_attention_int8kv(self.att, self.qr, c["kview"], c["ks"], c["vview"], c["vs"],
-                                    1.0 / np.sqrt(D))
-            self._lin(self.o, self.att.view(1, NH * D), self.w["o"][l])
+            self._attend(l)
             O.add_rms_norm(self.n, self.x, self.o, self.x, self.norm[l][1], 1e-6)
             self._lin(self.gu, self.n, self.w["gate_up"][l])
             O.swiglu(self.a, self.g, self.u)
             self._lin(self.prev, self.a, self.w["down"][l])
         O.add_rms_norm(self.n, self.x, self.prev, self.x, self.wf, 1e-6)
+        self._lin(self.logits, self.n, self.lm)
+        O.random_sample(self.tok, self.logits, 0.8, 50, 0.8, seed)
+
+    def _attend(self, l):
+        """RoPE + INT8 KV append, attention over the cache, o projection -> self.o."""
+        O, c = self.L.Ops, self.cache[l]
+        O.rope_kv_append_int8(self.qr, self.qv, self.kv, self.vv, self.pos, 1e6,
+                              c["k"], c["ks"], c["v"], c["vs"], self.CTX)
+        O.self_attention_int8kv(self.att, self.qr, c["kview"], c["ks"], c["vview"], c["vs"],
+                                1.0 / np.sqrt(D))
+        self._lin(self.o, self.att.view(1, NH * D), self.w["o"][l])
+
+    def run_fused(self, seed=0):
+        """The same step with the norms fused into the projections after them and swiglu
+        into the gate / up projection (llaisysRmsNormLinear): 7 launches per layer."""
+        O = self.L.Ops
+        O.embedding(self.prev, self.ids, self.table)
+        cur, nxt = self.zero, self.x
+        for l in range(self.LAYERS):
+            w, sc = self.w["qkv"][l]
+            O.rms_norm_linear(self.qkv, self.prev, self.norm[l][0], 1e-6, w, sc, self.bias[l],
+                              residual=cur, residual_out=nxt)
+            cur, nxt = nxt, (self.x2 if nxt is self.x else self.x)
+            self._attend(l)
+            w, sc = self.w["gate_up"][l]
+            O.rms_norm_linear(self.a, self.o, self.norm[l][1], 1e-6, w, sc, residual=cur,
+                              residual_out=nxt, swiglu=True)
+            cur, nxt = nxt, (self.x2 if nxt is self.x else self.x)
+            self._lin(self.prev, self.a, self.w["down"][l])
+        O.add_rms_norm(self.n, nxt, self.prev, cur, self.wf, 1e-6)
         self._lin(self.logits, self.n, self.lm)
         O.random_sample(self.tok, self.logits, 0.8, 50, 0.8, seed)
 
@@ -624,12 +653,18 @@ def measure_rearrange(L, hip, stream, e0, e1, steps):
 def measure_decode(L, hip, stream, e0, e1, graphs=True, int8_only=False):
     """One Qwen2-1.5B decode step (DecodeChain) at context 4096, replayed as one HIP graph
     (graphs=False: eager launches, for kernel tracing), with INT8 and with bf16 projection
-    weights: ms per token, tokens/s, and the weight bytes streamed per token against HBM."""
+    weights, each with the norms and swiglu fused into the projections and as separate
+    launches: ms per token, tokens/s, and the weight bytes streamed per token against HBM.
+    int8_only: the fused INT8 chain alone."""
     res = {}
-    for int8 in ((True,) if int8_only else (True, False)):
-        label = "INT8 weights (W8A16), INT8 KV" if int8 else "bf16 weights, INT8 KV"
+    variants = [(True, True), (True, False), (False, True), (False, False)]
+    for int8, fused in variants:
+        if int8_only and not (int8 and fused):
+            continue
+        label = ("INT8 weights (W8A16), INT8 KV" if int8 else "bf16 weights, INT8 KV") + \
+            ("" if fused else ", norms and swiglu as separate launches")
         print(f"bench: building decode chain ({label})", file=sys.stderr, flush=True)
-        dc = DecodeChain(L, int8)
+        dc = DecodeChain(L, int8, fused=fused)
         for i in range(2):
             dc.run(i)
         graph = None
@@ -774,7 +809,7 @@ def main():
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode-step chain; prints its JSON")
     ap.add_argument("--decode-eager", action="store_true",
-                    help="with --decode-only: INT8 weights only, eager launches (kernel tracing)")
+                    help="with --decode-only: the fused INT8 chain only, eager launches (kernel tracing)")
     ap.add_argument("--linear-only", action="store_true",
                     help="only the linear and rearrange lines (profiling); prints their JSON")
     ap.add_argument("--traffic-probe", action="store_true",

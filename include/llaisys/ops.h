@@ -132,6 +132,21 @@ __C {
     __export void llaisysLinearW8A16(llaisysTensor_t out, llaisysTensor_t in,
                                      llaisysTensor_t w_codes, llaisysTensor_t w_scale,
                                      llaisysTensor_t bias);
+    /* rms_norm fused ahead of a linear, optionally with swiglu after it (no reference
+     * counterpart; the decoder's input_layernorm -> q/k/v projections and add ->
+     * post_attention_layernorm -> gate / up -> swiglu, src/models/qwen2/layer.hpp:51-53,
+     * :66-71, src/models/qwen2/mlp.hpp:22-33).  h = residual ? in + residual : in (rounded as
+     * llaisysAdd; stored to residual_out, which must not overlap in or residual; both NULL for
+     * no add); xn = llaisysRmsNorm(h, norm_weight, eps); y = llaisysLinear(xn, weight, bias), or
+     * llaisysLinearW8A16 when weight_scale is non-NULL; out = y, or with swiglu != 0 out[m][n] =
+     * swiglu(gate = y[m][n], up = y[m][n + Nw/2]) for a weight of Nw rows (out [rows, Nw/2]).
+     * bias NULL or zero-element means no bias.  One launch for one row; other row counts run
+     * the ops one after another. */
+    __export void llaisysRmsNormLinear(llaisysTensor_t out, llaisysTensor_t residual_out,
+                                       llaisysTensor_t in, llaisysTensor_t residual,
+                                       llaisysTensor_t norm_weight, float eps,
+                                       llaisysTensor_t weight, llaisysTensor_t weight_scale,
+                                       llaisysTensor_t bias, uint8_t swiglu);
     /* Random sampling after argmax (no reference kernel: README.md:397-399 asks for a random
      * sample operator with temperature, top-k and top-p; python/llaisys/models/qwen2.py:216-218
      * takes the three and ignores them).  logits [V] or [rows, V] (F32 / BF16 / F16), out_idx

@@ -207,6 +207,16 @@ __C {
                                   bias ? bias->tensor : nullptr);
     }
 
+    void llaisysRmsNormLinear(llaisysTensor_t out, llaisysTensor_t residual_out, llaisysTensor_t in,
+                              llaisysTensor_t residual, llaisysTensor_t norm_weight, float eps,
+                              llaisysTensor_t weight, llaisysTensor_t weight_scale,
+                              llaisysTensor_t bias, uint8_t swiglu) {
+        const auto opt = [](llaisysTensor_t t) { return t ? t->tensor : nullptr; };
+        llaisys::ops::rmsNormLinear(out->tensor, opt(residual_out), in->tensor, opt(residual),
+                                    norm_weight->tensor, eps, weight->tensor, opt(weight_scale),
+                                    opt(bias), swiglu != 0);
+    }
+
     void llaisysRandomSample(llaisysTensor_t out_idx, llaisysTensor_t logits, float temperature,
                              int64_t top_k, float top_p, uint64_t seed) {
         llaisys::ops::randomSample(out_idx->tensor, logits->tensor, temperature, top_k, top_p, seed);

@@ -231,4 +231,21 @@ __device__ __forceinline__ V groupReduce(V v, V *red) {
     return v;
 }
 
+// swiglu of one element, reference src/ops/swiglu/cpu/swiglu_cpu.cpp:15-20: u * (g / (1 +
+// exp(-g))) in f32.  g / d is g * rcp(d) plus one Newton correction; where 1 / d would be
+// subnormal or zero it is the IEEE quotient.
+struct SwigluOp {
+    __device__ static float apply(float g, float u) {
+        const float d = 1.0f + __expf(-g);
+        float q;
+        if (__builtin_expect(d < 0x1p126f, 1)) {
+            const float r = __builtin_amdgcn_rcpf(d);
+            q = g * r;
+            q = __builtin_fmaf(__builtin_fmaf(-d, q, g), r, q);
+        } else {
+            q = g / d; // 1/d would be subnormal or 0: take the IEEE quotient
+        }
+        return u * q;
+    }
+};
 } // namespace llaisys::kernels

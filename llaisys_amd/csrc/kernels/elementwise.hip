@@ -34,20 +34,6 @@ constexpr int kDequantU = 4;
 // stream measured the same way: 65.1 vs 66.0 us).
 constexpr int kBinaryBlock = 64;
 
-struct SwigluOp {
-    __device__ static float apply(float g, float u) {
-        const float d = 1.0f + __expf(-g);
-        float q;
-        if (__builtin_expect(d < 0x1p126f, 1)) {
-            const float r = __builtin_amdgcn_rcpf(d);
-            q = g * r;
-            q = __builtin_fmaf(__builtin_fmaf(-d, q, g), r, q);
-        } else {
-            q = g / d; // 1/d would be subnormal or 0: take the IEEE quotient
-        }
-        return u * q;
-    }
-};
 struct AddOp {
     __device__ static float apply(float a, float b) { return a + b; }
 };

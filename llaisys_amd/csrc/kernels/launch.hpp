@@ -107,6 +107,17 @@ void linear(void *out, const void *x, const void *w, const float *w_scale, const
             size_t rows, size_t in_features, size_t out_features, llaisysDataType_t dt,
             hipStream_t stream);
 
+// One row: h = residual ? T(in + residual) : in (h stored to residual_out when residual is
+// non-null), xn = rms_norm(h) as rmsNorm computes it, y = linear(xn) (W8A16 when w_scale is
+// non-null) as linear computes one row with its GEMV, and out = y, or with `swiglu`
+// out[n] = swiglu(gate = y[n], up = y[n + out_features]) over a weight of 2 * out_features
+// rows.  residual_out must not overlap in or residual.  Returns false (nothing launched)
+// for shapes the fused kernel does not cover; the caller then composes the ops.
+bool rmsNormLinearFused(void *out, void *residual_out, const void *in, const void *residual,
+                        const void *norm_weight, float eps, const void *w, const float *w_scale,
+                        const void *bias, size_t rows, size_t in_features, size_t out_features,
+                        bool swiglu, llaisysDataType_t dt, hipStream_t stream);
+
 // out[i] = in[i] for every multi-index i of `shape` (ndim <= 8), element strides per layout,
 // elements of esize (1, 2, 4 or 8) bytes.
 void rearrange(void *out, const void *in, size_t ndim, const size_t *shape, const ptrdiff_t *in_strides,

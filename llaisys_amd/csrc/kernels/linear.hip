@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(NWW * NWX * 64)
     __shared__ __align__(16) char lds[2][(BW + BX) * kTPitch];
     const int tid = int(threadIdx.x);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int lane = tid % kWave, r16 = lane % 16, g4 = lane / 16;
+    const int lane = tid % kWave;
     // Blocks are dispatched to the 8 XCDs round-robin, each XCD with its own L2: give each
     // XCD a contiguous range of weight tiles and walk the activation tiles fastest inside it,
     // so that a weight tile stays in that L2 while every row tile passes over it.

@@ -1,0 +1,246 @@
+// rms_norm (after an optional residual add) fused ahead of a one-row projection, and
+// optionally swiglu after it, for gfx950.
+//
+// Semantics: the composition of the library's own ops, bit for bit --
+//   h  = in + residual, rounded as src/ops/add/cpu/add_cpu.cpp:12 (stored to residual_out),
+//   xn = rms_norm(h) as src/ops/rms_norm/cpu/rms_norm_cpu.cpp:15-33, computed exactly as the
+//        rmsNormRows kernel computes a row (same lane groups, same sums, same rounding),
+//   y  = linear(xn) as src/ops/linear/cpu/linear_cpu.cpp:11-41 (W8A16 with per-channel
+//        scales), each lane summing its chunks lane, lane + 64, lane + 128, ... with the
+//        same FMAs as the one-row linearGemv kernel, then the same butterfly,
+//   out = y, or swiglu(T(gate), T(up)) as src/ops/swiglu/cpu/swiglu_cpu.cpp:15-20 over the
+//        weight rows [0, N) (gate) and [N, 2N) (up).
+// So the fused output equals rmsNorm -> linear -> swiglu launched separately whenever the
+// separate linear takes linearGemv (one or two rows; INT8 weights with N < 4096).
+//
+// Design (HBM-bound on the weights, one launch instead of three): a block of 4 waves; each
+// wave owns one output channel (with swiglu: its gate and up rows).  The waves first
+// request their weight rows' first pass, then the block forms the normalised row in LDS
+// (wave 0 alone for a 64-lane norm group, all 4 waves for a 256-lane one) while those loads
+// are in flight, joins on an LDS-only barrier (the weight loads stay outstanding), and
+// streams the rest of the rows with the activations read from LDS.  Every block re-forms
+// the row from in / residual / weight (L2 hits after the first block); block 0 stores h.
+#include "common.hpp"
+#include "launch.hpp"
+#include "rowplan.hpp"
+
+#include <cmath>
+
+namespace llaisys::kernels {
+
+namespace {
+
+struct NormLinArgs {
+    void *out;
+    void *res_out;
+    const void *in;
+    const void *res; // null: no residual add
+    const void *norm_w;
+    float eps;
+    const void *w;
+    const float *scale; // INT8 only
+    const void *bias;   // null: no bias
+    int N, K;           // outputs (swiglu: gate / up pairs), row length
+};
+
+__device__ __forceinline__ void ldsBarrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <typename T, bool kInt8, int G, int VMAX, bool kSwiglu, int U>
+__global__ void __launch_bounds__(256)
+    linearNormGemv(NormLinArgs a) {
+    using F = Fmt<T>;
+    constexpr int NV = F::kVec;
+    constexpr int E = kInt8 ? 16 : 8;  // weight elements per 16-byte chunk
+    constexpr int R = kSwiglu ? 2 : 1; // weight rows per wave; U: chunks per lane and row per pass
+    static_assert(G == kWave || G == 256, "norm group: one wave or the whole block");
+    extern __shared__ __align__(16) char xs[]; // the normalised row, K elements of T
+    __shared__ float red[256 / kWave];
+    const int lane = int(threadIdx.x) % kWave;
+    const int n = int(blockIdx.x) * 4 + int(threadIdx.x) / kWave; // wave-uniform
+    const bool live = n < a.N; // a wave past the last channel loads a valid row, stores nothing
+    const int nc = a.K / E;    // K % E == 0
+    const size_t rowB = size_t(a.K) * (kInt8 ? 1 : 2);
+    const char *wrow[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+        wrow[r] = static_cast<const char *>(a.w) + (size_t(live ? n : a.N - 1) + size_t(r) * a.N) * rowB;
+    // The first pass's weight chunks are requested before the norm, so that their latency
+    // overlaps it (a chunk past the row end reads chunk 0 and is skipped below).
+    v4u wv[R][U];
+    const auto loadPass = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + kWave * u < nc ? c0 + kWave * u : 0;
+#pragma unroll
+            for (int r = 0; r < R; ++r) wv[r][u] = *reinterpret_cast<const v4u *>(wrow[r] + size_t(c) * 16);
+        }
+    };
+    loadPass(lane);
+
+    if (G == 256 || threadIdx.x < G) {
+        const int gl = int(threadIdx.x) % G;
+        const int nvec = a.K / NV;
+        const bool res = a.res != nullptr;
+        v4u raw[VMAX], rv[VMAX], nwv[VMAX];
+#pragma unroll
+        for (int v = 0; v < VMAX; ++v) {
+            const int vi = gl + v * G;
+            if (vi < nvec) {
+                raw[v] = load16<T>(a.in, size_t(vi) * NV);
+                if (res) rv[v] = load16<T>(a.res, size_t(vi) * NV);
+                nwv[v] = load16<T>(a.norm_w, size_t(vi) * NV);
+            }
+        }
+        if (res) {
+#pragma unroll
+            for (int v = 0; v < VMAX; ++v) {
+                const int vi = gl + v * G;
+                if (vi < nvec) {
+                    float x[NV], r[NV];
+                    F::unpack(raw[v], x);
+                    F::unpack(rv[v], r);
+#pragma unroll
+                    for (int e = 0; e < NV; ++e) x[e] = x[e] + r[e];
+                    raw[v] = F::packQ(x); // h = T(x + r), the value the reference's add stores
+                    if (blockIdx.x == 0) store16<T>(a.res_out, size_t(vi) * NV, raw[v]);
+                }
+            }
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int v = 0; v < VMAX; ++v) {
+            if (gl + v * G < nvec) {
+                float x[NV];
+                F::unpack(raw[v], x);
+#pragma unroll
+                for (int e = 0; e < NV; ++e) ss = fmaf(x[e], x[e], ss);
+            }
+        }
+        ss = groupReduce<G, SumOp>(ss, red);
+        const float rms = sqrtf(ss / float(a.K) + a.eps);
+        const float inv = 1.0f / rms;
+#pragma unroll
+        for (int v = 0; v < VMAX; ++v) {
+            const int vi = gl + v * G;
+            if (vi < nvec) {
+                float x[NV], w[NV], y[NV];
+                F::unpack(raw[v], x);
+                F::unpack(nwv[v], w);
+#pragma unroll
+                for (int e = 0; e < NV; ++e) y[e] = x[e] * w[e] * inv;
+                *reinterpret_cast<v4u *>(xs + size_t(vi) * 16) = F::packQ(y);
+            }
+        }
+    }
+    // the row in LDS is complete (LDS-only barrier: the weight loads stay in flight)
+    ldsBarrier();
+    if (!live) return;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    for (int c0 = lane;;) {
+        v4u xv[U][E / 8];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + kWave * u < nc ? c0 + kWave * u : 0;
+#pragma unroll
+            for (int h = 0; h < E / 8; ++h) xv[u][h] = *reinterpret_cast<const v4u *>(xs + (size_t(c) * E + 8 * h) * 2);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (c0 + kWave * u >= nc) continue;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float wf[E];
+                if constexpr (kInt8) {
+                    const uint32_t ww[4] = {wv[r][u].x, wv[r][u].y, wv[r][u].z, wv[r][u].w};
+#pragma unroll
+                    for (int e = 0; e < E; ++e) wf[e] = float(int8_t(ww[e / 4] >> (8 * (e % 4))));
+                } else {
+                    F::unpack(wv[r][u], wf);
+                }
+#pragma unroll
+                for (int h = 0; h < E / 8; ++h) {
+                    float xf[8];
+                    F::unpack(xv[u][h], xf);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[r] = __builtin_fmaf(xf[e], wf[8 * h + e], acc[r]);
+                }
+            }
+        }
+        c0 += kWave * U;
+        if (c0 >= nc) break;
+        loadPass(c0);
+    }
+    float y[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int ch = n + r * a.N;
+        float s = waveGroupReduce<kWave, SumOp>(acc[r]);
+        if constexpr (kInt8) s = a.scale[ch] * s;
+        if (a.bias) s = s + F::get(a.bias, ch);
+        y[r] = s;
+    }
+    if (lane == 0) {
+        if constexpr (kSwiglu)
+            F::put(a.out, n, SwigluOp::apply(F::round(y[0]), F::round(y[1])));
+        else
+            F::put(a.out, n, y[0]);
+    }
+}
+
+template <typename T, bool kInt8, bool kSwiglu, int U>
+void launchU(const NormLinArgs &a, const RowPlan &plan, hipStream_t s) {
+    const unsigned blocks = unsigned((a.N + 3) / 4);
+    const size_t lds = size_t(a.K) * 2;
+    if (plan.group == kWave)
+        linearNormGemv<T, kInt8, kWave, 4, kSwiglu, U><<<blocks, 256, lds, s>>>(a);
+    else if (plan.vmax == 4)
+        linearNormGemv<T, kInt8, 256, 4, kSwiglu, U><<<blocks, 256, lds, s>>>(a);
+    else
+        linearNormGemv<T, kInt8, 256, 8, kSwiglu, U><<<blocks, 256, lds, s>>>(a);
+}
+
+// Chunks per lane and pass: a row of at most 128 chunks (INT8 K <= 2048, 16-bit K <= 1024)
+// in one pass of 2, else passes of 4 (the chunk order per lane is the same either way).
+template <typename T, bool kInt8, bool kSwiglu>
+void launchNorm(const NormLinArgs &a, const RowPlan &plan, hipStream_t s) {
+    if (a.K / (kInt8 ? 16 : 8) <= 2 * kWave)
+        launchU<T, kInt8, kSwiglu, 2>(a, plan, s);
+    else
+        launchU<T, kInt8, kSwiglu, 4>(a, plan, s);
+}
+
+template <typename T>
+void dispatch(const NormLinArgs &a, const RowPlan &plan, bool int8, bool swiglu, hipStream_t s) {
+    if (int8)
+        swiglu ? launchNorm<T, true, true>(a, plan, s) : launchNorm<T, true, false>(a, plan, s);
+    else
+        swiglu ? launchNorm<T, false, true>(a, plan, s) : launchNorm<T, false, false>(a, plan, s);
+}
+
+} // namespace
+
+bool rmsNormLinearFused(void *out, void *residual_out, const void *in, const void *residual,
+                        const void *norm_weight, float eps, const void *w, const float *w_scale,
+                        const void *bias, size_t rows, size_t in_features, size_t out_features,
+                        bool swiglu, llaisysDataType_t dt, hipStream_t s) {
+    if (rows != 1 || (dt != LLAISYS_DTYPE_BF16 && dt != LLAISYS_DTYPE_F16) || std::isnan(eps)) return false;
+    const size_t K = in_features, E = w_scale ? 16 : 8;
+    // the normalised row lives in LDS: K * 2 bytes, at most 64 KB
+    if (K == 0 || K % E != 0 || K > 32768 || out_features == 0 || out_features >= (size_t(1) << 30)) return false;
+    if (!aligned16(in) || !aligned16(w) || !aligned16(norm_weight) ||
+        (residual && (!aligned16(residual) || !aligned16(residual_out))))
+        return false;
+    const RowPlan plan = planRow(K / 8);
+    if (plan.group != kWave && plan.group != 256) return false;
+    const NormLinArgs a{out, residual_out, in, residual, norm_weight, eps, w, w_scale, bias,
+                        int(out_features), int(K)};
+    if (dt == LLAISYS_DTYPE_BF16)
+        dispatch<BF16>(a, plan, w_scale != nullptr, swiglu, s);
+    else
+        dispatch<F16>(a, plan, w_scale != nullptr, swiglu, s);
+    return true;
+}
+
+} // namespace llaisys::kernels

@@ -491,6 +491,107 @@ void linearW8A16(tensor_t out, tensor_t in, tensor_t w_codes, tensor_t w_scale, 
     launched("linearW8A16");
 }
 
+namespace {
+// Byte ranges of two contiguous tensors intersect.
+bool overlaps(const tensor_t &a, const tensor_t &b) {
+    const std::byte *a0 = a->data(), *b0 = b->data();
+    return a0 < b0 + b->numel() * b->elementSize() && b0 < a0 + a->numel() * a->elementSize();
+}
+} // namespace
+
+// rms_norm (after an optional residual add) fused ahead of a linear, and optionally swiglu
+// after it: the decoder's input_layernorm -> q/k/v projections and add ->
+// post_attention_layernorm -> gate / up projections -> swiglu (reference
+// src/models/qwen2/layer.hpp:51-53, :66-71, src/models/qwen2/mlp.hpp:22-33) as one launch
+// for one row.  weight is [Nw, K] (INT8 codes with weight_scale, else the activation type);
+// with swiglu its rows [0, Nw/2) are the gate and [Nw/2, Nw) the up projection and out is
+// [rows, Nw/2].  Other row counts and shapes run the same ops one after another.
+void rmsNormLinear(tensor_t out, tensor_t residual_out, tensor_t in, tensor_t residual,
+                   tensor_t norm_weight, float eps, tensor_t weight, tensor_t weight_scale,
+                   tensor_t bias, bool swiglu) {
+    const bool has_res = residual != nullptr, has_bias = bias != nullptr && bias->numel() > 0;
+    const bool int8 = weight_scale != nullptr;
+    CHECK_SAME_DEVICE(out, in, norm_weight, weight);
+    ASSERT(has_res == (residual_out != nullptr),
+           "RmsNormLinear: residual and residual_out come together");
+    if (has_res) CHECK_SAME_DEVICE(out, residual, residual_out);
+    if (int8) CHECK_SAME_DEVICE(out, weight_scale);
+    if (has_bias) CHECK_SAME_DEVICE(out, bias);
+    CHECK_SAME_DTYPE(out->dtype(), in->dtype(), norm_weight->dtype());
+    if (has_res) CHECK_SAME_DTYPE(out->dtype(), residual->dtype(), residual_out->dtype());
+    if (has_bias) CHECK_SAME_DTYPE(out->dtype(), bias->dtype());
+    requireFloat(in->dtype());
+    for (const auto &t : {out, in, norm_weight, weight})
+        ASSERT(t->isContiguous(), "RmsNormLinear: tensors must be contiguous");
+    const size_t K = lastDim(in);
+    ASSERT(K > 0, "RmsNormLinear: empty rows");
+    const size_t rows = in->numel() / K;
+    ASSERT(norm_weight->ndim() == 1, "RMSNorm weight must be 1D");
+    ASSERT(norm_weight->shape()[0] == K, "RMSNorm weight shape mismatch");
+    if (has_res) {
+        ASSERT(residual->isContiguous() && residual_out->isContiguous(),
+               "RmsNormLinear: tensors must be contiguous");
+        CHECK_SAME_SHAPE(in->shape(), residual->shape(), residual_out->shape());
+        ASSERT(!overlaps(residual_out, in) && !overlaps(residual_out, residual),
+               "RmsNormLinear: residual_out must not overlap in or residual");
+    }
+    ASSERT(weight->ndim() == 2, "Linear: weight must be 2D");
+    ASSERT(weight->shape()[1] == K, "Linear: input feature dim mismatch");
+    const size_t Nw = weight->shape()[0];
+    ASSERT(Nw > 0, "Linear: empty weight");
+    if (int8) {
+        ASSERT(weight->dtype() == LLAISYS_DTYPE_I8, "LinearW8A16: weight codes must be INT8");
+        ASSERT(weight_scale->dtype() == LLAISYS_DTYPE_F32, "LinearW8A16: weight scales must be F32");
+        ASSERT(weight_scale->isContiguous() && weight_scale->numel() == Nw,
+               "LinearW8A16: one contiguous scale per output feature");
+    } else {
+        CHECK_SAME_DTYPE(out->dtype(), weight->dtype());
+    }
+    if (swiglu) ASSERT(Nw % 2 == 0, "RmsNormLinear: swiglu needs an even number of weight rows");
+    const size_t N = swiglu ? Nw / 2 : Nw;
+    ASSERT(lastDim(out) == N, "Linear: output feature dim mismatch");
+    ASSERT(out->numel() / N == rows, "Linear: input/output rows mismatch");
+    if (has_bias) {
+        ASSERT(bias->numel() == Nw, "Linear: bias shape mismatch");
+        ASSERT(bias->isContiguous(), "Linear bias must be contiguous");
+    }
+    ASSERT(!overlaps(out, in) && !(has_res && (overlaps(out, residual) || overlaps(out, residual_out))),
+           "RmsNormLinear: out must not overlap in, residual or residual_out");
+    ASSERT(rows < (size_t(1) << 31) && K < (size_t(1) << 31) && Nw < (size_t(1) << 31),
+           "Linear: dimensions must be below 2^31");
+    if (rows == 0) return;
+    auto s = streamFor(in);
+    const auto *sc = int8 ? reinterpret_cast<const float *>(weight_scale->data()) : nullptr;
+    const void *bp = has_bias ? bias->data() : nullptr;
+    void *ro = has_res ? residual_out->data() : nullptr;
+    const void *ri = has_res ? residual->data() : nullptr;
+    if (kernels::rmsNormLinearFused(out->data(), ro, in->data(), ri, norm_weight->data(), eps,
+                                    weight->data(), sc, bp, rows, K, N, swiglu, in->dtype(), s)) {
+        launched("rmsNormLinear");
+        return;
+    }
+    // The same ops one after another through library scratch: xn [rows, K], then (swiglu)
+    // gate and up [rows, N] from the two halves of the weight.
+    const size_t es = in->elementSize(), xb = (rows * K * es + 255) / 256 * 256;
+    const size_t gb = swiglu ? (rows * N * es + 255) / 256 * 256 : 0;
+    char *ws = static_cast<char *>(device::amd::workspace(
+                   in->deviceId(), kernels::kScratchReserved + xb + 2 * gb)) +
+               kernels::kScratchReserved;
+    kernels::rmsNorm(ws, ro, in->data(), ri, norm_weight->data(), rows, K, eps, in->dtype(), s);
+    if (!swiglu) {
+        kernels::linear(out->data(), ws, weight->data(), sc, bp, rows, K, N, in->dtype(), s);
+    } else {
+        const size_t wb = N * K * weight->elementSize();
+        char *g = ws + xb, *u = ws + xb + gb;
+        kernels::linear(g, ws, weight->data(), sc, bp, rows, K, N, in->dtype(), s);
+        kernels::linear(u, ws, weight->data() + wb, sc ? sc + N : nullptr,
+                        bp ? static_cast<const char *>(bp) + N * es : nullptr, rows, K, N,
+                        in->dtype(), s);
+        kernels::swiglu(out->data(), g, u, rows * N, in->dtype(), s);
+    }
+    launched("rmsNormLinear (composed)");
+}
+
 } // namespace llaisys::ops
 
 namespace llaisys::ops {

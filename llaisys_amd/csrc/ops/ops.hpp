@@ -31,6 +31,9 @@ void rearrange(tensor_t out, tensor_t in);
 void randomSample(tensor_t out_idx, tensor_t logits, float temperature, int64_t top_k,
                   float top_p, uint64_t seed);
 void linearW8A16(tensor_t out, tensor_t in, tensor_t w_codes, tensor_t w_scale, tensor_t bias);
+void rmsNormLinear(tensor_t out, tensor_t residual_out, tensor_t in, tensor_t residual,
+                   tensor_t norm_weight, float eps, tensor_t weight, tensor_t weight_scale,
+                   tensor_t bias, bool swiglu);
 void ropeKvAppendInt8(tensor_t q_out, tensor_t q_in, tensor_t k_in, tensor_t v_in,
                       tensor_t pos_ids, float theta, tensor_t k_cache, tensor_t k_scale,
                       tensor_t v_cache, tensor_t v_scale, size_t pos);

@@ -4,7 +4,7 @@ The nine reference entry points have the argtypes of the reference's
 python/llaisys/libllaisys/ops.py:4-36; the additive ones are bound when present, so the
 same loader also binds the reference library (used to write golden vectors).
 """
-from ctypes import c_float, c_int64, c_size_t, c_uint64
+from ctypes import c_float, c_int64, c_size_t, c_uint8, c_uint64
 
 from .tensor import llaisysTensor_t
 
@@ -35,6 +35,7 @@ ADDED_OPS = {
     "llaisysSelfAttentionInt8KV": [T, T, T, T, T, T, c_float],
     "llaisysLinearW8A16": [T, T, T, T, T],
     "llaisysRandomSample": [T, T, c_float, c_int64, c_float, c_uint64],
+    "llaisysRmsNormLinear": [T, T, T, T, T, c_float, T, T, T, c_uint8],
 }
 
 

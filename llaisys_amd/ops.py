@@ -4,7 +4,7 @@ The nine reference methods match python/llaisys/ops.py:6-55 (rearrange raises in
 library, as the reference's own C++ rearrange does); the rest wrap the additive entry points of
 include/llaisys/ops.h.
 """
-from ctypes import c_float, c_int64, c_size_t, c_uint64
+from ctypes import c_float, c_int64, c_size_t, c_uint8, c_uint64
 
 from .libllaisys import LIB_LLAISYS
 from .tensor import Tensor
@@ -120,6 +120,18 @@ class Ops:
         LIB_LLAISYS.llaisysLinearW8A16(out.lib_tensor(), inp.lib_tensor(), w_codes.lib_tensor(),
                                        w_scale.lib_tensor(),
                                        None if bias is None else bias.lib_tensor())
+
+    @staticmethod
+    def rms_norm_linear(out: Tensor, inp: Tensor, norm_weight: Tensor, eps: float, weight: Tensor,
+                        weight_scale: Tensor = None, bias: Tensor = None, residual: Tensor = None,
+                        residual_out: Tensor = None, swiglu: bool = False):
+        """out = linear(rms_norm(inp [+ residual])) [then swiglu over the weight's two halves];
+        residual_out receives inp + residual."""
+        opt = lambda t: None if t is None else t.lib_tensor()
+        LIB_LLAISYS.llaisysRmsNormLinear(out.lib_tensor(), opt(residual_out), inp.lib_tensor(),
+                                         opt(residual), norm_weight.lib_tensor(), c_float(eps),
+                                         weight.lib_tensor(), opt(weight_scale), opt(bias),
+                                         c_uint8(1 if swiglu else 0))
 
     @staticmethod
     def random_sample(out_idx: Tensor, logits: Tensor, temperature: float, top_k: int, top_p: float,

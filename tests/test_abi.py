@@ -169,6 +169,13 @@ def _run(code):
     ("L.Ops.linear(t((2,3)), t((2,2)), t((2,2)), t((2,)))", "Linear: output feature dim mismatch"),
     ("L.Ops.linear(t((2,2)), t((2,2)), t((2,2)))", "Unsupported device"),
     ("L.Ops.linear_w8a16(t((2,2)), t((2,2)), t((2,2)), t((2,)))", "weight codes must be INT8"),
+    ("L.Ops.rms_norm_linear(t((1,4)), t((1,8)), t((8,)), 1e-6, t((4,8)))", "Unsupported device"),
+    ("L.Ops.rms_norm_linear(t((1,3)), t((1,8)), t((8,)), 1e-6, t((7,8)), swiglu=True)", "swiglu needs an even number"),
+    ("L.Ops.rms_norm_linear(t((1,4)), t((1,8)), t((8,)), 1e-6, t((8,8)), swiglu=False)", "Linear: output feature dim mismatch"),
+    ("L.Ops.rms_norm_linear(t((1,4)), t((1,8)), t((8,)), 1e-6, t((4,8)), residual=t((1,8)))", "residual and residual_out come together"),
+    ("x=t((1,8)); L.Ops.rms_norm_linear(t((1,4)), x, t((8,)), 1e-6, t((4,8)), residual=t((1,8)), residual_out=x)", "residual_out must not overlap"),
+    ("x=t((1,8)); L.Ops.rms_norm_linear(x, x, t((8,)), 1e-6, t((8,8)))", "out must not overlap"),
+    ("L.Ops.rms_norm_linear(t((1,4)), t((1,8)), t((8,)), 1e-6, t((4,8)), weight_scale=t((4,)))", "weight codes must be INT8"),
     ("L.Ops.kv_append_int8(t((4,2,8), L.DataType.I8), t((4,2)), t((3,2,8)), 2)", "append past the cache end"),
     ("L.Ops.quantize_int8(t((4,8), L.DataType.I8), t((3,)), t((4,8)))", "one scale per last-dim row"),
     ("L.Tensor((2,), L.DataType.F32, L.DeviceType.AMD, 0)", "invalid device id"),
