@@ -134,3 +134,26 @@ def test_self_attention_int8kv(dt, shape):
     assert_attention_close(out.numpy(), ref.numpy(), vdq, "int8 vs dequantize + attend")
     exp = oracle.self_attention_int8kv(q, kq, ks, vq, vs, scale)
     assert_attention_close(out.numpy(), exp, vdq, f"int8 {dt} {shape}")
+
+
+def test_split_decode_across_calls():
+    """Split decode launches of different chunk counts, queries and GQA groups back to back:
+    each call's partials (library scratch) must be merged into its own output only."""
+    rng = np.random.default_rng(41)
+    for total, nh, nkvh, seq in ((4097, 12, 2, 1), (300, 12, 2, 1), (9000, 32, 8, 2), (4097, 12, 2, 1),
+                                 (2500, 16, 4, 3), (4097, 12, 2, 1)):
+        q = sample(rng, (seq, nh, 128), "bf16")
+        k, v = sample(rng, (total, nkvh, 128), "bf16"), sample(rng, (total, nkvh, 128), "bf16")
+        scale = 1.0 / np.sqrt(128)
+        got = attend(q, k, v, scale, "bf16")
+        assert_attention_close(got, oracle.self_attention(q, k, v, scale), v, f"split decode {total} {nh}/{nkvh} x{seq}")
+
+
+def test_split_decode_at_the_chunk_limit():
+    """A group of 16 q heads over a cache long enough for the maximum of 1024 key chunks."""
+    rng = np.random.default_rng(43)
+    total = 1024 * 128 + 5
+    q = sample(rng, (1, 16, 128), "bf16")
+    k, v = sample(rng, (total, 1, 128), "bf16"), sample(rng, (total, 1, 128), "bf16")
+    got = attend(q, k, v, 0.05, "bf16")
+    assert_attention_close(got, oracle.self_attention(q, k, v, 0.05), v, "1024 chunks, group 16")
