@@ -275,10 +275,14 @@ __global__ void __launch_bounds__(kWave * kWaves)
     }
 }
 
-// Merge of the chunk partials of a split launch: one 1024-thread block per (query, head);
-// thread t takes column t % D of the chunks c = t / D (mod 1024 / D), so the partials are
-// read in a few rounds of independent loads.
+// Merge of the chunk partials of a split launch: one 1024-thread block per (query, head,
+// slab of 32 output columns); thread t takes column t % 32 of the slab for the chunks c =
+// t / 32 (mod 32), so a thread reads at most nchunks / 32 partial values (one round of
+// independent loads for up to 256 chunks) and the (query, head) pairs of a decode launch
+// spread over D / 32 times as many blocks.  Every block of a pair forms the same maximum and
+// sum from the chunks' (m, l).
 constexpr int kCombineThreads = 1024;
+constexpr int kCombineCols = 32; // output columns per block (head_dim is 64 or 128)
 
 template <typename T>
 __global__ void __launch_bounds__(kCombineThreads)
@@ -286,7 +290,9 @@ __global__ void __launch_bounds__(kCombineThreads)
     __shared__ float w[1024];  // per-chunk factor exp(m_c - M), nchunks <= 1024
     __shared__ float red[kCombineThreads];
     __shared__ float wred[kCombineThreads / kWave];
-    const size_t ih = blockIdx.x; // i * nh + h
+    const int slabs = D / kCombineCols;
+    const size_t ih = blockIdx.x / unsigned(slabs); // i * nh + h
+    const int col0 = int(blockIdx.x % unsigned(slabs)) * kCombineCols;
     const float *pp = part + ih * size_t(nchunks) * (D + 2);
     const int t = threadIdx.x;
     const float mc = t < nchunks ? pp[size_t(t) * (D + 2) + D] : -INFINITY;
@@ -296,19 +302,17 @@ __global__ void __launch_bounds__(kCombineThreads)
     if (t < nchunks) w[t] = f;
     const float L = groupReduce<kCombineThreads, SumOp>(t < nchunks ? lc * f : 0.0f, wred);
     __syncthreads();
-    const int parts = kCombineThreads / D;
-    const int e = t % D, pidx = t / D;
+    constexpr int kGroups = kCombineThreads / kCombineCols;
+    const int e = col0 + t % kCombineCols, grp = t / kCombineCols;
     float acc = 0.0f;
-    if (pidx < parts) {
 #pragma unroll 8
-        for (int k = pidx; k < nchunks; k += parts) acc += pp[size_t(k) * (D + 2) + e] * w[k];
-    }
+    for (int k = grp; k < nchunks; k += kGroups) acc += pp[size_t(k) * (D + 2) + e] * w[k];
     red[t] = acc;
     __syncthreads();
-    if (t < D) {
+    if (t < kCombineCols) {
         float O = 0.0f;
-        for (int k = 0; k < parts; ++k) O += red[k * D + t];
-        Fmt<T>::put(out, ih * D + t, L > 0.0f ? O / L : 0.0f);
+        for (int g = 0; g < kGroups; ++g) O += red[g * kCombineCols + t];
+        Fmt<T>::put(out, ih * D + col0 + t, L > 0.0f ? O / L : 0.0f);
     }
 }
 
@@ -856,7 +860,7 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
             const unsigned blocks = unsigned(a.seq * size_t(a.nkvh) * nchunks);
             attnDecodeMfma<kInt8><<<blocks, kWave * kDecWaves, 0, s>>>(a);
             if (nchunks > 1)
-                attnCombine<T><<<unsigned(pairs), kCombineThreads, 0, s>>>(a.out, a.part, a.nchunks, d);
+                attnCombine<T><<<unsigned(pairs) * unsigned(d / kCombineCols), kCombineThreads, 0, s>>>(a.out, a.part, a.nchunks, d);
             return;
         }
     }
@@ -882,7 +886,7 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
     else
         launchD<T, kInt8, 128>(a, G, blocks, s);
     if (nchunks > 1)
-        attnCombine<T><<<unsigned(a.seq * size_t(a.nh)), kCombineThreads, 0, s>>>(a.out, a.part, a.nchunks, d);
+        attnCombine<T><<<unsigned(a.seq * size_t(a.nh)) * unsigned(d / kCombineCols), kCombineThreads, 0, s>>>(a.out, a.part, a.nchunks, d);
 }
 
 template <bool kInt8>
