@@ -8,14 +8,24 @@
 // the sum differs from the reference's left-to-right loop, which the tests bound by the f32
 // accumulation error.
 //
-// Design (MFMA-bound for prefill-sized M): v_mfma_f32_16x16x32_{bf16,f16} with both
-// operands read straight from their rows -- A is 16 rows of x with 8 consecutive k per lane,
-// B is 16 rows of w (out-channel major, k contiguous) with 8 consecutive k per lane, which
-// is exactly the MFMA's B layout -- so no transpose and no LDS.  A wave owns a 64 x 64 output
-// tile (16 accumulators), a block of 4 waves 128 x 128; the loads of K step s + 1 are issued
-// before the 16 MFMAs of step s.  INT8 codes enter B as exact bf16 / f16 values and the
-// per-channel scale multiplies the f32 sum once.  Other shapes / types: one thread per
-// output, the reference's sequential sum.
+// Design, by row count M (the launcher at the end picks the kernel):
+//  - M <= 2 (decode), linearGemv: HBM-bound on the weights, one wave per output channel
+//    streaming its weight row in 1 KB load instructions, f32 FMAs, a butterfly; no LDS.
+//    INT8 weights with N >= 4096 go to linearSkinny instead.
+//  - M <= 16, linearSkinny: HBM-bound; a block owns 16 channels, its waves split K, load
+//    weight rows row-contiguously and transpose them through a per-wave LDS tile into
+//    v_mfma_f32_16x16x32 operands; partials summed in LDS in wave order.
+//  - more rows (prefill): MFMA-bound, v_mfma_f32_32x32x16 on 128 x 128 output tiles of 8
+//    waves computing out^T = w x^T (each lane ends with 4 consecutive channels of one row).
+//    linearDirect (16-bit weights, K % 64 == 0) moves the operands HBM -> LDS with
+//    global_load_lds_dwordx4 through 3 stages and XOR-swizzled rows; linearTiled (INT8
+//    weights or other K) stages them through registers and a padded LDS tile, converting
+//    INT8 codes to exact bf16 / f16 on the way.  Blocks map to the 8 XCDs so that a weight
+//    tile stays in one L2 while the row tiles pass over it.
+//  - anything else (f32, unaligned rows, K not a multiple of 8 / 16): linearScalar, one
+//    thread per output with the reference's sequential sum.
+// INT8 codes enter every MFMA as exact bf16 / f16 values and the per-channel scale multiplies
+// the f32 sum once.
 #include "common.hpp"
 #include "launch.hpp"
 #include "rowplan.hpp"
@@ -77,7 +87,7 @@ __device__ __forceinline__ v4u codesToT(const v2u &c) {
     return v4u{w[0], w[1], w[2], w[3]};
 }
 
-// Many rows (prefill): MFMA-bound.  A block of 4 waves owns BW output channels x BX rows;
+// Many rows (prefill): MFMA-bound.  A block of NWW x NWX waves owns BW output channels x BX rows;
 // per stage of 64 k it stages both tiles in LDS (row-contiguous global loads, 144-byte row
 // pitch: the MFMA-operand reads and the tile writes are bank-conflict-free), double-buffered
 // with the next stage's global loads in flight during the MFMAs.  The MFMA computes
