@@ -14,15 +14,21 @@
 // exp through the hardware exp2, and (sum p v) / (sum p) instead of sum (p / sum) v.  The
 // tests bound the difference by the f32 accumulation error of the reference itself.
 //
-// Design (HBM-bound for decode, VALU-bound for long prefill): one wavefront per q head; the
-// waves of a block are q heads of one kv head, so they read the same K / V rows (the
-// later waves hit the lines the first brought in).  A key row of D elements is spread over
-// R = D / 8 lanes, 8 elements per lane (one 16-byte load for bf16 / f16, 8 bytes of codes
-// for INT8), so one load instruction covers 64 / R keys.  Per batch of U instructions the
-// wave forms its scores (8 FMAs, a butterfly over R lanes), updates the running max once,
-// and folds p * v into per-lane accumulators.  Long key ranges with few (query, head) pairs
-// (decode) are cut into chunks whose partial (max, sum, output) a second kernel merges.
-// No MFMA here: a decode step is a matrix-vector product per head.
+// Design, three kernels (the launcher at the end picks one):
+//  - attnMfma (bf16, head_dim 128, >= 16 queries: prefill): MFMA-bound; 16 queries x one kv
+//    head's q heads per block, S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16
+//    with K / V tiles staged through LDS one tile ahead.
+//  - attnDecodeMfma (bf16 q, head_dim 128, fewer queries: decode, cache in bf16 or INT8):
+//    HBM-bound; the key range is cut into chunks, one block per (query, kv head, chunk) with
+//    the kv head's q heads as the MFMA columns; attnCombine merges the chunk partials.
+//  - attnGroup (other dtypes, head_dim 64): one wavefront per q head, the waves of a block
+//    being q heads of one kv head (they read the same K / V rows).  A key row of D elements
+//    is spread over R = D / 8 lanes, 8 elements per lane, so one load instruction covers
+//    64 / R keys; per batch of U instructions the wave forms its scores (8 FMAs, a butterfly
+//    over R lanes), updates the running max once and folds p * v into per-lane
+//    accumulators.  Long key ranges with few (query, head) pairs are split and merged by
+//    attnCombine as well.
+//  - attnScalar: any other head_dim / v_head_dim, one wave per (query, head).
 #include "common.hpp"
 #include "launch.hpp"
 #include "rowplan.hpp"
