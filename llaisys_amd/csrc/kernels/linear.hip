@@ -28,6 +28,7 @@
 // the f32 sum once.
 #include "common.hpp"
 #include "launch.hpp"
+#include "linear_common.hpp"
 #include "rowplan.hpp"
 
 #include <algorithm>
@@ -37,11 +38,8 @@ namespace llaisys::kernels {
 
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+using namespace lin;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 
 struct LinearArgs {
     void *out;
@@ -52,14 +50,6 @@ struct LinearArgs {
     int M, N, K;
 };
 
-template <typename T>
-__device__ __forceinline__ f32x4 mfma(const v4u &a, const v4u &b, f32x4 c) {
-    if constexpr (std::is_same_v<T, BF16>)
-        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-    else
-        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
 // 32 x 32 x 16: A[m = l % 32][k = 8 (l / 32) + j], B[k = 8 (l / 32) + j][n = l % 32],
 // D[m = 8 (i / 4) + 4 (l / 32) + i % 4][n = l % 32]; twice the sustained rate of 16 x 16 x 32
 template <typename T>
@@ -68,23 +58,6 @@ __device__ __forceinline__ f32x16 mfma32(const v4u &a, const v4u &b, const f32x1
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
     else
         return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-}
-
-// 8 INT8 codes as 8 elements of T (exact: |code| <= 127 fits both 8- and 11-bit mantissas)
-template <typename T>
-__device__ __forceinline__ v4u codesToT(const v2u &c) {
-    uint32_t w[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint32_t src = e < 2 ? c.x : c.y;
-        const int sh = 16 * (e % 2);
-        const float lo = float(int8_t(src >> sh)), hi = float(int8_t(src >> (sh + 8)));
-        if constexpr (std::is_same_v<T, BF16>)
-            w[e] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xFFFF0000u); // exact: 8-bit values
-        else
-            w[e] = f32ToF16(lo) | (f32ToF16(hi) << 16);
-    }
-    return v4u{w[0], w[1], w[2], w[3]};
 }
 
 // Many rows (prefill): MFMA-bound.  A block of NWW x NWX waves owns BW output channels x BX rows;
@@ -352,93 +325,34 @@ __global__ void __launch_bounds__(NWW * NWX * 64)
     storeTiles<T, false, TW, TX>(a, acc, w0 + ww0, x0 + wx0, lane);
 }
 
-// Few rows (M <= 16, decode): HBM-bound on the weights.  A block owns 16 output channels
-// and its waves split K into groups of 128 k.  A load instruction that hands MFMA operands
-// straight to registers touches 16 weight rows (lane l holds row l % 16), which streams
-// HBM measurably slower than touching 4 rows with 256 contiguous bytes each; so each wave
-// loads its group row-contiguously, transposes it through its own padded LDS tile
-// (conflict-free on both sides) and reads the MFMA operand from there.  x rows >= M enter
-// as zeros.  The waves' 16 x 16 partials are summed in LDS in wave order.
-//
-// k order inside a group (A and B agree, so the MFMA sum covers every k once):
-//   16-bit weights: step s, lane (r, g) holds k = 32 s + 8 g + [0, 8)
-//   INT8 weights:   step s, lane (r, g) holds k = 64 (s / 2) + 16 g + 8 (s % 2) + [0, 8)
-// (an INT8 lane reads 16 codes, two steps' worth, in one LDS read).
-constexpr int kSkK = 128; // k per group
-constexpr int skinnyPitch(bool int8) { return (int8 ? kSkK : 2 * kSkK) + 16; }
-
+// Few rows (M <= 16, decode): HBM-bound on the weights; the skinny MFMA loop of
+// linear_common.hpp over one set of 16 channels, x rows >= M entering as zeros.  The waves'
+// 16 x 16 partials are summed in LDS in wave order.
 template <typename T, bool kInt8>
 __global__ void __launch_bounds__(1024)
     linearSkinny(LinearArgs a) {
-    constexpr int kRowB = kInt8 ? kSkK : 2 * kSkK;  // bytes of one weight row in a group
-    constexpr int kPitch = skinnyPitch(kInt8);       // LDS row pitch: rows shift by 4 banks
-    constexpr int kLanesPerRow = kRowB / 16;         // lanes covering a row in one load
-    constexpr int kRowsPerLoad = kWave / kLanesPerRow;
-    constexpr int kLoads = 16 / kRowsPerLoad;        // loads per group: 4 (16-bit) / 2 (INT8)
-    constexpr int kElemB = kInt8 ? 1 : 2;
     // dynamic LDS, sized by the launch: nw transpose tiles, then nw partial tiles
     extern __shared__ __align__(16) char smem[];
     const int nw = int(blockDim.x) / kWave;
-    char(*stage)[16 * kPitch] = reinterpret_cast<char(*)[16 * kPitch]>(smem);
-    float(*red)[256] = reinterpret_cast<float(*)[256]>(smem + nw * 16 * kPitch);
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
     const int r16 = lane % 16, g4 = lane / 16;
     const int n0 = int(blockIdx.x) * 16;
-    const int ng = (a.K + kSkK - 1) / kSkK;
-    char *tile = stage[wave];
-    // row-contiguous load: instruction j, lane l -> row j * kRowsPerLoad + l / kLanesPerRow,
-    // 16 bytes at column (l % kLanesPerRow)
-    const int lrow = lane / kLanesPerRow, lcol = lane % kLanesPerRow;
-    const char *wbase = static_cast<const char *>(a.w);
+    char *tile = smem + size_t(wave) * 16 * skinnyPitch(kInt8);
+    float(*red)[256] = reinterpret_cast<float(*)[256]>(smem + nw * 16 * skinnyPitch(kInt8));
     const char *xrow = static_cast<const char *>(a.x) + size_t(min(r16, a.M - 1)) * a.K * 2;
     const bool xlane = r16 < a.M;
     const v4u z4 = {0u, 0u, 0u, 0u};
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int g = wave; g < ng; g += nw) {
-        const int kg = g * kSkK;
-        // weights: all loads of the group first
-        v4u wl[kLoads];
-        const int kw = kg + lcol * (16 / kElemB);
-        const bool win = kw < a.K; // K % (16 / element bytes) == 0: a 16-byte chunk is all in or out
-#pragma unroll
-        for (int j = 0; j < kLoads; ++j) {
-            const int row = min(n0 + j * kRowsPerLoad + lrow, a.N - 1);
-            wl[j] = *reinterpret_cast<const v4u *>(wbase + (size_t(row) * a.K + (win ? kw : 0)) * kElemB);
-        }
-        // activations (few rows, cache-resident), in the MFMA's A layout
-        v4u xa[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int k = kg + (kInt8 ? 64 * (s / 2) + 16 * g4 + 8 * (s % 2) : 32 * s + 8 * g4);
-            xa[s] = *reinterpret_cast<const v4u *>(xrow + size_t(k < a.K ? k : 0) * 2);
-            if (!(xlane && k < a.K)) xa[s] = z4;
-        }
-#pragma unroll
-        for (int j = 0; j < kLoads; ++j)
-            *reinterpret_cast<v4u *>(tile + (j * kRowsPerLoad + lrow) * kPitch + 16 * lcol) = win ? wl[j] : z4;
-        // same wave writes and reads its tile: LDS executes a wave's accesses in order
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if constexpr (kInt8) {
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const v4u c = *reinterpret_cast<const v4u *>(tile + r16 * kPitch + 64 * h + 16 * g4);
-                acc = mfma<T>(xa[2 * h], codesToT<T>(v2u{c.x, c.y}), acc);
-                acc = mfma<T>(xa[2 * h + 1], codesToT<T>(v2u{c.z, c.w}), acc);
-            }
-        } else {
-#pragma unroll
-            for (int s = 0; s < 4; ++s)
-                acc = mfma<T>(xa[s], *reinterpret_cast<const v4u *>(tile + r16 * kPitch + 64 * s + 16 * g4), acc);
-        }
-        // the next group's writes must not overtake this group's reads
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
+    const auto xop = [&](int k) {
+        const v4u v = *reinterpret_cast<const v4u *>(xrow + size_t(k < a.K ? k : 0) * 2);
+        return xlane && k < a.K ? v : z4;
+    };
+    f32x4 acc[1] = {{0.0f, 0.0f, 0.0f, 0.0f}};
+    const int rows0[1] = {n0};
+    skinnyGroups<T, kInt8, 1>(acc, static_cast<const char *>(a.w), rows0, a.N, a.K, tile, wave, nw, lane, xop);
     // D[m = 4 g + e][n = r16]
 #pragma unroll
-    for (int e = 0; e < 4; ++e) red[wave][(4 * g4 + e) * 16 + r16] = acc[e];
+    for (int e = 0; e < 4; ++e) red[wave][(4 * g4 + e) * 16 + r16] = acc[0][e];
     __syncthreads();
     for (int t = int(threadIdx.x); t < 16 * a.M; t += int(blockDim.x)) {
         const int m = t / 16, n = n0 + t % 16;
@@ -559,8 +473,7 @@ void launch(const LinearArgs &a, hipStream_t s) {
             if (a.M <= 16) {
                 // waves per block: enough blocks x waves to fill the chip, at most one wave
                 // per group of 128 k
-                const int tiles = (a.N + 15) / 16, ng = (a.K + kSkK - 1) / kSkK;
-                const int nw = std::max(1, std::min({16, ng, std::max(2, 2048 / tiles)}));
+                const int tiles = (a.N + 15) / 16, nw = skinnyWaves(a.N, a.K);
                 const size_t lds = size_t(nw) * (16 * skinnyPitch(kInt8) + 256 * sizeof(float));
                 linearSkinny<T, kInt8><<<unsigned(tiles), unsigned(nw * kWave), lds, s>>>(a);
                 return;

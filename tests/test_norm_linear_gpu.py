@@ -116,6 +116,18 @@ def test_one_row_equals_separate_ops_bit_for_bit(K, dt, int8, swiglu):
     assert_exact(got, want, f"K={K} {dt} int8={int8} swiglu={swiglu}")
 
 
+@pytest.mark.parametrize("swiglu", [False, True], ids=["plain", "swiglu"])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_int8_many_channels_equal_separate_ops_bit_for_bit(dt, swiglu):
+    """INT8 weights over 4096+ channels: the separate linear takes the skinny MFMA kernel
+    and so does the fused one (same K split, same order of the partials)."""
+    c = Case(1, 1536, 4100 if not swiglu else 4104, dt, True, swiglu, bias=True, res=True, seed=11)
+    got, h = c.fused()
+    want, _, h_want = c.composed()
+    assert_exact(h, h_want, "residual")
+    assert_exact(got, want, f"INT8 N={c.N} {dt} swiglu={swiglu}")
+
+
 @pytest.mark.parametrize("res", [False, True], ids=["norm", "add_norm"])
 @pytest.mark.parametrize("bias", [False, True], ids=["nobias", "bias"])
 def test_qwen2_decode_projections_against_oracle(res, bias):
@@ -152,8 +164,7 @@ def test_qwen2_decode_projections_against_oracle(res, bias):
                    + np.abs(silu) * 2.0 ** -7 * np.abs(uf))
             err = np.abs(to_f32(got, "bf16").astype(np.float64) - ref)
             assert np.all(err <= tol), f"N={N} int8={int8}: max err {err.max()}"
-            if not int8:  # the separate INT8 linear takes the multi-row kernel at N >= 4096
-                assert_exact(got, want, f"N={N} swiglu vs separate ops")
+            assert_exact(got, want, f"N={N} int8={int8} swiglu vs separate ops")
 
 
 @pytest.mark.parametrize("rows", [2, 5])
