@@ -182,6 +182,11 @@ __global__ void __launch_bounds__(256)
     char *out1 = static_cast<char *>(tp.out1) + t * size_t(tp.n_heads1) * kRowBytes + v_lane * 16 -
                  size_t(nh0) * kRowBytes;
 
+    // the lane's first frequency before the row loads: the vector memory counter drains in
+    // issue order, so a frequency read issued after them would hold the angle work until all
+    // the rows had landed
+    const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
+    __builtin_amdgcn_sched_barrier(0);
     double c[N], sn[N];
     int pass = 0;
     do {
@@ -197,7 +202,7 @@ __global__ void __launch_bounds__(256)
             bool far = false;
             for (int sl = lane; sl < kHalf; sl += kWave) {
                 const int j = angleOf(sl);
-                const double ang = double(p) * ft.f[j];
+                const double ang = double(p) * (sl == lane ? f_first : ft.f[j]);
                 double s0 = 0.0, c0 = 0.0;
                 if (fabs(ang) <= kSincosFastLimit)
                     sincosReduced(ang, &s0, &c0);
