@@ -192,3 +192,38 @@ def test_ragged_channel_count_and_repeat():
     want, _, _ = c.composed()
     assert_exact(a, b, "repeat")
     assert_exact(a, want, "ragged")
+
+
+def test_graph_replays_of_the_decode_projections_match_eager():
+    """The two fused decode projections (q/k/v with bias and add+norm; gate/up with swiglu,
+    INT8, the skinny form) and the separate attention-output GEMV captured in one HIP graph
+    and replayed three times, with eager work between replays: every replay equals the eager
+    results (outputs cleared before each replay)."""
+    api = L.RuntimeAPI(L.DeviceType.AMD)
+    qkv = Case(1, 1536, 2048, "bf16", True, False, bias=True, res=True, seed=21)
+    gu = Case(1, 1536, 8960, "bf16", True, True, bias=False, res=True, seed=22)
+    outs = {"qkv": empty((1, 2048), "bf16"), "h1": empty((1, 1536), "bf16"),
+            "act": empty((1, 8960), "bf16"), "h2": empty((1, 1536), "bf16")}
+
+    def step():
+        t = qkv.t
+        L.Ops.rms_norm_linear(outs["qkv"], t["x"], t["nw"], EPS, t["w"], t["sc"], t["b"], residual=t["r"],
+                              residual_out=outs["h1"])
+        t = gu.t
+        L.Ops.rms_norm_linear(outs["act"], outs["h1"], t["nw"], EPS, t["w"], t["sc"], residual=t["r"],
+                              residual_out=outs["h2"], swiglu=True)
+
+    step()
+    eager = {k: v.numpy() for k, v in outs.items()}
+    graph = L.Graph.capture()
+    step()
+    graph.end()
+    for _ in range(3):
+        for tt in outs.values():
+            z = np.zeros(tt.shape(), dtype=np.uint16)
+            api.memcpy_sync(tt.data_ptr(), z.ctypes.data, z.nbytes, L.MemcpyKind.H2D)
+        gu.fused()  # unrelated eager work between replays
+        graph.launch()
+        api.device_synchronize()
+        for k, v in outs.items():
+            assert_exact(v.numpy(), eager[k], f"replay {k}")
