@@ -397,17 +397,28 @@ __device__ __forceinline__ bf16x8 asBf16x8(const v4u &r) { return __builtin_bit_
 // MFMA work and a step needs one barrier.  K is stored as loaded (row-major); V is stored
 // transposed from pairs of consecutive keys, one 4-byte write per column and pair (the 32
 // lanes of a pair of rows write 32 consecutive words, the other 32 lanes rows 32 banks on).
-template <int W>
-__global__ void __launch_bounds__(kWave * W)
+// kSplit: the block holds two waves per q head, and the key tiles are cut in two halves that
+// the two wave sets walk in lockstep (one barrier per step for both), each staging its own
+// tiles; at the end the second half's (max, sum, output) is merged into the first's through
+// LDS.  It halves the longest block's chain of tiles -- the causal imbalance that bounds
+// a prefill with about one block per CU.
+template <int W, bool kSplit>
+__global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
     attnMfma(AttnArgs a) {
     constexpr int D = 128, KB = D / 32, DT = D / 16;
+    constexpr int NHALF = kSplit ? 2 : 1;
     constexpr int kKItems = kMfmaKT * (D / 8);           // 16-byte K pieces per tile
     constexpr int kVItems = (kMfmaKT / 2) * (D / 8);     // V pieces: 2 keys x 8 columns
     constexpr int kKPer = (kKItems + kWave * W - 1) / (kWave * W);
     constexpr int kVPer = (kVItems + kWave * W - 1) / (kWave * W);
-    __shared__ uint16_t kt[2][kMfmaKT][kKtLd];
-    __shared__ uint16_t vt[2][D][kVtLd];
-    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    __shared__ uint16_t kt_all[NHALF][2][kMfmaKT][kKtLd];
+    __shared__ uint16_t vt_all[NHALF][2][D][kVtLd];
+    const int wave_all = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int half = kSplit ? wave_all / W : 0;   // key half this wave walks
+    const int wave = wave_all % W;                 // q head of the slice
+    const int ltid = int(threadIdx.x) % (kWave * W); // thread index within the half
+    auto &kt = kt_all[half];
+    auto &vt = vt_all[half];
     const int lane = int(threadIdx.x) % kWave;
     const int n = lane % 16, g4 = lane / 16;
 
@@ -444,7 +455,7 @@ __global__ void __launch_bounds__(kWave * W)
         const size_t left = a.total - t0; // keys of the cache from t0 on (> 0)
 #pragma unroll
         for (int r = 0; r < kKPer; ++r) {
-            const int idx = int(threadIdx.x) + r * kWave * W;
+            const int idx = ltid + r * kWave * W;
             const int kk = idx / (D / 8), col = 8 * (idx % (D / 8));
             kraw[r] = v4u{0u, 0u, 0u, 0u}; // keys past the cache: zeros
             if (idx < kKItems && size_t(kk) < left)
@@ -452,7 +463,7 @@ __global__ void __launch_bounds__(kWave * W)
         }
 #pragma unroll
         for (int r = 0; r < kVPer; ++r) {
-            const int idx = int(threadIdx.x) + r * kWave * W;
+            const int idx = ltid + r * kWave * W;
             const int kp = idx % (kMfmaKT / 2), col = 8 * (idx / (kMfmaKT / 2));
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
@@ -465,13 +476,13 @@ __global__ void __launch_bounds__(kWave * W)
     const auto storeTile = [&](int buf) {
 #pragma unroll
         for (int r = 0; r < kKPer; ++r) {
-            const int idx = int(threadIdx.x) + r * kWave * W;
+            const int idx = ltid + r * kWave * W;
             if (idx < kKItems)
                 *reinterpret_cast<v4u *>(&kt[buf][idx / (D / 8)][8 * (idx % (D / 8))]) = kraw[r];
         }
 #pragma unroll
         for (int r = 0; r < kVPer; ++r) {
-            const int idx = int(threadIdx.x) + r * kWave * W;
+            const int idx = ltid + r * kWave * W;
             if (idx >= kVItems) continue;
             const int kp = idx % (kMfmaKT / 2), col = 8 * (idx / (kMfmaKT / 2));
             const uint32_t w0[4] = {vraw[r][0].x, vraw[r][0].y, vraw[r][0].z, vraw[r][0].w};
@@ -487,13 +498,19 @@ __global__ void __launch_bounds__(kWave * W)
         }
     };
 
-    loadTile(0);
-    for (size_t ti = 0; ti < ntiles; ++ti) {
-        const int buf = int(ti & 1);
+    // this half's tiles: [tbeg, tbeg + tcount); both halves step nsteps times
+    const size_t nsteps = kSplit ? (ntiles + 1) / 2 : ntiles;
+    const size_t tbeg = half ? nsteps : 0;
+    const size_t tcount = half ? ntiles - nsteps : nsteps;
+    if (tcount > 0) loadTile(tbeg * kMfmaKT);
+    for (size_t it = 0; it < nsteps; ++it) {
+        const int buf = int(it & 1);
+        const size_t ti = tbeg + it;
         const size_t kt0 = ti * kMfmaKT;
         storeTile(buf);
-        if (ti + 1 < ntiles) loadTile(kt0 + kMfmaKT); // in flight during this step's math
+        if (it + 1 < tcount) loadTile(kt0 + kMfmaKT); // in flight during this step's math
         __syncthreads(); // tile ti in LDS; every wave is past the step that read buf last
+        if (kSplit && it >= tcount) continue; // the shorter half idles through its last step
         // keys of this lane's query visible in the tile: offsets < nvis
         const int nvis = int(min(vis_q - min(vis_q, kt0), size_t(kMfmaKT)));
         float p[4][4];
@@ -555,6 +572,32 @@ __global__ void __launch_bounds__(kWave * W)
     }
     float lt = lsum + __shfl_xor(lsum, 16, kWave);
     lt += __shfl_xor(lt, 32, kWave);
+    if constexpr (kSplit) {
+        // the second half hands (max, sum, output) to its partner wave through LDS (the
+        // tiles' storage, free once every wave is past its last step)
+        float *xch = reinterpret_cast<float *>(&kt_all[0][0][0][0]) + size_t(wave) * kWave * (2 + 4 * DT);
+        __syncthreads();
+        if (half == 1) {
+            xch[lane] = m;
+            xch[kWave + lane] = lt;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xch[(2 + 4 * dt + i) * kWave + lane] = o[dt][i];
+        }
+        __syncthreads();
+        if (half == 1) return;
+        const float m1 = xch[lane], l1 = xch[kWave + lane];
+        const float M = fmaxf(m, m1);
+        // a half with no visible key has m = -inf: weight 0 (the other half holds key 0)
+        const float f0 = m == M ? 1.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m, c2, -M * c2));
+        const float f1 = m1 == M ? 1.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m1, c2, -M * c2));
+        lt = lt * f0 + l1 * f1;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[dt][i] = o[dt][i] * f0 + xch[(2 + 4 * dt + i) * kWave + lane] * f1;
+    }
     if (q0 + size_t(n) >= a.seq) return;
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     uint16_t *op = static_cast<uint16_t *>(a.out) + (qi * a.nh + h) * D + 4 * g4;
@@ -842,12 +885,23 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
         if (d == 128 && a.total > 0 && a.seq >= size_t(kMfmaQ) && mblocks < (size_t(1) << 31) &&
             a.scale > 0.0f && std::isfinite(a.scale)) {
             a.nchunks = 1;
+            // few blocks per CU: the causal imbalance is not averaged out across blocks, so
+            // the key tiles of each block are split over two wave sets
+            // (groups of 8 keep one wave per head: 16 waves of 8 heads would spill registers)
+            if (mblocks <= 512 && G <= 6) {
+                switch (G) {
+                case 6: attnMfma<6, true><<<unsigned(mblocks), kWave * 12, 0, s>>>(a); return;
+                case 4: attnMfma<4, true><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
+                case 2: attnMfma<2, true><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
+                default: attnMfma<1, true><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
+                }
+            }
             switch (G) {
-            case 8: attnMfma<8><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
-            case 6: attnMfma<6><<<unsigned(mblocks), kWave * 6, 0, s>>>(a); return;
-            case 4: attnMfma<4><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
-            case 2: attnMfma<2><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
-            default: attnMfma<1><<<unsigned(mblocks), kWave, 0, s>>>(a); return;
+            case 8: attnMfma<8, false><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
+            case 6: attnMfma<6, false><<<unsigned(mblocks), kWave * 6, 0, s>>>(a); return;
+            case 4: attnMfma<4, false><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
+            case 2: attnMfma<2, false><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
+            default: attnMfma<1, false><<<unsigned(mblocks), kWave, 0, s>>>(a); return;
             }
         }
     }
