@@ -17,7 +17,8 @@
 // Design, three kernels (the launcher at the end picks one):
 //  - attnMfma (bf16, head_dim 128, >= 16 queries: prefill): MFMA-bound; 16 queries x one kv
 //    head's q heads per block, S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16
-//    with K / V tiles staged through LDS one tile ahead.
+//    with K / V tiles staged through LDS one tile ahead; with few blocks per CU, two wave
+//    sets per block split the key tiles (kSplit).
 //  - attnDecodeMfma (bf16 q, head_dim 128, fewer queries: decode, cache in bf16 or INT8):
 //    HBM-bound; the key range is cut into chunks, one block per (query, kv head, chunk) with
 //    the kv head's q heads as the MFMA columns; attnCombine merges the chunk partials.

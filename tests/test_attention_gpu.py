@@ -46,6 +46,9 @@ SHAPES = [
     # groups of 8, 4 and 1, a single tile
     (200, 1000, 12, 2, 128), (33, 33, 16, 2, 128), (48, 48, 32, 8, 128), (17, 17, 4, 4, 128),
     (16, 16, 12, 2, 128),
+    # more than 512 MFMA blocks: one wave per head (the key tiles of a block unsplit), with
+    # groups of 6 and of 1
+    (300, 300, 168, 28, 128), (600, 600, 16, 16, 128),
 ]
 
 
