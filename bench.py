@@ -514,6 +514,12 @@ def attention_ops(L, rng):
     ops.append(("prefill 2048 tokens causal, 12 q / 2 kv heads, bf16", "flops",
                 4 * nh * d * tp * (tp + 1) // 2,
                 lambda i: O.self_attention(op_, qp, kp, vp, sc)))
+    kpq, kps = P.empty((tp, nkv, d), I8, 1)[0], P.empty((tp, nkv), F32, 1)[0]
+    vpq, vps = P.empty((tp, nkv, d), I8, 1)[0], P.empty((tp, nkv), F32, 1)[0]
+    O.kv_append_int8_pair(kpq, kps, vpq, vps, kp, vp, 0)
+    ops.append(("prefill 2048 tokens causal, 12 q / 2 kv heads, INT8 KV", "flops",
+                4 * nh * d * tp * (tp + 1) // 2,
+                lambda i: O.self_attention_int8kv(op_, qp, kpq, kps, vpq, vps, sc)))
     return ops, P
 
 

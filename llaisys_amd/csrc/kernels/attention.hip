@@ -369,7 +369,35 @@ __global__ void __launch_bounds__(kWave)
     for (int e = lane; e < dv; e += kWave) Fmt<T>::put(a.out, ih * dv + e, acc[e] * inv);
 }
 
-// ---- prefill on MFMA (bf16, head_dim 128) ---------------------------------------------
+// 8 consecutive elements of a cache row (128 per row) as raw bits: bf16 (16 bytes) or INT8
+// codes (8 bytes, in .x / .y).
+template <bool kInt8>
+__device__ __forceinline__ v4u loadRow8(const void *base, size_t row, int col) {
+    if constexpr (kInt8) {
+        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+        const v2u c = *reinterpret_cast<const v2u *>(static_cast<const int8_t *>(base) + row * 128 + col);
+        return v4u{c.x, c.y, 0u, 0u};
+    } else {
+        return *reinterpret_cast<const v4u *>(static_cast<const uint16_t *>(base) + row * 128 + col);
+    }
+}
+
+// 8 INT8 codes -> bf16(code * sc) as 4 packed words.  code = u - 128 for the unsigned byte
+// u of code ^ 0x80, and fma(u, sc, -128 sc) rounds u * sc - 128 sc = code * sc once (-128 sc
+// is exact), i.e. exactly float(code) * sc; the pair conversion then rounds to bf16 as the
+// reference does for every non-NaN value.
+__device__ __forceinline__ v4u codesToBf16(const v4u &raw, float sc) {
+    const uint32_t ux = raw.x ^ 0x80808080u, uy = raw.y ^ 0x80808080u;
+    const float off = -128.0f * sc;
+    const auto cv = [&](uint32_t u, int k) {
+        const float b = float((u >> (8 * k)) & 0xFFu); // v_cvt_f32_ubyte{k}
+        return __builtin_fmaf(b, sc, off);
+    };
+    return v4u{Bf16Cvt::narrow2Q(cv(ux, 0), cv(ux, 1)), Bf16Cvt::narrow2Q(cv(ux, 2), cv(ux, 3)),
+               Bf16Cvt::narrow2Q(cv(uy, 0), cv(uy, 1)), Bf16Cvt::narrow2Q(cv(uy, 2), cv(uy, 3))};
+}
+
+// ---- prefill on MFMA (bf16 q / out, head_dim 128, cache in bf16 or INT8) --------------
 // One block per (16 queries, kv head, slice of W q heads), one wave per q head.  Per tile
 // of 64 keys a wave forms S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A = 16 key rows of
 // the tile, B = the wave's 16 queries kept in registers), so each lane holds the scores of
@@ -403,7 +431,7 @@ __device__ __forceinline__ bf16x8 asBf16x8(const v4u &r) { return __builtin_bit_
 // tiles; at the end the second half's (max, sum, output) is merged into the first's through
 // LDS.  It halves the longest block's chain of tiles -- the causal imbalance that bounds
 // a prefill with about one block per CU.
-template <int W, bool kSplit>
+template <int W, bool kSplit, bool kInt8>
 __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
     attnMfma(AttnArgs a) {
     constexpr int D = 128, KB = D / 32, DT = D / 16;
@@ -435,7 +463,6 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
     const size_t vis_q = visibleKeys(a.total, a.seq, qi);
     const size_t vis_blk = visibleKeys(a.total, a.seq, min(q0 + kMfmaQ - 1, a.seq - 1));
     const size_t ntiles = (vis_blk + kMfmaKT - 1) / kMfmaKT;
-    const size_t kstride = size_t(a.nkvh) * D; // elements between key rows
     const float c2 = a.scale * 1.4426950408889634f; // scores to base-2 exponents
 
     bf16x8 qreg[KB];
@@ -449,9 +476,11 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const uint16_t *kbase = static_cast<const uint16_t *>(a.k) + size_t(g) * D;
-    const uint16_t *vbase = static_cast<const uint16_t *>(a.v) + size_t(g) * D;
+    // cache rows of the kv head: row t at element (t * nkvh + g) * D; INT8 codes with one
+    // scale per (t, g), turned into bf16(code * scale) (codesToBf16) when staged into LDS
+    const size_t rstride = size_t(a.nkvh);
     v4u kraw[kKPer], vraw[kVPer][2];
+    float ksc[kInt8 ? kKPer : 1], vsc[kInt8 ? kVPer : 1][2];
     const auto loadTile = [&](size_t t0) {
         const size_t left = a.total - t0; // keys of the cache from t0 on (> 0)
 #pragma unroll
@@ -459,8 +488,11 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
             const int idx = ltid + r * kWave * W;
             const int kk = idx / (D / 8), col = 8 * (idx % (D / 8));
             kraw[r] = v4u{0u, 0u, 0u, 0u}; // keys past the cache: zeros
-            if (idx < kKItems && size_t(kk) < left)
-                kraw[r] = *reinterpret_cast<const v4u *>(kbase + (t0 + kk) * kstride + col);
+            if constexpr (kInt8) ksc[r] = 0.0f;
+            if (idx < kKItems && size_t(kk) < left) {
+                kraw[r] = loadRow8<kInt8>(a.k, (t0 + kk) * rstride + g, col);
+                if constexpr (kInt8) ksc[r] = a.ks[(t0 + kk) * rstride + g];
+            }
         }
 #pragma unroll
         for (int r = 0; r < kVPer; ++r) {
@@ -469,12 +501,23 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 vraw[r][e] = v4u{0u, 0u, 0u, 0u};
-                if (idx < kVItems && size_t(2 * kp + e) < left)
-                    vraw[r][e] = *reinterpret_cast<const v4u *>(vbase + (t0 + 2 * kp + e) * kstride + col);
+                if constexpr (kInt8) vsc[r][e] = 0.0f;
+                if (idx < kVItems && size_t(2 * kp + e) < left) {
+                    vraw[r][e] = loadRow8<kInt8>(a.v, (t0 + 2 * kp + e) * rstride + g, col);
+                    if constexpr (kInt8) vsc[r][e] = a.vs[(t0 + 2 * kp + e) * rstride + g];
+                }
             }
         }
     };
     const auto storeTile = [&](int buf) {
+        if constexpr (kInt8) {
+#pragma unroll
+            for (int r = 0; r < kKPer; ++r) kraw[r] = codesToBf16(kraw[r], ksc[r]);
+#pragma unroll
+            for (int r = 0; r < kVPer; ++r)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) vraw[r][e] = codesToBf16(vraw[r][e], vsc[r][e]);
+        }
 #pragma unroll
         for (int r = 0; r < kKPer; ++r) {
             const int idx = ltid + r * kWave * W;
@@ -625,34 +668,6 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
 constexpr int kDecWaves = 4;
 constexpr int kDecKT = 32;   // keys per wave step
 constexpr int kDecVtLd = 40; // V^T row stride (bf16): 16-byte reads of rows 16 apart hit distinct banks
-
-// 8 consecutive elements of a cache row (128 per row) as raw bits: bf16 (16 bytes) or INT8
-// codes (8 bytes, in .x / .y).
-template <bool kInt8>
-__device__ __forceinline__ v4u loadRow8(const void *base, size_t row, int col) {
-    if constexpr (kInt8) {
-        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
-        const v2u c = *reinterpret_cast<const v2u *>(static_cast<const int8_t *>(base) + row * 128 + col);
-        return v4u{c.x, c.y, 0u, 0u};
-    } else {
-        return *reinterpret_cast<const v4u *>(static_cast<const uint16_t *>(base) + row * 128 + col);
-    }
-}
-
-// 8 INT8 codes -> bf16(code * sc) as 4 packed words.  code = u - 128 for the unsigned byte
-// u of code ^ 0x80, and fma(u, sc, -128 sc) rounds u * sc - 128 sc = code * sc once (-128 sc
-// is exact), i.e. exactly float(code) * sc; the pair conversion then rounds to bf16 as the
-// reference does for every non-NaN value.
-__device__ __forceinline__ v4u codesToBf16(const v4u &raw, float sc) {
-    const uint32_t ux = raw.x ^ 0x80808080u, uy = raw.y ^ 0x80808080u;
-    const float off = -128.0f * sc;
-    const auto cv = [&](uint32_t u, int k) {
-        const float b = float((u >> (8 * k)) & 0xFFu); // v_cvt_f32_ubyte{k}
-        return __builtin_fmaf(b, sc, off);
-    };
-    return v4u{Bf16Cvt::narrow2Q(cv(ux, 0), cv(ux, 1)), Bf16Cvt::narrow2Q(cv(ux, 2), cv(ux, 3)),
-               Bf16Cvt::narrow2Q(cv(uy, 0), cv(uy, 1)), Bf16Cvt::narrow2Q(cv(uy, 2), cv(uy, 3))};
-}
 
 template <bool kInt8>
 __global__ void __launch_bounds__(kWave * kDecWaves)
@@ -878,9 +893,9 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
     }
     const int G = sliceOf(a.group);
     a.slices = a.group / G;
-    // bf16 prefill (16 or more queries) goes to the MFMA kernel; decode and the other
-    // types stay on the vector kernel
-    if constexpr (std::is_same_v<T, BF16> && !kInt8) {
+    // bf16 prefill (16 or more queries, cache in bf16 or INT8) goes to the MFMA kernel;
+    // decode and the other types stay on the vector kernel
+    if constexpr (std::is_same_v<T, BF16>) {
         const size_t mblocks = (a.seq + kMfmaQ - 1) / kMfmaQ * size_t(a.nkvh) * size_t(a.slices);
         // (the MFMA kernel tracks the max of the raw dot products: valid for a positive scale)
         if (d == 128 && a.total > 0 && a.seq >= size_t(kMfmaQ) && mblocks < (size_t(1) << 31) &&
@@ -891,18 +906,18 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
             // (groups of 8 keep one wave per head: 16 waves of 8 heads would spill registers)
             if (mblocks <= 512 && G <= 6) {
                 switch (G) {
-                case 6: attnMfma<6, true><<<unsigned(mblocks), kWave * 12, 0, s>>>(a); return;
-                case 4: attnMfma<4, true><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
-                case 2: attnMfma<2, true><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
-                default: attnMfma<1, true><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
+                case 6: attnMfma<6, true, kInt8><<<unsigned(mblocks), kWave * 12, 0, s>>>(a); return;
+                case 4: attnMfma<4, true, kInt8><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
+                case 2: attnMfma<2, true, kInt8><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
+                default: attnMfma<1, true, kInt8><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
                 }
             }
             switch (G) {
-            case 8: attnMfma<8, false><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
-            case 6: attnMfma<6, false><<<unsigned(mblocks), kWave * 6, 0, s>>>(a); return;
-            case 4: attnMfma<4, false><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
-            case 2: attnMfma<2, false><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
-            default: attnMfma<1, false><<<unsigned(mblocks), kWave, 0, s>>>(a); return;
+            case 8: attnMfma<8, false, kInt8><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
+            case 6: attnMfma<6, false, kInt8><<<unsigned(mblocks), kWave * 6, 0, s>>>(a); return;
+            case 4: attnMfma<4, false, kInt8><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
+            case 2: attnMfma<2, false, kInt8><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
+            default: attnMfma<1, false, kInt8><<<unsigned(mblocks), kWave, 0, s>>>(a); return;
             }
         }
     }

@@ -109,7 +109,10 @@ def test_self_attention_empty_cache_gives_zeros():
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
-@pytest.mark.parametrize("shape", [(1, 4097, 12, 2, 128), (128, 128, 12, 2, 128), (5, 11, 4, 2, 8), (7, 33, 4, 2, 64)],
+@pytest.mark.parametrize("shape", [(1, 4097, 12, 2, 128), (128, 128, 12, 2, 128), (5, 11, 4, 2, 8), (7, 33, 4, 2, 64),
+                                   # bf16 prefill over the INT8 cache on the MFMA kernel: a prefix
+                                   # cache, GQA 4 with ragged tiles, unsplit (> 512 blocks)
+                                   (200, 1000, 12, 2, 128), (48, 70, 32, 8, 128), (300, 300, 168, 28, 128)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_self_attention_int8kv(dt, shape):
     """INT8 cache (1% outliers x20, as config 3) against dequantize-then-attend on the GPU
