@@ -700,8 +700,10 @@ def measure_decode(L, hip, stream, e0, e1, graphs=True, int8_only=False):
 
 
 def cpu_baseline(seconds):
-    """Reference CPU ops (oracle/_ref, else the oracle port) on a row sample of config 1,
-    single thread pinned to one core; GB/s with the same bytes formula as the GPU."""
+    """The oracle's restatement of the reference CPU ops (oracle/, pinned bit for bit to the
+    compiled reference by tests/test_oracle.py; the reference itself never travels to the
+    GPU box) on a row sample of config 1, single thread pinned to one core; GB/s with the
+    same bytes formula as the GPU."""
     import oracle
     rng = np.random.default_rng(7)
     rows, srows, stok = 512, 128, 512
@@ -718,44 +720,16 @@ def cpu_baseline(seconds):
                   + (2 * stok * (NH + NKV) * D * 2 + 2 * stok * 8) + 3 * srows * I * 2 + (V * 2 + 10))
     sample = (f"config-1 ops on a sample: embedding 8192 ids, rms_norm and add+rms_norm "
               f"{rows} rows, rope q+k {stok} tokens, swiglu {srows} rows, argmax [1,{V}]")
-    ref = oracle.reference_library()
-    if ref is not None:
-        import llaisys_amd as L
-        from llaisys_amd.libllaisys import bind
-        bind(ref)
-        C, BF = L.DeviceType.CPU, L.DataType.BF16
 
-        def ht(a, dt=BF):
-            return L.Tensor.from_numpy(a, dt, device=C, lib=ref)
-
-        hx, hr, hw, hq, hk, hp = ht(x), ht(r), ht(w), ht(q), ht(k), ht(pos, L.DataType.I64)
-        hg, hu, htab, hid, hl = ht(g), ht(u), ht(table), ht(ids, L.DataType.I64), ht(logits)
-        o1, o2, o3 = (L.Tensor((rows, H), BF, C, lib=ref) for _ in range(3))
-        oq, ok = L.Tensor(q.shape, BF, C, lib=ref), L.Tensor(k.shape, BF, C, lib=ref)
-        og, oe = L.Tensor(g.shape, BF, C, lib=ref), L.Tensor((T, H), BF, C, lib=ref)
-        oi, ov = L.Tensor((1,), L.DataType.I64, C, lib=ref), L.Tensor((1,), BF, C, lib=ref)
-        f = ctypes.c_float
-
-        def step():
-            ref.llaisysEmbedding(oe.lib_tensor(), hid.lib_tensor(), htab.lib_tensor())
-            ref.llaisysRmsNorm(o1.lib_tensor(), hx.lib_tensor(), hw.lib_tensor(), f(1e-6))
-            ref.llaisysAdd(o2.lib_tensor(), hx.lib_tensor(), hr.lib_tensor())
-            ref.llaisysRmsNorm(o3.lib_tensor(), o2.lib_tensor(), hw.lib_tensor(), f(1e-6))
-            ref.llaisysROPE(oq.lib_tensor(), hq.lib_tensor(), hp.lib_tensor(), f(1e4))
-            ref.llaisysROPE(ok.lib_tensor(), hk.lib_tensor(), hp.lib_tensor(), f(1e4))
-            ref.llaisysSwiGLU(og.lib_tensor(), hg.lib_tensor(), hu.lib_tensor())
-            ref.llaisysArgmax(oi.lib_tensor(), ov.lib_tensor(), hl.lib_tensor())
-        kind = "reference"
-    else:
-        def step():
-            oracle.embedding(ids, table)
-            oracle.rms_norm(x, w, 1e-6)
-            oracle.add_rms_norm(x, r, w, 1e-6)
-            oracle.rope(q, pos, 1e4)
-            oracle.rope(k, pos, 1e4)
-            oracle.swiglu(g, u)
-            oracle.argmax(logits)
-        kind = "port"
+    def step():
+        oracle.embedding(ids, table)
+        oracle.rms_norm(x, w, 1e-6)
+        oracle.add_rms_norm(x, r, w, 1e-6)
+        oracle.rope(q, pos, 1e4)
+        oracle.rope(k, pos, 1e4)
+        oracle.swiglu(g, u)
+        oracle.argmax(logits)
+    kind = "port"
     saved = os.sched_getaffinity(0)
     os.sched_setaffinity(0, {min(saved)})
     try:

@@ -67,8 +67,11 @@ __C {
      * per-op host launch cost).  Between Begin and End every op called on this thread for
      * (device_type, device_id) is recorded instead of run; End returns an executable graph
      * that Launch replays on the same stream, with the tensors captured at record time.
-     * Only the AMD device supports capture.  Ops whose scratch would have to grow during
-     * capture (a flat argmax over more than 2^29 elements) fail at capture time. */
+     * Only the AMD device supports capture.  Begin reserves the library scratch a captured
+     * op may use (64 MiB beyond its fixed head, every attention launch fits; the environment
+     * variable LLAISYS_GRAPH_WORKSPACE_BYTES sets another size); an op that would need more
+     * during capture fails with a message.  A graph keeps the scratch it captured alive
+     * until Destroy, so later eager ops that grow the scratch do not invalidate it. */
     typedef struct LlaisysGraph *llaisysGraph_t;
     __export void llaisysGraphBeginCapture(llaisysDeviceType_t, int);
     __export llaisysGraph_t llaisysGraphEndCapture(llaisysDeviceType_t, int);

@@ -59,7 +59,7 @@ __C {
         if (type != LLAISYS_DEVICE_AMD) EXCEPTION_UNSUPPORTED_DEVICE;
         auto &ctx = llaisys::core::context();
         ctx.setDevice(type, id);
-        return llaisys::device::amd::endCapture(ctx.runtime().stream());
+        return llaisys::device::amd::endCapture(id, ctx.runtime().stream());
     }
 
     void llaisysGraphLaunch(llaisysGraph_t g) { llaisys::device::amd::launchGraph(g); }

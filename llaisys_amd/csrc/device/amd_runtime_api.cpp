@@ -10,6 +10,10 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include "../kernels/launch.hpp"
+
+#include <cstdlib>
+#include <memory>
 #include <mutex>
 #include <vector>
 
@@ -104,9 +108,44 @@ constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 int *g_err[kMaxDevices] = {};
 // Workspaces are per thread: every thread has its own Context and hence its own stream
-// per device, and stream order is what makes reuse of a workspace safe.
-thread_local void *g_ws[kMaxDevices] = {};
-thread_local size_t g_ws_size[kMaxDevices] = {};
+// per device, and stream order is what makes reuse of a workspace safe.  A buffer is
+// shared: the thread's slot holds the current one, and every graph captured on it holds
+// it too, so a later growth (which moves the slot to a bigger buffer) never frees memory
+// that a graph's kernels still address.  The last owner frees it.
+struct WsBuffer {
+    void *ptr = nullptr;
+    size_t size = 0;
+    WsBuffer(const WsBuffer &) = delete;
+    WsBuffer &operator=(const WsBuffer &) = delete;
+    WsBuffer(void *p, size_t n) : ptr(p), size(n) {}
+    ~WsBuffer() {
+        // kernels queued on any stream may still use it; teardown ignores errors
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ptr);
+    }
+};
+struct WsSlots {
+    std::shared_ptr<WsBuffer> buf[kMaxDevices];
+    bool capturing[kMaxDevices] = {};
+};
+// Never destroyed: at thread (and process) exit the HIP runtime may already be gone, so
+// the thread's buffers are left to the driver, as any device memory at exit.
+WsSlots &wsSlots() {
+    thread_local WsSlots *slots = new WsSlots();
+    return *slots;
+}
+
+// Workspace reserved when a capture starts (bytes beyond the library's reserved head):
+// enough for every attention launch (its partials are capped at 64 MiB).  The environment
+// variable LLAISYS_GRAPH_WORKSPACE_BYTES overrides it.
+size_t captureReserve() {
+    if (const char *e = std::getenv("LLAISYS_GRAPH_WORKSPACE_BYTES")) {
+        char *end = nullptr;
+        const unsigned long long v = std::strtoull(e, &end, 10);
+        if (end != e && *end == '\0') return size_t(v);
+    }
+    return size_t(64) << 20;
+}
 
 int currentDevice() {
     int d = 0;
@@ -154,21 +193,30 @@ void raiseIfError(llaisysStream_t s) {
 
 void *workspace(int dev, size_t bytes) {
     CHECK_ARGUMENT(dev >= 0 && dev < kMaxDevices, "device id out of range");
-    if (g_ws_size[dev] < bytes) {
-        // Stream order makes reuse safe; a grow must wait for kernels still reading it.
-        if (g_ws[dev]) {
-            check(hipDeviceSynchronize(), "hipDeviceSynchronize(workspace)");
-            check(hipFree(g_ws[dev]), "hipFree(workspace)");
-        }
+    WsSlots &ws = wsSlots();
+    std::shared_ptr<WsBuffer> &cur = ws.buf[dev];
+    if (!cur || cur->size < bytes) {
+        // Growing inside a capture would record a synchronisation and a memset into the
+        // graph and hand the graph a buffer chosen mid-recording: refuse it.
+        if (ws.capturing[dev])
+            LLAISYS_FAIL(std::runtime_error,
+                         "library workspace must grow to " << bytes
+                             << " bytes during HIP graph capture; set LLAISYS_GRAPH_WORKSPACE_BYTES "
+                                "above that before llaisysGraphBeginCapture",
+                         "workspace growth during capture");
         size_t n = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
         void *p = nullptr;
         check(hipMalloc(&p, n), "hipMalloc(workspace)");
         // Kernels that keep a completion counter in the workspace expect it zeroed once.
-        check(hipMemset(p, 0, n), "hipMemset(workspace)");
-        g_ws[dev] = p;
-        g_ws_size[dev] = n;
+        const int st = hipMemset(p, 0, n);
+        if (st != hipSuccess) {
+            (void)hipFree(p);
+            check(st, "hipMemset(workspace)");
+        }
+        // The old buffer is freed (after a device synchronisation) once no graph holds it.
+        cur = std::make_shared<WsBuffer>(p, n);
     }
-    return g_ws[dev];
+    return cur->ptr;
 }
 
 } // namespace llaisys::device::amd
@@ -177,6 +225,8 @@ struct LlaisysGraph {
     hipGraph_t graph;
     hipGraphExec_t exec;
     hipStream_t stream;
+    // the workspace the captured kernels address: kept alive until the graph is destroyed
+    std::shared_ptr<llaisys::device::amd::WsBuffer> workspace;
 };
 
 namespace llaisys::device::amd {
@@ -184,13 +234,17 @@ namespace llaisys::device::amd {
 void beginCapture(int dev, llaisysStream_t s) {
     // Everything an op may allocate lazily must exist before capture starts.
     (void)errorWord(dev);
-    (void)workspace(dev, 1);
+    (void)workspace(dev, kernels::kScratchReserved + captureReserve());
     check(hipStreamBeginCapture(static_cast<hipStream_t>(s), hipStreamCaptureModeRelaxed),
           "hipStreamBeginCapture");
+    wsSlots().capturing[dev] = true;
 }
 
-llaisysGraph_t endCapture(llaisysStream_t s) {
-    auto *g = new LlaisysGraph{nullptr, nullptr, static_cast<hipStream_t>(s)};
+llaisysGraph_t endCapture(int dev, llaisysStream_t s) {
+    CHECK_ARGUMENT(dev >= 0 && dev < kMaxDevices, "device id out of range");
+    WsSlots &ws = wsSlots();
+    ws.capturing[dev] = false;
+    auto *g = new LlaisysGraph{nullptr, nullptr, static_cast<hipStream_t>(s), ws.buf[dev]};
     const int st = hipStreamEndCapture(g->stream, &g->graph);
     if (st != hipSuccess) {
         delete g;

@@ -26,12 +26,15 @@ void raiseIfError(llaisysStream_t stream);
 
 // Grow-only scratch for multi-block kernels (partial results and a completion counter),
 // one per (thread, device) because each thread launches on its own stream.  Returns at
-// least `bytes` of device memory, zeroed when first allocated.
+// least `bytes` of device memory, zeroed when first allocated.  A growth moves the thread
+// to a new buffer; the old one is freed once no captured graph holds it.
 void *workspace(int device_id, size_t bytes);
 
 // HIP-graph capture of the work enqueued on `stream` (the current device's context stream).
+// beginCapture reserves the workspace a captured op may need (growth during capture is an
+// error); the graph keeps the workspace it captured alive until destroyGraph.
 void beginCapture(int device_id, llaisysStream_t stream);
-llaisysGraph_t endCapture(llaisysStream_t stream);
+llaisysGraph_t endCapture(int device_id, llaisysStream_t stream);
 void launchGraph(llaisysGraph_t g);
 void destroyGraph(llaisysGraph_t g);
 

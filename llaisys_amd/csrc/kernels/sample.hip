@@ -3,7 +3,9 @@
 // No reference kernel: README.md:397-399 asks for a random sample operator with
 // temperature, top-k and top-p, and python/llaisys/models/qwen2.py:216-218 takes the three
 // parameters.  The rule (z = x * (1/T); order by (z desc, index asc); keep the top k;
-// integer weights w = floor(2^31 * 2^((z - zmax) log2 e)) from a fixed exp2 polynomial;
+// integer weights w = floor(2^31 * 2^((z - zmax) log2 e)) from a fixed exp2 polynomial, with
+// (z - zmax) taken as 0 for candidates tied with the top one (infinite ties included) and a
+// NaN z ordered as -inf;
 // top-p prefix by integer weight sum; inverse-CDF draw with a splitmix64 uniform) is made of
 // integer work and IEEE single multiplies / adds in a fixed order, so every GPU result is
 // bit-identical to the CPU statement of the rule whatever the thread order.
@@ -32,8 +34,10 @@ constexpr int kSmpChunk = kSmpBlock * 8; // elements per histogram block
 constexpr int kMaxK = 1024;
 constexpr int kTieCap = 4096;
 
+// Order-preserving key of z; a NaN z (either sign) takes the key of -inf, so it is never
+// preferred to a number and ties with -inf by index.
 __device__ __forceinline__ uint32_t keyOf(float z) {
-    const uint32_t b = __float_as_uint(z);
+    const uint32_t b = z != z ? 0xFF800000u : __float_as_uint(z);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 __device__ __forceinline__ float unkey(uint32_t k) {
@@ -335,7 +339,9 @@ __global__ void __launch_bounds__(kFinThreads)
         w4[e] = 0;
         if (j < k) {
             const float z = unkey(~uint32_t(item[j] >> 32));
-            const float p = sampleExp2(__fmul_rn(__fsub_rn(z, zmax), 1.4426950408889634f));
+            // a candidate tied with the top key weighs 2^0 also when both are infinite
+            const bool top = uint32_t(item[j] >> 32) == uint32_t(item[0] >> 32);
+            const float p = sampleExp2(top ? 0.0f : __fmul_rn(__fsub_rn(z, zmax), 1.4426950408889634f));
             w4[e] = uint32_t(__fmul_rn(p, 2147483648.0f));
         }
         run += w4[e];

@@ -401,8 +401,10 @@ float orc_sample_exp2(float t) {
     return ldexpf(y * 1.4142135623730951f, (int)n);
 }
 
+/* a NaN z (either sign) takes the key of -inf: never preferred to a number */
 static uint32_t smp_key(float z) {
     uint32_t b;
+    if (z != z) z = -INFINITY;
     memcpy(&b, &z, 4);
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
@@ -454,7 +456,10 @@ int orc_random_sample(int64_t *out_idx, const void *logits, size_t rows, size_t 
         const float zmax = smp_unkey(it[0].key);
         uint64_t W = 0;
         for (size_t j = 0; j < k; j++) {
-            const float p = orc_sample_exp2((smp_unkey(it[j].key) - zmax) * 1.4426950408889634f);
+            /* (z - zmax) is 0 for candidates tied with the top key, infinite ties included */
+            const float p = it[j].key == it[0].key
+                                ? orc_sample_exp2(0.0f)
+                                : orc_sample_exp2((smp_unkey(it[j].key) - zmax) * 1.4426950408889634f);
             w[j] = (uint32_t)(p * 2147483648.0f);
             W += w[j];
             cum[j] = W;

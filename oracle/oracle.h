@@ -67,9 +67,11 @@ void orc_linear_w8a16(void *out, const void *x, const int8_t *code, const float 
  * ignores them).  The rule, per row of `logits` [rows, V]:
  *   temperature <= 0 or top_k == 1: the row's argmax (first maximum);
  *   else z = x * (1 / temperature) (1/T rounded to f32 once), order the V elements by
- *   (key(z) desc, index asc) with key the order-preserving u32 of the f32 bits, keep the
- *   first min(top_k, V) (top_k must be in [2, 1024]), weights w = floor(p * 2^31) with
- *   p = orc_sample_exp2((z - zmax) * log2(e)), W = sum of w; top_p < 1 keeps the shortest
+ *   (key(z) desc, index asc) with key the order-preserving u32 of the f32 bits (a NaN z
+ *   takes the key of -inf), keep the first min(top_k, V) (top_k must be in [2, 1024]),
+ *   weights w = floor(p * 2^31) with p = orc_sample_exp2((z - zmax) * log2(e)), where
+ *   z - zmax counts as 0 for an element whose key equals the first one's (so infinite
+ *   ties weigh 2^0 and W > 0), W = sum of w; top_p < 1 keeps the shortest
  *   prefix whose w-sum >= max(1, floor(top_p * W)) (top_p <= 0: the first element);
  *   then with u24 = splitmix64(seed + row) >> 40 and r = floor(u24 * W_kept / 2^24), the
  *   sample is the first element of the kept prefix whose running w-sum exceeds r.

@@ -475,6 +475,55 @@ def test_config2_shapes_properties():
     no_device_error()
 
 
+def test_config2_swiglu_full():
+    """swiglu [16384, 14336] bf16 (config 2), every element against the oracle
+    (reference src/ops/swiglu/cpu/swiglu_cpu.cpp:15-20)."""
+    rng = np.random.default_rng(21)
+    BF = L.DataType.BF16
+    g, u = sample(rng, (16384, 14336), "bf16"), sample(rng, (16384, 14336), "bf16")
+    y = empty(g.shape, BF)
+    L.Ops.swiglu(y, dev(g, BF), dev(u, BF))
+    got = y.numpy()
+    for r0 in range(0, 16384, 4096):  # chunks bound the oracle's host memory
+        assert_close(got[r0:r0 + 4096], oracle.swiglu(g[r0:r0 + 4096], u[r0:r0 + 4096]), f"rows {r0}+")
+    no_device_error()
+
+
+def test_config2_embedding_full():
+    """Embedding from a [128256, 4096] bf16 table with 16384 int64 ids (config 2):
+    bit-exact against table[ids] (a gather is its own oracle,
+    src/ops/embedding/cpu/embedding_cpu.cpp:16-22), first and last rows included."""
+    rng = np.random.default_rng(22)
+    BF = L.DataType.BF16
+    table = sample(rng, (128256, 4096), "bf16", 0.02)
+    ids = rng.integers(0, 128256, size=16384).astype(np.int64)
+    ids[:2] = (0, 128255)
+    out = empty((16384, 4096), BF)
+    L.Ops.embedding(out, dev(ids), dev(table, BF))
+    assert_exact(out.numpy(), table[ids])
+    no_device_error()
+
+
+def test_config2_rope_qk_full():
+    """RoPE q [16384, 32, 128] and k [16384, 8, 128] bf16, theta 5e5, positions
+    0..16383 (config 2) through the fused q/k launch and the reference-ABI single-tensor
+    launch: every element against the oracle (src/ops/rope/cpu/rope_cpu.cpp:28-44)."""
+    rng = np.random.default_rng(23)
+    BF = L.DataType.BF16
+    q, k = sample(rng, (16384, 32, 128), "bf16"), sample(rng, (16384, 8, 128), "bf16")
+    pos = np.arange(16384, dtype=np.int64)
+    tq, tk, tp = dev(q, BF), dev(k, BF), dev(pos)
+    qo, ko = empty(q.shape, BF), empty(k.shape, BF)
+    L.Ops.rope_qk(qo, tq, ko, tk, tp, 5e5)
+    eq, ek = oracle.rope(q, pos, 5e5), oracle.rope(k, pos, 5e5)
+    assert_close(qo.numpy(), eq, "q (fused q/k)")
+    assert_close(ko.numpy(), ek, "k (fused q/k)")
+    ko2 = empty(k.shape, BF)
+    L.Ops.rope(ko2, tk, tp, 5e5)
+    assert_close(ko2.numpy(), ek, "k (llaisysROPE)")
+    no_device_error()
+
+
 # ---- fused q/k RoPE ------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
@@ -544,6 +593,61 @@ def test_graph_replays_match_eager():
         for name, tt in outs.items():
             assert_exact(tt.numpy(), eager[name], f"replay {replay}: {name}")
     no_device_error()
+
+
+def test_graph_keeps_its_workspace_after_growth(monkeypatch):
+    """A graph whose kernels use the library scratch (the flat argmax's counter, the
+    decode attention's partials) stays valid after a later eager op grows the scratch:
+    captured in a fresh thread (its own stream and scratch) with no capture reservation,
+    then a long decode attention run eagerly needs more scratch than the graph captured,
+    and three replays must still equal the eager results."""
+    import threading
+    monkeypatch.setenv("LLAISYS_GRAPH_WORKSPACE_BYTES", "0")
+    BF, I64 = L.DataType.BF16, L.DataType.I64
+    rng = np.random.default_rng(37)
+    logits = sample(rng, (1, 151936), "bf16")
+    q1, k1, v1 = (sample(rng, s, "bf16") for s in ((1, 12, 128), (64, 2, 128), (64, 2, 128)))
+    qb, kb, vb = (sample(rng, s, "bf16") for s in ((4, 12, 128), (32768, 2, 128), (32768, 2, 128)))
+    errors = []
+
+    def body():
+        try:
+            tl = dev(logits, BF)
+            tq, tk, tv = dev(q1, BF), dev(k1, BF), dev(v1, BF)
+            fi, fv, ao = empty((1,), I64), empty((1,), BF), empty((1, 12, 128), BF)
+
+            def ops():
+                L.Ops.argmax(fi, fv, tl)
+                L.Ops.self_attention(ao, tq, tk, tv, 0.0883883)
+
+            ops()
+            eager = [t.numpy() for t in (fi, fv, ao)]
+            graph = L.Graph.capture()
+            ops()
+            graph.end()
+            # 4 queries x 12 heads over 32768 keys: partials beyond the captured scratch
+            big = empty((4, 12, 128), BF)
+            L.Ops.self_attention(big, dev(qb, BF), dev(kb, BF), dev(vb, BF), 0.0883883)
+            api = L.RuntimeAPI(L.DeviceType.AMD)
+            api.device_synchronize()
+            for replay in range(3):
+                for t in (fi, fv, ao):
+                    z = np.zeros(t.shape(), dtype=t.numpy().dtype)
+                    api.memcpy_sync(t.data_ptr(), z.ctypes.data, z.nbytes, L.MemcpyKind.H2D)
+                graph.launch()
+                api.device_synchronize()
+                for name, t, e in zip(("idx", "val", "attn"), (fi, fv, ao), eager):
+                    assert_exact(t.numpy(), e, f"replay {replay}: {name}")
+            del graph
+            assert L.take_device_error() == 0
+        except BaseException as e:  # re-raised in the test thread
+            errors.append(e)
+
+    th = threading.Thread(target=body)
+    th.start()
+    th.join()
+    if errors:
+        raise errors[0]
 
 
 # ---- fused RoPE + INT8 KV append ---------------------------------------------------------

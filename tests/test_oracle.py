@@ -473,12 +473,15 @@ def _sample_rule(x, temperature, top_k, top_p, seed):
         return int(np.argmax(x))
     inv = np.float32(1.0) / np.float32(temperature)
     z = (x * inv).astype(np.float32)
+    z = np.where(np.isnan(z), np.float32(-np.inf), z).astype(np.float32)  # NaN orders as -inf
     bits = z.view(np.uint32).astype(np.int64)
     key = np.where(bits & 0x80000000, (~bits) & 0xFFFFFFFF, bits | 0x80000000)
     order = sorted(range(len(z)), key=lambda i: (-int(key[i]), i))[:min(top_k, len(z))]
     zmax = z[order[0]]
-    w = [int(np.float32(oracle.sample_exp2(np.float32(z[i] - zmax) * np.float32(1.4426950408889634)))
-             * np.float32(2 ** 31)) for i in order]
+    with np.errstate(invalid="ignore"):
+        d = [np.float32(0.0) if key[i] == key[order[0]] else np.float32(z[i] - zmax) for i in order]
+    w = [int(np.float32(oracle.sample_exp2(di * np.float32(1.4426950408889634))) * np.float32(2 ** 31))
+         for di in d]
     cum = np.cumsum(w, dtype=object)
     W = int(cum[-1])
     kept = len(order)
@@ -503,6 +506,32 @@ def test_random_sample_matches_the_rule_restated():
         seed = int(rng.integers(0, 2 ** 62))
         got = oracle.random_sample(x, T, k, p, seed)[0]
         assert got == _sample_rule(x, T, k, p, seed), (case, V, T, k, p)
+
+
+def test_random_sample_nan_and_infinite_logits():
+    """NaN logits order as -inf (never drawn while a number is among the candidates);
+    infinite maxima share the mass equally; an all -inf / NaN row still draws a candidate."""
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal(64).astype(np.float32)
+    x[[3, 10, 40]] = np.nan
+    x[11] = -np.nan
+    for seed in range(200):
+        got = oracle.random_sample(x, 0.8, 50, 0.9, seed)[0]
+        assert not np.isnan(x[got])
+        assert got == _sample_rule(x, 0.8, 50, 0.9, seed)
+    y = x.copy()
+    y[[5, 20]] = np.inf
+    draws = [oracle.random_sample(y, 1.0, 8, 0.95, s)[0] for s in range(400)]
+    assert set(draws) == {5, 20}
+    assert 120 < draws.count(5) < 280
+    for s in range(50):
+        assert oracle.random_sample(y, 1.0, 8, 0.95, s)[0] == _sample_rule(y, 1.0, 8, 0.95, s)
+    z = np.full(16, -np.inf, np.float32)
+    z[[2, 9]] = np.nan
+    draws = {oracle.random_sample(z, 1.0, 4, 1.0, s)[0] for s in range(100)}
+    assert draws == {0, 1, 2, 3}  # the four lowest indices, equal weights
+    for s in range(20):
+        assert oracle.random_sample(z, 1.0, 4, 0.5, s)[0] == _sample_rule(z, 1.0, 4, 0.5, s)
 
 
 def test_random_sample_greedy_cases_are_argmax():

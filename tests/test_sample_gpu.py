@@ -94,3 +94,27 @@ def test_random_sample_distribution_on_gpu():
     m = exp > 0
     chi2 = float((((counts[m] - exp[m]) ** 2) / exp[m]).sum())
     assert chi2 < 30, (counts, exp)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_random_sample_nan_and_infinite_logits(dt):
+    """NaN logits order as -inf, infinite maxima share the mass, an all -inf / NaN row
+    draws among its lowest indices: the GPU equals the oracle's rule on every row."""
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal((4, 151936)) * 3).astype(np.float32)
+    x[0, rng.choice(151936, 500, replace=False)] = np.nan
+    x[0, 7] = -np.nan
+    x[1, [100, 90000]] = np.inf
+    x[1, [5, 6]] = np.nan
+    x[2, :] = -np.inf
+    x[2, [3, 77]] = np.nan
+    x[3, :] = np.nan
+    x[3, 1234] = 1.0
+    xd = conv(x, dt)
+    for seed in (0, 5, 2 ** 40 + 3):
+        for k, p in ((50, 0.8), (1024, 1.0), (3, 0.5)):
+            exp = oracle.random_sample(xd, 1.0, k, p, seed)
+            got = gpu_sample(xd, dt, 1.0, k, p, seed)
+            assert np.array_equal(got, exp), (dt, seed, k, p, got, exp)
+            assert not np.isnan(x[0, got[0]])
+            assert x[1, got[1]] == np.inf and got[3] == 1234
