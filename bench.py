@@ -33,6 +33,38 @@ PEAK_GBS = 8000.0  # MI355X HBM3E
 
 T, H, V, NH, NKV, D, I = 8192, 1536, 151936, 12, 2, 128, 8960
 NSETS = 4
+REPS, WARMUP = 60, 10      # per-op timing: median of REPS launches after WARMUP
+FOOTPRINT = 1 << 30         # bytes each per-op loop rotates through (4x the 256 MB MALL)
+
+
+def time_launches(hip, stream, fn, batch=64, reps=REPS, warmup=WARMUP):
+    """Median and mean time in us of one call fn(i) over `reps` timed reps after `warmup`
+    untimed calls.  A rep is a batch of `batch` consecutive calls bracketed by HIP events on
+    the library stream (an event between single calls would add its own ~3 us to every
+    interval); i keeps counting across reps, so the reps walk through every rotating buffer
+    set of the case."""
+    i = 0
+    for _ in range(warmup):
+        fn(i)
+        i += 1
+    evs = hip.events(reps + 1)
+    hip.record(evs[0], stream)
+    for r in range(reps):
+        for _ in range(batch):
+            fn(i)
+            i += 1
+        hip.record(evs[r + 1], stream)
+    t = np.array([hip.elapsed_ms(evs[r], evs[r + 1]) * 1e3 / batch for r in range(reps)])
+    return float(np.median(t)), float(t.mean())
+
+
+def rate(name_us, nbytes, mean_us=None):
+    gbs = nbytes / (name_us * 1e-6) / 1e9
+    r = {"us": round(name_us, 3), "bytes": nbytes, "GB_s": round(gbs, 1),
+         "frac_peak": round(gbs / PEAK_GBS, 4)}
+    if mean_us is not None:
+        r["mean_us"] = round(mean_us, 3)
+    return r
 
 
 class HipEvents:
@@ -49,6 +81,11 @@ class HipEvents:
         ev = ctypes.c_void_p()
         assert self.hip.hipEventCreate(ctypes.byref(ev)) == 0
         return ev
+
+    def events(self, n):
+        if len(getattr(self, "_pool", [])) < n:
+            self._pool = [self.event() for _ in range(n)]
+        return self._pool[:n]
 
     def record(self, ev, stream):
         assert self.hip.hipEventRecord(ev, ctypes.c_void_p(stream)) == 0
@@ -339,7 +376,7 @@ class DecodeChain:
 class Pool:
     """Disjoint buffer sets cut from one allocation per tensor (slice + view keep the byte
     offset), filled with seeded normal samples; enough sets that one pass over them moves
-    >= 512 MB, so the 256 MB Infinity Cache does not serve the timed launches."""
+    >= 1 GiB (FOOTPRINT), so the 256 MB Infinity Cache does not serve the timed launches."""
 
     def __init__(self, L, rng):
         self.L, self.rng = L, rng
@@ -347,8 +384,8 @@ class Pool:
         self.api = L.RuntimeAPI(L.DeviceType.AMD)
         self.keep = []
 
-    def sets_for(self, nbytes, cap=256):
-        return int(max(2, min(cap, -(-(512 << 20) // max(1, nbytes)))))
+    def sets_for(self, nbytes, cap=4096):
+        return int(max(4, min(cap, -(-FOOTPRINT // max(1, nbytes)))))
 
     def fill(self, shape, dtype, sets, scale=1.0, loc=0.0):
         """`sets` tensors of `shape`; the first is sampled, the others copy it."""
@@ -381,6 +418,57 @@ class Pool:
 
     def ints(self, values_list):
         return [self.L.Tensor.from_numpy(v, **self.dev) for v in values_list]
+
+
+def config1_ops(L, rng):
+    """(op, algorithmic bytes per launch, launch(i)) for the config-1 ops one at a time,
+    each over its own >= 1 GiB of rotating buffer sets; the reference-ABI rope (q and k as
+    two calls) is timed beside the fused launch."""
+    O, BF, I64 = L.Ops, L.DataType.BF16, L.DataType.I64
+    P = Pool(L, rng)
+    tok = T * H * 2
+    cases = []
+    table = P.fill((V, H), BF, 1, 0.02)[0]
+    w = P.fill((H,), BF, 1, 0.1, 1.0)[0]
+    pos = L.Tensor.from_numpy(np.arange(T, dtype=np.int64), **P.dev)
+
+    b = T * 8 + 2 * tok
+    s = P.sets_for(b)
+    ids = P.ints([rng.integers(0, V, size=T).astype(np.int64) for _ in range(s)])
+    emb = P.empty((T, H), BF, s)
+    cases.append(("embedding", b, lambda i, s=s: O.embedding(emb[i % s], ids[i % s], table)))
+
+    b = 2 * tok + H * 2
+    s = P.sets_for(b)
+    x, y = P.fill((T, H), BF, s), P.empty((T, H), BF, s)
+    cases.append(("rms_norm", b, lambda i, s=s: O.rms_norm(y[i % s], x[i % s], w, 1e-6)))
+
+    b = 4 * tok + H * 2
+    s = P.sets_for(b)
+    xa, ra = P.fill((T, H), BF, s), P.fill((T, H), BF, s)
+    ya, ha = P.empty((T, H), BF, s), P.empty((T, H), BF, s)
+    cases.append(("add_rms_norm", b,
+                  lambda i, s=s: O.add_rms_norm(ya[i % s], ha[i % s], xa[i % s], ra[i % s], w, 1e-6)))
+
+    b = 2 * T * (NH + NKV) * D * 2 + T * 8
+    s = P.sets_for(b)
+    q, k = P.fill((T, NH, D), BF, s), P.fill((T, NKV, D), BF, s)
+    qo, ko = P.empty((T, NH, D), BF, s), P.empty((T, NKV, D), BF, s)
+    cases.append(("rope_qk", b, lambda i, s=s: O.rope_qk(qo[i % s], q[i % s], ko[i % s], k[i % s], pos, 1e4)))
+    cases.append(("rope_q", 2 * T * NH * D * 2 + T * 8, lambda i, s=s: O.rope(qo[i % s], q[i % s], pos, 1e4)))
+    cases.append(("rope_k", 2 * T * NKV * D * 2 + T * 8, lambda i, s=s: O.rope(ko[i % s], k[i % s], pos, 1e4)))
+
+    b = 3 * T * I * 2
+    s = P.sets_for(b)
+    g, u, act = P.fill((T, I), BF, s), P.fill((T, I), BF, s), P.empty((T, I), BF, s)
+    cases.append(("swiglu", b, lambda i, s=s: O.swiglu(act[i % s], g[i % s], u[i % s])))
+
+    b = V * 2 + 8 + 2
+    s = P.sets_for(b)
+    lg = P.fill((1, V), BF, s)
+    mi, mv = P.empty((1,), I64, 1)[0], P.empty((1,), BF, 1)[0]
+    cases.append(("argmax", b, lambda i, s=s: O.argmax(mi, mv, lg[i % s])))
+    return cases, P
 
 
 def config_ops(L, rng):
@@ -418,25 +506,26 @@ def config_ops(L, rng):
     cases.append(("config0", "argmax f32 [1,151936] (latency)", V0 * 4 + 12, 1,
                   lambda i: O.argmax(mi, mv, lg[i % sa])))
 
-    # config 2: Llama-8B shapes, bf16, 16384 tokens
+    # config 2: Llama-8B shapes, bf16, 16384 tokens (4 sets: >= 1 GiB per loop)
     t2, H2, I2, V2 = 16384, 4096, 14336, 128256
-    x2, y2 = P.fill((t2, H2), BF, 2), P.empty((t2, H2), BF, 2)
+    n2 = 4
+    x2, y2 = P.fill((t2, H2), BF, n2), P.empty((t2, H2), BF, n2)
     w2 = P.fill((H2,), BF, 1, 0.1, 1.0)[0]
     cases.append(("config2", "rms_norm [16384,4096]", 2 * t2 * H2 * 2 + H2 * 2, 1,
-                  lambda i: O.rms_norm(y2[i % 2], x2[i % 2], w2, 1e-5)))
-    q2, k2 = P.fill((t2, 32, D), BF, 2), P.fill((t2, 8, D), BF, 2)
-    qo2, ko2 = P.empty((t2, 32, D), BF, 2), P.empty((t2, 8, D), BF, 2)
+                  lambda i: O.rms_norm(y2[i % n2], x2[i % n2], w2, 1e-5)))
+    q2, k2 = P.fill((t2, 32, D), BF, n2), P.fill((t2, 8, D), BF, n2)
+    qo2, ko2 = P.empty((t2, 32, D), BF, n2), P.empty((t2, 8, D), BF, n2)
     pos2 = L.Tensor.from_numpy(np.arange(t2, dtype=np.int64), **P.dev)
     cases.append(("config2", "rope q+k [16384,32+8,128] theta 5e5", 2 * t2 * 40 * D * 2 + t2 * 8, 1,
-                  lambda i: O.rope_qk(qo2[i % 2], q2[i % 2], ko2[i % 2], k2[i % 2], pos2, 5e5)))
-    g2, u2, a2 = P.fill((t2, I2), BF, 2), P.fill((t2, I2), BF, 2), P.empty((t2, I2), BF, 2)
+                  lambda i: O.rope_qk(qo2[i % n2], q2[i % n2], ko2[i % n2], k2[i % n2], pos2, 5e5)))
+    g2, u2, a2 = P.fill((t2, I2), BF, n2), P.fill((t2, I2), BF, n2), P.empty((t2, I2), BF, n2)
     cases.append(("config2", "swiglu [16384,14336]", 3 * t2 * I2 * 2, 1,
-                  lambda i: O.swiglu(a2[i % 2], g2[i % 2], u2[i % 2])))
+                  lambda i: O.swiglu(a2[i % n2], g2[i % n2], u2[i % n2])))
     table2 = P.fill((V2, H2), BF, 1, 0.02)[0]
-    ids2 = P.ints([rng.integers(0, V2, size=t2).astype(np.int64) for _ in range(2)])
-    emb2 = P.empty((t2, H2), BF, 2)
+    ids2 = P.ints([rng.integers(0, V2, size=t2).astype(np.int64) for _ in range(n2)])
+    emb2 = P.empty((t2, H2), BF, n2)
     cases.append(("config2", "embedding [128256,4096] x 16384 ids", t2 * 8 + 2 * t2 * H2 * 2, 1,
-                  lambda i: O.embedding(emb2[i % 2], ids2[i % 2], table2)))
+                  lambda i: O.embedding(emb2[i % n2], ids2[i % n2], table2)))
 
     # config 3: INT8 weights (per output channel) and KV cache (per token and head)
     for rows, cols in ((8960, 1536), (1536, 8960)):
@@ -528,22 +617,13 @@ def time_cases(L, hip, stream, e0, e1, steps, cases):
     stream; kind "bytes" is rated against HBM, "flops" against the bf16 MFMA peak."""
     res = {}
     for name, kind, amount, fn in cases:
-        for i in range(3):
-            fn(i)
-        reps = max(steps // 2, 10)
-        hip.record(e0, stream)
-        for i in range(reps):
-            fn(i)
-        hip.record(e1, stream)
-        us = hip.elapsed_ms(e0, e1) / reps * 1e3
+        us, mean = time_launches(hip, stream, fn)
         if kind == "bytes":
-            gbs = amount / (us * 1e-6) / 1e9
-            res[name] = {"us": round(us, 3), "bytes": amount, "GB_s": round(gbs, 1),
-                         "frac_peak": round(gbs / PEAK_GBS, 4), "bound": "hbm"}
+            res[name] = dict(rate(us, amount, mean), bound="hbm")
         else:
             tf = amount / (us * 1e-6) / 1e12
-            res[name] = {"us": round(us, 3), "flops": amount, "TFLOP_s": round(tf, 2),
-                         "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            res[name] = {"us": round(us, 3), "mean_us": round(mean, 3), "flops": amount,
+                         "TFLOP_s": round(tf, 2), "frac_peak": round(tf / PEAK_BF16_TFLOPS, 4),
                          "bound": "mfma (bf16 dense peak)"}
     assert L.take_device_error() == 0
     return res
@@ -865,50 +945,36 @@ def main():
     ms_step = hip.elapsed_ms(e0, e1) / args.steps
     assert L.take_device_error() == 0
 
+    del wl
+    print("bench: building config-1 per-op buffers", file=sys.stderr, flush=True)
+    c1, c1pool = config1_ops(L, np.random.default_rng(3))
     per_op = {}
-    reps = max(args.steps, 20)
-    for name, nbytes, fn in ops + wl.extra_ops():
-        for i in range(3):
-            fn(wl.sets[i % NSETS])
-        hip.record(e0, stream)
-        for i in range(reps):
-            fn(wl.sets[i % NSETS])
-        hip.record(e1, stream)
-        us = hip.elapsed_ms(e0, e1) / reps * 1e3
-        gbs = nbytes / (us * 1e-6) / 1e9
-        per_op[name] = {"us": round(us, 3), "bytes": nbytes, "GB_s": round(gbs, 1),
-                        "frac_peak": round(gbs / PEAK_GBS, 4)}
+    for name, nbytes, fn in c1:
+        med, mean = time_launches(hip, stream, fn)
+        per_op[name] = rate(med, nbytes, mean)
+    assert L.take_device_error() == 0
+    del c1, c1pool
     print("bench: per-op " + json.dumps(per_op), file=sys.stderr, flush=True)
 
     chain = None
     if not args.no_chain:
-        del wl
         print("bench: building config-4 chain buffers", file=sys.stderr, flush=True)
         ch = Chain(L)
-        for _ in range(2):
-            ch.run()
-        nrep = 10
-        hip.record(e0, stream)
-        for _ in range(nrep):
-            ch.run()
-        hip.record(e1, stream)
-        ms_eager = hip.elapsed_ms(e0, e1) / nrep
+        us_eager, _ = time_launches(hip, stream, lambda i: ch.run(), batch=2, reps=10, warmup=2)
+        ms_eager = us_eager * 1e-3
         graph = L.Graph.capture()
         ch.run()
         graph.end()
-        for _ in range(2):
-            graph.launch()
-        hip.record(e0, stream)
-        for _ in range(nrep):
-            graph.launch()
-        hip.record(e1, stream)
-        ms = hip.elapsed_ms(e0, e1) / nrep
+        us, us_mean = time_launches(hip, stream, lambda i: graph.launch(), batch=4)
+        ms = us * 1e-3
         del graph
         cb = ch.bytes()
         chain = {"workload": "config 4: 28 Qwen2-1.5B layers, 2048-token prefill, bf16, INT8 KV "
                              "append, final rms_norm + argmax over [2048, 151936]; replayed "
                              "as one HIP graph",
-                 "ms": round(ms, 4), "tokens_per_s": round(Chain.TOK / (ms * 1e-3)),
+                 "ms": round(ms, 4), "ms_mean": round(us_mean * 1e-3, 4),
+                 "timing": "median over 60 reps of 4 graph replays, after 10",
+                 "tokens_per_s": round(Chain.TOK / (ms * 1e-3)),
                  "bytes": cb, "GB_s": round(cb / (ms * 1e-3) / 1e9, 1),
                  "frac_peak": round(cb / (ms * 1e-3) / 1e9 / PEAK_GBS, 4),
                  "ms_eager_launches": round(ms_eager, 4),
@@ -922,18 +988,8 @@ def main():
         cases, pool = config_ops(L, np.random.default_rng(9))
         configs = {}
         for cfg, name, nbytes, launches, fn in cases:
-            for i in range(3):
-                fn(i)
-            reps = max(args.steps, 20)
-            hip.record(e0, stream)
-            for i in range(reps):
-                fn(i)
-            hip.record(e1, stream)
-            us = hip.elapsed_ms(e0, e1) / reps * 1e3
-            gbs = nbytes / (us * 1e-6) / 1e9
-            configs.setdefault(cfg, {})[name] = {
-                "us": round(us, 3), "bytes": nbytes, "launches": launches,
-                "GB_s": round(gbs, 1), "frac_peak": round(gbs / PEAK_GBS, 4)}
+            med, mean = time_launches(hip, stream, fn)
+            configs.setdefault(cfg, {})[name] = dict(rate(med, nbytes, mean), launches=launches)
         assert L.take_device_error() == 0
         del cases, pool
         print("bench: configs " + json.dumps(configs), file=sys.stderr, flush=True)
