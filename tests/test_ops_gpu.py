@@ -271,6 +271,18 @@ def test_embedding_out_of_range_sets_the_device_error():
     assert np.array_equal(got[0], w[3]) and np.array_equal(got[3], w[5])
     assert not got[1].any() and not got[2].any()  # out-of-range rows untouched
     assert L.take_device_error() == 0  # the error word was cleared
+    # Qwen2 rows (8 ids per wavefront): bad ids inside full and partial groups
+    w2 = sample(np.random.default_rng(1), (1000, 1536), "bf16")
+    idx2 = np.arange(40, dtype=np.int64) * 7
+    idx2[[5, 17, 38]] = [1000, -3, 2 ** 40]
+    out2 = dev(np.zeros((40, 1536), np.uint16), L.DataType.BF16)
+    L.Ops.embedding(out2, dev(idx2), dev(w2, L.DataType.BF16))
+    assert L.take_device_error() == 1
+    got2 = out2.numpy()
+    good = np.ones(40, bool)
+    good[[5, 17, 38]] = False
+    assert np.array_equal(got2[good], w2[idx2[good]])
+    assert not got2[~good].any()
 
 
 # ---- argmax ------------------------------------------------------------------------------
