@@ -215,18 +215,24 @@ __device__ __forceinline__ V waveGroupReduce(V v) {
     return v;
 }
 
+// Workgroup barrier for an LDS hand-off only: waits for this wave's LDS accesses, not for
+// its global loads and stores.  __syncthreads() carries a workgroup fence, for which the
+// compiler waits on every outstanding global access (s_waitcnt vmcnt(0), which on gfx9
+// counts stores too) -- that would drain loads issued ahead of the barrier to overlap it.
+__device__ __forceinline__ void ldsBarrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <int G, typename Op, typename V>
 __device__ __forceinline__ V groupReduce(V v, V *red) {
     v = waveGroupReduce<(G < kWave ? G : kWave), Op>(v);
     if constexpr (G > kWave) {
         const int wave = threadIdx.x / kWave;
         if (threadIdx.x % kWave == 0) red[wave] = v;
-        __syncthreads();
+        ldsBarrier();
         const int first = (threadIdx.x / G) * (G / kWave);
         v = red[first];
 #pragma unroll
         for (int k = 1; k < G / kWave; ++k) v = Op::apply(v, red[first + k]);
-        __syncthreads();
+        ldsBarrier();
     }
     return v;
 }

@@ -73,7 +73,6 @@ constexpr int kXcds = 8;              // accelerator complex dies of an MI355X
 // Workgroup barrier for LDS hand-offs only: waits for this wave's LDS accesses, not for its
 // global loads (__syncthreads' fence would also drain the prefetches in flight).  The
 // memory clobber keeps the compiler from moving accesses across it.
-__device__ __forceinline__ void ldsBarrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 constexpr int kTPitch = 2 * kTK + 16; // LDS row pitch (bytes)
 
 // Epilogue of the tiled kernels: D[8 q + 4 h + e][r32] of 32 x 32 tile (i, j) (q, e < 4) is

@@ -46,7 +46,6 @@ struct NormLinArgs {
     int N, K;           // outputs (swiglu: gate / up pairs), row length
 };
 
-__device__ __forceinline__ void ldsBarrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <typename T, bool kInt8, int G, int VMAX, bool kSwiglu, int U>
 __global__ void __launch_bounds__(256)

@@ -81,7 +81,7 @@ __device__ __forceinline__ void blockCosSin(double2 *cs, AngleInputs first, cons
                                             size_t t0, int ntok, int half, const FreqTable &ft) {
     __shared__ int far_angle;
     if (threadIdx.x == 0) far_angle = 0;
-    __syncthreads();
+    ldsBarrier(); // LDS only: the item loads the caller issued stay in flight
     bool far = false;
     for (int i = threadIdx.x; i < ntok * half; i += blockDim.x) {
         const double ang =
@@ -94,7 +94,7 @@ __device__ __forceinline__ void blockCosSin(double2 *cs, AngleInputs first, cons
         cs[i] = make_double2(c, sn);
     }
     if (far) far_angle = 1;
-    __syncthreads();
+    ldsBarrier();
     if (__builtin_expect(far_angle != 0, 0)) {
         for (int i = threadIdx.x; i < ntok * half; i += blockDim.x) {
             const double ang = angleAt(pos, t0, i, half, ft);

@@ -8,11 +8,22 @@
 // quantize.hpp.  The codes therefore equal llaisysROPE followed by llaisysKVAppendInt8 bit
 // for bit; the rope'd k never goes to HBM in bf16.
 //
-// Design: one launch covers the q, k and v head rows of a run of tokens (Qwen2-1.5B: 12 +
-// 2 + 2 rows of 16 vectors = 256 items per token, one per lane).  Lane layout and the f64
-// (cos, sin) staging are those of rope.hip.  A k or v row sits on 2*VPH consecutive lanes;
-// its absmax is reduced across them with xor shuffles, then each lane writes its 8 (bf16 /
-// f16) or 4 (f32) codes, so the group stores the whole code row contiguously.
+// Design: one launch covers the q, k and v head rows of the tokens; one wavefront per token
+// (rope.hip's ropeWave layout: a head row on 2*VPH consecutive lanes, 16 bytes each, so
+// every wave instruction moves 1 KB of contiguous rows).  The wave computes its token's
+// f64 (cos, sin) pairs into its own LDS slice while the row loads are in flight; no block
+// barrier.  A k or v row's absmax is reduced across its lanes with DPP, then each lane
+// writes its 8 (bf16 / f16) or 4 (f32) codes, so the group stores the whole code row
+// contiguously.
+//
+// Bound (MI355X, Qwen2 shapes, 2048 tokens, 15 MB): 5.2 us against 3.8 us for a copy
+// kernel with the same traffic.  rocprofv3 counters put the difference in VALU issue: ~690
+// VALU instructions per token-wave (the f64 rotation -- two f32->f64 conversions, a
+// multiply, an fma and the conversion back per element, which the bit-exact k codes
+// need -- the f64 sincos, and the quantizer's divisions and correctly rounded quotients),
+// i.e. ~2.3 us of issue per SIMD at 4 cycles per wave64 instruction, only partly hidden
+// behind the 1.7 us of transfer.  A block-per-2-tokens layout with block-wide (cos, sin)
+// staging took 5.3-5.45 us.
 #include "common.hpp"
 #include "launch.hpp"
 #include "quantize.hpp"
@@ -29,8 +40,6 @@ namespace {
 
 using namespace rope_detail;
 
-constexpr int kMaxItemsKv = 4;
-
 struct RopeKvArgs {
     void *q_out;
     const void *q_in;
@@ -44,118 +53,166 @@ struct RopeKvArgs {
     int nk; // k and v heads
 };
 
-// Items of a block are tensor-major, as in rope.hip: the block's q vectors (one contiguous
-// range of q), then its k vectors, then its v vectors; an item's addresses are per-block
-// bases plus 32-bit lane offsets, and item -> token a multiply by the tensor's magic.
+// One wavefront per token (the layout of rope.hip's ropeWave): the token's head rows --
+// q rows, then k rows, then v rows, kRowVec lanes each -- are taken in passes of IPT wave
+// instructions.  Each lane computes one (cos, sin) pair of the token into the wave's own
+// LDS slice (no block barrier) while the row loads are in flight, then keeps its column's
+// pairs in registers.  Waves past the last token redo the last token and store nothing.
 template <typename T, int IPT, int VPH>
 __global__ void __launch_bounds__(256)
-    ropeKvVec(RopeKvArgs a, const int64_t *__restrict__ pos, size_t seq, int tok_per_block,
-              uint32_t magic_q, uint32_t magic_kv, FreqTable ft) {
+    ropeKvWave(RopeKvArgs a, const int64_t *__restrict__ pos, size_t seq, int passes, FreqTable ft) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
-    constexpr int kRowVec = 2 * VPH;
+    constexpr int kRowVec = 2 * VPH;       // lanes per head row
+    constexpr int kRows = kWave / kRowVec; // rows per wave instruction
     constexpr int kHalf = VPH * N;
-    constexpr int kShift = __builtin_ctz(kRowVec);
-    __shared__ double2 cs[kLdsPairs];
+    constexpr int kRowBytes = kRowVec * 16;
+    constexpr int kRowCodes = kRowVec * N; // head_dim
+    __shared__ double2 cs[256 / kWave][kHalf];
+    const auto angleOf = [](int slot) { return (slot % VPH) * N + slot / VPH; };
 
-    const int nqv = a.nq * kRowVec, nkv = a.nk * kRowVec; // vectors per token
-    const size_t t0 = size_t(blockIdx.x) * tok_per_block;
-    const int ntok = int(min(size_t(tok_per_block), seq - t0));
-    const int end_q = ntok * nqv, end_k = end_q + ntok * nkv, items = end_k + ntok * nkv;
-    const int v_lane = threadIdx.x & (kRowVec - 1);
-    const size_t vq0 = t0 * size_t(nqv), vkv0 = t0 * size_t(nkv); // first vector of the block
-    const char *q_in = static_cast<const char *>(a.q_in) + vq0 * 16;
-    const char *k_in = static_cast<const char *>(a.k_in) + vkv0 * 16;
-    const char *v_in = static_cast<const char *>(a.v_in) + vkv0 * 16;
-    char *q_out = static_cast<char *>(a.q_out) + vq0 * 16;
-    int8_t *k_codes = a.k_codes + vkv0 * N, *v_codes = a.v_codes + vkv0 * N;
-    float *k_scale = a.k_scale + vkv0 / kRowVec, *v_scale = a.v_scale + vkv0 / kRowVec;
-
-    const AngleInputs ang0 = firstAngle(pos, t0, ntok, kHalf, ft); // before the item loads
-
-    // 1. issue this lane's loads (unconditional: idle lanes read the block's first q vector,
-    //    so the trig below can wait for its own inputs only)
-    v4u raw[IPT];
-    uint32_t rel[IPT]; // vector index within the block's range of its tensor
-    int tok[IPT], kind[IPT]; // kind: 0 = q, 1 = k, 2 = v
-#pragma unroll
-    for (int k = 0; k < IPT; ++k) {
-        const int it = threadIdx.x + k * 256;
-        kind[k] = it < end_q ? 0 : (it < end_k ? 1 : 2);
-        rel[k] = uint32_t(kind[k] == 0 ? it : (kind[k] == 1 ? it - end_q : it - end_k));
-        tok[k] = int(__umulhi(rel[k], kind[k] == 0 ? magic_q : magic_kv));
-        const char *src = it < items ? (kind[k] == 0 ? q_in : (kind[k] == 1 ? k_in : v_in)) + rel[k] * 16u : q_in;
-        raw[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
-    }
-
-    // 2. (cos, sin) of this block's tokens, while the loads are in flight
-    blockCosSin(cs, ang0, pos, t0, ntok, kHalf, ft);
-
-    // 3. rotate (q, k), quantize (k, v), store
-    const bool upper = v_lane >= VPH;
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = int(threadIdx.x) % kWave;
+    const size_t t0 = size_t(blockIdx.x) * (256 / kWave) + size_t(wave);
+    const bool live = t0 < seq;
+    const size_t t = live ? t0 : seq - 1;
+    const int nq = a.nq, nk = a.nk, rows = nq + 2 * nk;
+    const int rlane = lane / kRowVec, v_lane = lane % kRowVec;
     const int jv = v_lane & (VPH - 1);
-    const uint32_t flip = upper ? 0u : F::kSignBits; // first half: x*c + (-partner)*s
+    const bool lower = v_lane < VPH;
+    const char *q_in = static_cast<const char *>(a.q_in) + t * size_t(nq) * kRowBytes + v_lane * 16;
+    const char *k_in = static_cast<const char *>(a.k_in) + t * size_t(nk) * kRowBytes + v_lane * 16;
+    const char *v_in = static_cast<const char *>(a.v_in) + t * size_t(nk) * kRowBytes + v_lane * 16;
+    char *q_out = static_cast<char *>(a.q_out) + t * size_t(nq) * kRowBytes + v_lane * 16;
+    int8_t *k_codes = a.k_codes + t * size_t(nk) * kRowCodes + v_lane * N;
+    int8_t *v_codes = a.v_codes + t * size_t(nk) * kRowCodes + v_lane * N;
+    float *k_scale = a.k_scale + t * size_t(nk), *v_scale = a.v_scale + t * size_t(nk);
+
+    // the first frequency before the row loads (vector loads complete in issue order)
+    const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
+    __builtin_amdgcn_sched_barrier(0);
+    double c[N], sn[N];
+    int pass = 0;
+    do {
+        v4u raw[IPT];
 #pragma unroll
-    for (int k = 0; k < IPT; ++k) {
-        v4u other;
-        other.x = partnerOf<VPH>(raw[k].x) ^ flip;
-        other.y = partnerOf<VPH>(raw[k].y) ^ flip;
-        other.z = partnerOf<VPH>(raw[k].z) ^ flip;
-        other.w = partnerOf<VPH>(raw[k].w) ^ flip;
-        const int it = threadIdx.x + k * 256;
-        const bool active = it < items;
-        v4u out = raw[k];
-        if (active && kind[k] != 2) {
-            float x[N], p[N], y[N];
-            F::unpack(raw[k], x);
-            F::unpack(other, p);
-            const double2 *row = cs + tok[k] * kHalf + jv * N;
+        for (int k = 0; k < IPT; ++k) {
+            const int r = (pass * IPT + k) * kRows + rlane;
+            // rows past the token's last one read its first q row and store nothing
+            const char *src = r < nq ? q_in + size_t(r) * kRowBytes
+                              : r < nq + nk ? k_in + size_t(r - nq) * kRowBytes
+                              : r < rows ? v_in + size_t(r - nq - nk) * kRowBytes
+                                         : q_in;
+            raw[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
+        }
+        if (pass == 0) {
+            const int64_t p = pos[t];
+            bool far = false;
+            for (int sl = lane; sl < kHalf; sl += kWave) {
+                const int j = angleOf(sl);
+                const double ang = double(p) * (sl == lane ? f_first : ft.f[j]);
+                double s0 = 0.0, c0 = 0.0;
+                if (fabs(ang) <= kSincosFastLimit)
+                    sincosReduced(ang, &s0, &c0);
+                else
+                    far = true; // also NaN
+                cs[wave][sl] = make_double2(c0, s0);
+            }
+            if (__builtin_expect(__any(far), 0)) {
+                for (int sl = lane; sl < kHalf; sl += kWave) {
+                    const double ang = double(p) * ft.f[angleOf(sl)];
+                    if (!(fabs(ang) <= kSincosFastLimit)) {
+                        double s0, c0;
+                        librarySinCos(ang, &s0, &c0);
+                        cs[wave][sl] = make_double2(c0, s0);
+                    }
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
             for (int e = 0; e < N; ++e) {
-                const double c = row[e].x, sn = row[e].y;
-                y[e] = float(double(x[e]) * c + double(p[e]) * sn);
+                const double2 v = cs[wave][e * VPH + jv];
+                c[e] = v.x;
+                sn[e] = lower ? -v.y : v.y; // first half: x*c - partner*s
             }
-            out = F::packQ(y); // the element-type value llaisysROPE would store
         }
-        // quantizer input: the stored element values of the k / v row; amax as in
-        // quant.hip (integer max of magnitude bits, float rule for a row with a NaN)
-        using A = AbsBits<T>;
-        uint32_t bits = active && kind[k] != 0 ? A::finish(A::fold(0u, out)) : 0u;
-        bits = waveGroupReduce<kRowVec, MaxU32Op>(bits);
-        float val[N];
-        F::unpack(out, val);
-        float amax = A::value(bits);
-        if (__builtin_expect(bits > A::kInf, 0)) { // uniform over the row's lanes
-            amax = 0.0f;
 #pragma unroll
-            for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(val[e]));
+        for (int k = 0; k < IPT; ++k) {
+            v4u other;
+            other.x = partnerOf<VPH>(raw[k].x);
+            other.y = partnerOf<VPH>(raw[k].y);
+            other.z = partnerOf<VPH>(raw[k].z);
+            other.w = partnerOf<VPH>(raw[k].w);
+            const int r = (pass * IPT + k) * kRows + rlane;
+            const int kind = r < nq ? 0 : (r < nq + nk ? 1 : (r < rows ? 2 : 3)); // 3: none
+            v4u out = raw[k];
+            if (kind <= 1) {
+                float x[N], q[N], y[N];
+                F::unpack(raw[k], x);
+                F::unpack(other, q);
 #pragma unroll
-            for (int m = kRowVec / 2; m > 0; m >>= 1) amax = MaxOp::apply(amax, __shfl_xor(amax, m, kWave));
+                // the reference's two rounded f64 products and their rounded sum
+                // (rope_cpu.cpp:40-41), so k's codes are those of the reference's rope
+                for (int e = 0; e < N; ++e) y[e] = float(double(x[e]) * c[e] + double(q[e]) * sn[e]);
+                out = F::packQ(y); // the element-type value llaisysROPE would store
+            }
+            // k / v rows: quantizer input is the stored element values of the row; amax as
+            // in quant.hip (integer max of magnitude bits, float rule for a row with a NaN)
+            using A = AbsBits<T>;
+            uint32_t bits = kind == 1 || kind == 2 ? A::finish(A::fold(0u, out)) : 0u;
+            bits = waveGroupReduce<kRowVec, MaxU32Op>(bits);
+            float val[N];
+            F::unpack(out, val);
+            float amax = A::value(bits);
+            if (__builtin_expect(bits > A::kInf, 0)) { // uniform over the row's lanes
+                amax = 0.0f;
+#pragma unroll
+                for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(val[e]));
+#pragma unroll
+                for (int m = kRowVec / 2; m > 0; m >>= 1) amax = MaxOp::apply(amax, __shfl_xor(amax, m, kWave));
+            }
+            if (!live || kind == 3) continue;
+            if (kind == 0) {
+                __builtin_nontemporal_store(out, reinterpret_cast<v4u *>(q_out + size_t(r) * kRowBytes));
+            } else {
+                const int hr = kind == 1 ? r - nq : r - nq - nk; // head row within k / v
+                const RowQuantizer qz(amax);
+                uint32_t cd[N];
+                qz.codes<N, std::is_same_v<T, F32>>(val, cd);
+                storeCodes<N>(kind == 1 ? k_codes : v_codes, size_t(hr) * kRowCodes, cd);
+                if (v_lane == 0) (kind == 1 ? k_scale : v_scale)[hr] = qz.scale;
+            }
         }
-        if (!active) continue;
-        if (kind[k] == 0) {
-            __builtin_nontemporal_store(out, reinterpret_cast<v4u *>(q_out + rel[k] * 16u));
-        } else {
-            const RowQuantizer qz(amax);
-            uint32_t c[N];
-            qz.codes<N, std::is_same_v<T, F32>>(val, c);
-            storeCodes<N>(kind[k] == 1 ? k_codes : v_codes, size_t(rel[k]) * N, c);
-            if (v_lane == 0) (kind[k] == 1 ? k_scale : v_scale)[rel[k] >> kShift] = qz.scale;
-        }
-    }
+    } while (++pass < passes);
 }
 
 template <typename T, int IPT>
-void launchKvIpt(int vph, const RopeKvArgs &a, const int64_t *pos, size_t seq, size_t tpb,
-                 uint32_t magic_q, uint32_t magic_kv, const FreqTable &ft, hipStream_t s) {
-    const unsigned grid = blocksFor(seq, tpb);
+void launchKvWaveIpt(int vph, int passes, const RopeKvArgs &a, const int64_t *pos, size_t seq,
+                     const FreqTable &ft, hipStream_t s) {
+    const unsigned grid = blocksFor(seq, 256 / kWave);
     switch (vph) {
-    case 2: ropeKvVec<T, IPT, 2><<<grid, 256, 0, s>>>(a, pos, seq, int(tpb), magic_q, magic_kv, ft); break;
-    case 4: ropeKvVec<T, IPT, 4><<<grid, 256, 0, s>>>(a, pos, seq, int(tpb), magic_q, magic_kv, ft); break;
-    case 8: ropeKvVec<T, IPT, 8><<<grid, 256, 0, s>>>(a, pos, seq, int(tpb), magic_q, magic_kv, ft); break;
-    case 16: ropeKvVec<T, IPT, 16><<<grid, 256, 0, s>>>(a, pos, seq, int(tpb), magic_q, magic_kv, ft); break;
-    case 32: ropeKvVec<T, IPT, 32><<<grid, 256, 0, s>>>(a, pos, seq, int(tpb), magic_q, magic_kv, ft); break;
+    case 2: ropeKvWave<T, IPT, 2><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 4: ropeKvWave<T, IPT, 4><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 8: ropeKvWave<T, IPT, 8><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 16: ropeKvWave<T, IPT, 16><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 32: ropeKvWave<T, IPT, 32><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
     default: break;
+    }
+}
+
+template <typename T>
+void launchKvWave(int vph, const RopeKvArgs &a, const int64_t *pos, size_t seq, const FreqTable &ft,
+                  hipStream_t s) {
+    const int rows_per_instr = kWave / (2 * vph);
+    const int instr = (a.nq + 2 * a.nk + rows_per_instr - 1) / rows_per_instr;
+    const int passes = (instr + 3) / 4, ipt = (instr + passes - 1) / passes;
+    switch (ipt) {
+    case 1: launchKvWaveIpt<T, 1>(vph, passes, a, pos, seq, ft, s); break;
+    case 2: launchKvWaveIpt<T, 2>(vph, passes, a, pos, seq, ft, s); break;
+    case 3: launchKvWaveIpt<T, 3>(vph, passes, a, pos, seq, ft, s); break;
+    default: launchKvWaveIpt<T, 4>(vph, passes, a, pos, seq, ft, s); break;
     }
 }
 
@@ -171,21 +228,8 @@ bool launchKv(const RopeKvArgs &a, const int64_t *pos, size_t seq, size_t d, flo
         if (!aligned16(p)) return false;
     if (reinterpret_cast<uintptr_t>(a.k_codes) % N || reinterpret_cast<uintptr_t>(a.v_codes) % N)
         return false;
-    const size_t per_tok = (size_t(a.nq) + 2 * size_t(a.nk)) * 2 * vph;
-    if (per_tok == 0 || per_tok > size_t(256 * kMaxItemsKv)) return false;
-    const size_t tpb = tokensPerBlock(per_tok, half, 256 * kMaxItemsKv);
-    const int ipt = int((tpb * per_tok + 255) / 256);
-    const auto magicOf = [&](int heads) {
-        return heads ? uint32_t((uint64_t(1) << 32) / (size_t(heads) * 2 * vph) + 1) : 0u;
-    };
-    const uint32_t magic_q = magicOf(a.nq), magic_kv = magicOf(a.nk);
-    const FreqTable ft = hostFreqs(d, theta);
-    switch (ipt) {
-    case 1: launchKvIpt<T, 1>(int(vph), a, pos, seq, tpb, magic_q, magic_kv, ft, s); break;
-    case 2: launchKvIpt<T, 2>(int(vph), a, pos, seq, tpb, magic_q, magic_kv, ft, s); break;
-    case 3: launchKvIpt<T, 3>(int(vph), a, pos, seq, tpb, magic_q, magic_kv, ft, s); break;
-    default: launchKvIpt<T, 4>(int(vph), a, pos, seq, tpb, magic_q, magic_kv, ft, s); break;
-    }
+    if (a.nq + 2 * a.nk == 0) return false;
+    launchKvWave<T>(int(vph), a, pos, seq, hostFreqs(d, theta), s);
     return true;
 }
 
