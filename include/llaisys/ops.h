@@ -124,6 +124,19 @@ __C {
                                              llaisysTensor_t k_codes, llaisysTensor_t k_scale,
                                              llaisysTensor_t v_codes, llaisysTensor_t v_scale,
                                              float scale);
+    /* No counterpart in the reference: llaisysSelfAttentionInt8KV for callers that cannot
+     * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+     * that forbid hipMalloc).  Same arguments, checks and result bits as
+     * llaisysSelfAttentionInt8KV, but its split partials go to a file-scope device scratch
+     * of 24 MiB per GPU (held until the process ends) instead of the library workspace, and
+     * it calls no allocator.  A call whose partials exceed the scratch -- queries x q heads x
+     * (head_dim + 2) x 4 KiB, e.g. more than 47 query-heads at head_dim 128 -- fails with a
+     * message.  Calls on one GPU share the scratch: calls that overlap (other threads or
+     * streams) race. */
+    __export void llaisysSelfAttentionInt8KVNoAlloc(llaisysTensor_t attn_val, llaisysTensor_t q,
+                                                    llaisysTensor_t k_codes, llaisysTensor_t k_scale,
+                                                    llaisysTensor_t v_codes, llaisysTensor_t v_scale,
+                                                    float scale);
     /* llaisysLinear with INT8 weights (no reference counterpart; the decoder's projections,
      * src/models/qwen2/components.hpp:114, with weights quantized by llaisysQuantizeInt8 per output row):
      * w_codes [N, K] I8, w_scale [N] F32, in / out / bias of one float dtype;

@@ -195,6 +195,14 @@ __C {
         llaisys::ops::selfAttentionInt8KV(attn_val->tensor, q->tensor, k_codes->tensor,
                                           k_scale->tensor, v_codes->tensor, v_scale->tensor, scale);
     }
+    void llaisysSelfAttentionInt8KVNoAlloc(llaisysTensor_t attn_val, llaisysTensor_t q,
+                                           llaisysTensor_t k_codes, llaisysTensor_t k_scale,
+                                           llaisysTensor_t v_codes, llaisysTensor_t v_scale,
+                                           float scale) {
+        llaisys::ops::selfAttentionInt8KVNoAlloc(attn_val->tensor, q->tensor, k_codes->tensor,
+                                                 k_scale->tensor, v_codes->tensor, v_scale->tensor,
+                                                 scale);
+    }
     void llaisysDequantizeInt8Pair(llaisysTensor_t out0, llaisysTensor_t q0, llaisysTensor_t scale0,
                                    llaisysTensor_t out1, llaisysTensor_t q1, llaisysTensor_t scale1) {
         llaisys::ops::dequantizeInt8Pair(out0->tensor, q0->tensor, scale0->tensor, out1->tensor,

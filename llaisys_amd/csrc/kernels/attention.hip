@@ -35,6 +35,8 @@
 #include "rowplan.hpp"
 
 #include <algorithm>
+#include <cstdio>
+#include <mutex>
 #include <cmath>
 #include <type_traits>
 
@@ -976,6 +978,39 @@ void dispatch(AttnArgs a, int d, int dv, llaisysDataType_t dt, void *ws, size_t 
 }
 
 } // namespace
+
+// ---- scratch of the allocation-free entry point -----------------------------------------
+// File-scope device array holding the split attention's partials for
+// llaisysSelfAttentionInt8KVNoAlloc.  Each GPU the library runs on holds its own copy (at its
+// own address) until the process ends.  In host code the name `scratch` is only a stand-in:
+// its device address comes from hipGetSymbolAddress, resolved once per device with that
+// device current, and only that address is ever handed to kernels.  Nothing in it needs to
+// start at zero: every partial a launch reads was written earlier in the same launch pair.
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kScratchDevices] = {};
+} // namespace
+
+void *noAllocScratch(int device, char *err, size_t err_len) {
+    if (device < 0 || device >= kScratchDevices) {
+        snprintf(err, err_len, "device id %d out of range", device);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void *ptr = nullptr;
+        const hipError_t st = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (st != hipSuccess || ptr == nullptr) {
+            snprintf(err, err_len, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(st));
+            return nullptr;
+        }
+        g_scratch_ptr[device] = ptr;
+    }
+    return g_scratch_ptr[device];
+}
 
 size_t selfAttentionWorkspaceBytes(size_t seq, size_t nh, size_t head_dim) {
     // up to 1024 partials of head_dim + 2 floats per (query, head), capped at 64 MiB: a

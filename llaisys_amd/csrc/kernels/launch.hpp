@@ -95,6 +95,13 @@ void dequantizeInt8Pair(void *out0, const int8_t *q0, const float *scale0, size_
 // scale per (token, kv head) row.  `ws` (ws_bytes) holds the partials of a split launch;
 // selfAttentionWorkspaceBytes(seq, nh, d) lets it split decode launches fully.
 size_t selfAttentionWorkspaceBytes(size_t seq, size_t nh, size_t head_dim);
+
+// Scratch of the allocation-free attention entry point: a file-scope device array of
+// kNoAllocScratchBytes per GPU.  noAllocScratch returns its device address on `device`
+// (which must be current), resolved once per device by hipGetSymbolAddress; on failure it
+// returns null and writes the reason to err.
+constexpr size_t kNoAllocScratchBytes = size_t(24) << 20;
+void *noAllocScratch(int device, char *err, size_t err_len);
 void selfAttention(void *out, const void *q, const void *k, const void *v, const float *k_scale,
                    const float *v_scale, size_t seq, size_t total, size_t nh, size_t nkvh,
                    size_t d, size_t dv, float scale, llaisysDataType_t dt, void *ws,

@@ -366,8 +366,9 @@ void selfAttention(tensor_t attn_val, tensor_t q, tensor_t k, tensor_t v, float 
 
 // Attention over an INT8 cache: the composition dequantizeInt8 (into q's dtype) then
 // selfAttention, reading the caches as codes.
-void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor_t k_scale,
-                         tensor_t v_codes, tensor_t v_scale, float scale) {
+namespace {
+void checkAttentionInt8KV(const tensor_t &attn_val, const tensor_t &q, const tensor_t &k_codes,
+                          const tensor_t &k_scale, const tensor_t &v_codes, const tensor_t &v_scale) {
     CHECK_SAME_DEVICE(attn_val, q, k_codes, v_codes);
     CHECK_SAME_DEVICE(q, k_scale, v_scale);
     checkAttention(attn_val, q, k_codes, v_codes);
@@ -382,10 +383,43 @@ void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor
     ASSERT(k_scale->ndim() == 2 && k_scale->shape()[0] == total && k_scale->shape()[1] == nkvh &&
                v_scale->ndim() == 2 && v_scale->shape()[0] == total && v_scale->shape()[1] == nkvh,
            "SelfAttentionInt8KV: scales must be [total_len, kv_head]");
+}
+} // namespace
+
+void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor_t k_scale,
+                         tensor_t v_codes, tensor_t v_scale, float scale) {
+    checkAttentionInt8KV(attn_val, q, k_codes, k_scale, v_codes, v_scale);
     launchAttention(attn_val, q, k_codes, v_codes, reinterpret_cast<const float *>(k_scale->data()),
                     reinterpret_cast<const float *>(v_scale->data()), scale);
 }
 
+// The same op with its split partials in the library's file-scope device scratch
+// (kernels::kNoAllocScratchBytes per GPU) instead of the workspace: nothing is allocated.
+// It launches exactly the kernels selfAttentionInt8KV launches (same chunking, so the same
+// bits), and rejects calls whose partials would not fit.  Calls on one GPU share the
+// scratch: overlapping calls (several threads or streams) race.
+void selfAttentionInt8KVNoAlloc(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor_t k_scale,
+                                tensor_t v_codes, tensor_t v_scale, float scale) {
+    checkAttentionInt8KV(attn_val, q, k_codes, k_scale, v_codes, v_scale);
+    const size_t seq = q->shape()[0], nh = q->shape()[1], d = q->shape()[2];
+    const size_t need = kernels::selfAttentionWorkspaceBytes(seq, nh, d);
+    if (need > kernels::kNoAllocScratchBytes)
+        LLAISYS_FAIL(std::invalid_argument,
+                     "SelfAttentionInt8KVNoAlloc: the call needs " << need << " bytes of scratch, more than the "
+                         << kernels::kNoAllocScratchBytes << " it holds (queries x heads x (head_dim + 2) x 4 KiB); "
+                            "use llaisysSelfAttentionInt8KV",
+                     "scratch too small");
+    auto s = streamFor(q); // makes q's device current
+    char err[256] = {};
+    void *ws = kernels::noAllocScratch(q->deviceId(), err, sizeof err);
+    if (!ws) LLAISYS_FAIL(std::runtime_error, "SelfAttentionInt8KVNoAlloc: " << err, "no scratch");
+    kernels::selfAttention(attn_val->data(), q->data(), k_codes->data(), v_codes->data(),
+                           reinterpret_cast<const float *>(k_scale->data()),
+                           reinterpret_cast<const float *>(v_scale->data()), seq, k_codes->shape()[0],
+                           nh, k_codes->shape()[1], d, v_codes->shape()[2], scale, q->dtype(), ws,
+                           need, s);
+    launched("selfAttentionInt8KVNoAlloc");
+}
 
 // reference src/ops/rearrange/op.cpp:4-6 (a stub there): out[i] = in[i] for every
 // multi-index, between any two layouts of one shape (Tensor::copyInto on the GPU).

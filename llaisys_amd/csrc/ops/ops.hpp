@@ -24,6 +24,8 @@ void kvAppendInt8Pair(tensor_t k_cache, tensor_t k_scale, tensor_t v_cache, tens
 void selfAttention(tensor_t attn_val, tensor_t q, tensor_t k, tensor_t v, float scale);
 void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor_t k_scale,
                          tensor_t v_codes, tensor_t v_scale, float scale);
+void selfAttentionInt8KVNoAlloc(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor_t k_scale,
+                                tensor_t v_codes, tensor_t v_scale, float scale);
 void dequantizeInt8Pair(tensor_t out0, tensor_t q0, tensor_t scale0, tensor_t out1, tensor_t q1,
                         tensor_t scale1);
 void linear(tensor_t out, tensor_t in, tensor_t weight, tensor_t bias);

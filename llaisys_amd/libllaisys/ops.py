@@ -33,6 +33,7 @@ ADDED_OPS = {
     "llaisysKVAppendInt8Pair": [T, T, T, T, T, T, c_size_t],
     "llaisysDequantizeInt8Pair": [T, T, T, T, T, T],
     "llaisysSelfAttentionInt8KV": [T, T, T, T, T, T, c_float],
+    "llaisysSelfAttentionInt8KVNoAlloc": [T, T, T, T, T, T, c_float],
     "llaisysLinearW8A16": [T, T, T, T, T],
     "llaisysRandomSample": [T, T, c_float, c_int64, c_float, c_uint64],
     "llaisysRmsNormLinear": [T, T, T, T, T, c_float, T, T, T, c_uint8],

@@ -108,6 +108,16 @@ class Ops:
                                                c_float(scale))
 
     @staticmethod
+    def self_attention_int8kv_noalloc(attn_val: Tensor, q: Tensor, k_codes: Tensor, k_scale: Tensor,
+                                      v_codes: Tensor, v_scale: Tensor, scale: float):
+        """self_attention_int8kv without allocating: partials in the library's fixed device
+        scratch (llaisysSelfAttentionInt8KVNoAlloc)."""
+        LIB_LLAISYS.llaisysSelfAttentionInt8KVNoAlloc(attn_val.lib_tensor(), q.lib_tensor(),
+                                                      k_codes.lib_tensor(), k_scale.lib_tensor(),
+                                                      v_codes.lib_tensor(), v_scale.lib_tensor(),
+                                                      c_float(scale))
+
+    @staticmethod
     def dequantize_int8_pair(out0: Tensor, q0: Tensor, scale0: Tensor, out1: Tensor, q1: Tensor,
                              scale1: Tensor):
         LIB_LLAISYS.llaisysDequantizeInt8Pair(out0.lib_tensor(), q0.lib_tensor(),
