@@ -137,6 +137,14 @@ __C {
                                                     llaisysTensor_t k_codes, llaisysTensor_t k_scale,
                                                     llaisysTensor_t v_codes, llaisysTensor_t v_scale,
                                                     float scale);
+    /* Device-side dtype conversion: out[i] = cast<out dtype>(in[i]) with the reference's
+     * cast<To>(From) (src/utils/types.hpp:116-139: through f32; f32 -> bf16 rounds half to
+     * even by "+0x7FFF + lsb" with no NaN case, f32 -> f16 truncates, widening is exact,
+     * equal types copy the bits).  out and in: same shape, contiguous, F32 / BF16 / F16,
+     * same device.  It replaces the reference loader's host upcast of bf16 / f16 weights to
+     * f32 (python/llaisys/models/qwen2.py:118-120): weights stay bf16 in HBM, uploaded as
+     * bf16 bits, or as f32 and cast here. */
+    __export void llaisysCast(llaisysTensor_t out, llaisysTensor_t in);
     /* llaisysLinear with INT8 weights (no reference counterpart; the decoder's projections,
      * src/models/qwen2/components.hpp:114, with weights quantized by llaisysQuantizeInt8 per output row):
      * w_codes [N, K] I8, w_scale [N] F32, in / out / bias of one float dtype;

@@ -203,6 +203,9 @@ __C {
                                                  k_scale->tensor, v_codes->tensor, v_scale->tensor,
                                                  scale);
     }
+    void llaisysCast(llaisysTensor_t out, llaisysTensor_t in) {
+        llaisys::ops::cast(out->tensor, in->tensor);
+    }
     void llaisysDequantizeInt8Pair(llaisysTensor_t out0, llaisysTensor_t q0, llaisysTensor_t scale0,
                                    llaisysTensor_t out1, llaisysTensor_t q1, llaisysTensor_t scale1) {
         llaisys::ops::dequantizeInt8Pair(out0->tensor, q0->tensor, scale0->tensor, out1->tensor,

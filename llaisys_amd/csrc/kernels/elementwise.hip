@@ -1,4 +1,4 @@
-// Streaming element-wise kernels for gfx950: swiglu, add, INT8 dequantize.
+// Streaming element-wise kernels for gfx950: swiglu, add, INT8 dequantize, dtype cast.
 //
 // swiglu follows src/ops/swiglu/cpu/swiglu_cpu.cpp:15-20: out = T(u * (g / (1 + exp(-g))))
 // in f32.  exp is the hardware exp2 of -g*log2(e) and the quotient is the hardware
@@ -201,6 +201,69 @@ void launchDequant(const DequantArgs &a0, const DequantArgs &a1, size_t cols, hi
     }
 }
 
+// ---- dtype conversion ---------------------------------------------------------------------
+// out[i] = cast<To>(in[i]) as the reference's types.hpp:116-139: through f32, with the
+// reference rules (Fmt<T>::unpack / pack: bf16 round-half-even without a NaN case, f16
+// truncation).  pack, not packQ: the inputs are caller data whose NaN payloads the
+// hardware converter would not round like the reference.  Eight elements per lane: one
+// or two 16-byte loads, one or two 16-byte stores.
+
+template <typename T>
+__device__ __forceinline__ void load8(const void *p, size_t i, float *f) {
+    if constexpr (Fmt<T>::kVec == 8) {
+        Fmt<T>::unpack(load16Stream<T>(p, i), f);
+    } else {
+        Fmt<T>::unpack(load16Stream<T>(p, i), f);
+        Fmt<T>::unpack(load16Stream<T>(p, i + 4), f + 4);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(void *p, size_t i, const float *f) {
+    if constexpr (Fmt<T>::kVec == 8) {
+        store16Stream<T>(p, i, Fmt<T>::pack(f));
+    } else {
+        store16Stream<T>(p, i, Fmt<T>::pack(f));
+        store16Stream<T>(p, i + 4, Fmt<T>::pack(f + 4));
+    }
+}
+
+template <typename To, typename From>
+__global__ void __launch_bounds__(256) castVec(void *__restrict__ out, const void *__restrict__ in, size_t n8) {
+    const size_t k = size_t(blockIdx.x) * 256 + threadIdx.x;
+    if (k >= n8) return;
+    float f[8];
+    load8<From>(in, k * 8, f);
+    store8<To>(out, k * 8, f);
+}
+
+template <typename To, typename From>
+__global__ void __launch_bounds__(256) castScalar(void *out, const void *in, size_t n) {
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256)
+        Fmt<To>::put(out, i, Fmt<From>::get(in, i));
+}
+
+template <typename To, typename From>
+void launchCast(void *out, const void *in, size_t n, hipStream_t s) {
+    if (n == 0) return;
+    if (n % 8 == 0 && aligned16(out) && aligned16(in)) {
+        castVec<To, From><<<blocksFor(n / 8, 256), 256, 0, s>>>(out, in, n / 8);
+        return;
+    }
+    const unsigned grid = unsigned(std::min<size_t>(blocksFor(n, 256), 1u << 20));
+    castScalar<To, From><<<grid, 256, 0, s>>>(out, in, n);
+}
+
+template <typename To>
+void castFrom(void *out, const void *in, llaisysDataType_t in_dt, size_t n, hipStream_t s) {
+    switch (in_dt) {
+    case LLAISYS_DTYPE_F32: return launchCast<To, F32>(out, in, n, s);
+    case LLAISYS_DTYPE_BF16: return launchCast<To, BF16>(out, in, n, s);
+    case LLAISYS_DTYPE_F16: return launchCast<To, F16>(out, in, n, s);
+    default: return;
+    }
+}
+
 } // namespace
 
 void swiglu(void *out, const void *gate, const void *up, size_t n, llaisysDataType_t dt,
@@ -227,6 +290,16 @@ void dequantizeInt8Pair(void *out0, const int8_t *q0, const float *scale0, size_
 void dequantizeInt8(void *out, const int8_t *q, const float *scale, size_t rows, size_t cols,
                     llaisysDataType_t dt, hipStream_t s) {
     dequantizeInt8Pair(out, q, scale, rows, nullptr, nullptr, nullptr, 0, cols, dt, s);
+}
+
+void cast(void *out, llaisysDataType_t out_dt, const void *in, llaisysDataType_t in_dt, size_t n,
+          hipStream_t s) {
+    switch (out_dt) {
+    case LLAISYS_DTYPE_F32: return castFrom<F32>(out, in, in_dt, n, s);
+    case LLAISYS_DTYPE_BF16: return castFrom<BF16>(out, in, in_dt, n, s);
+    case LLAISYS_DTYPE_F16: return castFrom<F16>(out, in, in_dt, n, s);
+    default: return;
+    }
 }
 
 } // namespace llaisys::kernels

@@ -38,6 +38,11 @@ bool ropeKvAppendFused(void *q_out, const void *q_in, size_t nh_q, const void *k
                        size_t head_dim, float theta, llaisysDataType_t dt, hipStream_t stream);
 size_t ropeKvAppendWorkspaceBytes(size_t seq, size_t nh_kv, size_t head_dim, llaisysDataType_t dt);
 
+// out[i] = cast<out type>(in[i]) over n elements of F32 / BF16 / F16, through f32 with the
+// reference's rounding rules (types.hpp:116-139); the caller copies equal types itself.
+void cast(void *out, llaisysDataType_t out_dt, const void *in, llaisysDataType_t in_dt, size_t n,
+          hipStream_t stream);
+
 // out = up * gate / (1 + exp(-gate)) over n elements.
 void swiglu(void *out, const void *gate, const void *up, size_t n, llaisysDataType_t dt,
             hipStream_t stream);

@@ -198,6 +198,29 @@ void ropeQK(tensor_t q_out, tensor_t q_in, tensor_t k_out, tensor_t k_in, tensor
     launched("ropeQK");
 }
 
+// Device-side dtype conversion (no reference op; it replaces the reference loader's host
+// upcast of every bf16 / f16 weight to f32, python/llaisys/models/qwen2.py:118-120, and
+// follows its cast<To>(From), src/utils/types.hpp:116-139): out[i] = cast(in[i]), same
+// shape, contiguous, F32 / BF16 / F16.
+void cast(tensor_t out, tensor_t in) {
+    CHECK_SAME_DEVICE(out, in);
+    CHECK_SAME_SHAPE(out->shape(), in->shape());
+    ASSERT(out->isContiguous() && in->isContiguous(), "Cast: tensors must be contiguous");
+    requireFloat(out->dtype());
+    requireFloat(in->dtype());
+    auto s = streamFor(out);
+    const size_t n = out->numel();
+    if (out->dtype() == in->dtype()) { // cast<T>(T) is the value itself
+        if (n && out->data() != in->data())
+            device::amd::check(hipMemcpyAsync(out->data(), in->data(), n * out->elementSize(),
+                                              hipMemcpyDeviceToDevice, s),
+                               "hipMemcpyAsync(cast)");
+        return;
+    }
+    kernels::cast(out->data(), out->dtype(), in->data(), in->dtype(), n, s);
+    launched("cast");
+}
+
 // reference src/ops/swiglu/op.cpp:7-38
 void swiglu(tensor_t out, tensor_t gate, tensor_t up) {
     CHECK_SAME_DEVICE(out, gate, up);

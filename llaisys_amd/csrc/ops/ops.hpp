@@ -15,6 +15,7 @@ void addRmsNorm(tensor_t out, tensor_t residual_out, tensor_t in, tensor_t resid
 void rope(tensor_t out, tensor_t in, tensor_t pos_ids, float theta);
 void ropeQK(tensor_t q_out, tensor_t q_in, tensor_t k_out, tensor_t k_in, tensor_t pos_ids,
             float theta);
+void cast(tensor_t out, tensor_t in);
 void swiglu(tensor_t out, tensor_t gate, tensor_t up);
 void quantizeInt8(tensor_t q, tensor_t scale, tensor_t in);
 void dequantizeInt8(tensor_t out, tensor_t q, tensor_t scale);

@@ -34,6 +34,7 @@ ADDED_OPS = {
     "llaisysDequantizeInt8Pair": [T, T, T, T, T, T],
     "llaisysSelfAttentionInt8KV": [T, T, T, T, T, T, c_float],
     "llaisysSelfAttentionInt8KVNoAlloc": [T, T, T, T, T, T, c_float],
+    "llaisysCast": [T, T],
     "llaisysLinearW8A16": [T, T, T, T, T],
     "llaisysRandomSample": [T, T, c_float, c_int64, c_float, c_uint64],
     "llaisysRmsNormLinear": [T, T, T, T, T, c_float, T, T, T, c_uint8],

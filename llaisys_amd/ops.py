@@ -1,8 +1,8 @@
 """Ops: the LLAISYS operators as static methods.
 
-The nine reference methods match python/llaisys/ops.py:6-55 (rearrange raises in this
-library, as the reference's own C++ rearrange does); the rest wrap the additive entry points of
-include/llaisys/ops.h.
+The nine reference methods match python/llaisys/ops.py:6-55 (rearrange is implemented here:
+a strided copy between two layouts of one shape, where the reference's C++ rearrange is a
+stub); the rest wrap the additive entry points of include/llaisys/ops.h.
 """
 from ctypes import c_float, c_int64, c_size_t, c_uint8, c_uint64
 
@@ -116,6 +116,11 @@ class Ops:
                                                       k_codes.lib_tensor(), k_scale.lib_tensor(),
                                                       v_codes.lib_tensor(), v_scale.lib_tensor(),
                                                       c_float(scale))
+
+    @staticmethod
+    def cast(out: Tensor, inp: Tensor):
+        """out = cast(inp) on the device with the reference's conversion rules (llaisysCast)."""
+        LIB_LLAISYS.llaisysCast(out.lib_tensor(), inp.lib_tensor())
 
     @staticmethod
     def dequantize_int8_pair(out0: Tensor, q0: Tensor, scale0: Tensor, out1: Tensor, q1: Tensor,

@@ -49,6 +49,7 @@ def lib():
             "orc_linear_w8a16": [P, P, P, P, P, c_size_t, c_size_t, c_size_t, c_int],
             "orc_random_sample": [P, P, c_size_t, c_size_t, c_int, c_float, ctypes.c_int64, c_float,
                                   ctypes.c_uint64],
+            "orc_cast": [P, c_int, P, c_int, c_size_t],
         }
         for name, args in sig.items():
             fn = getattr(L, name)
@@ -86,6 +87,18 @@ def _code(a):
 
 def _c(a):
     return np.ascontiguousarray(a)
+
+
+_NP_OF = {F32: np.float32, F16: np.float16, BF16: np.uint16}
+
+
+def cast(x, out_code):
+    """The reference's cast<To>(From) (types.hpp:116-139) of every element of x (host
+    formats: bf16 as uint16 bits) into out_code (F32 / F16 / BF16)."""
+    x = _c(x)
+    out = np.empty(x.shape, dtype=_NP_OF[out_code])
+    lib().orc_cast(_p(out), out_code, _p(x), _code(x), x.size)
+    return out
 
 
 def add(a, b):

@@ -374,6 +374,19 @@ void orc_linear_w8a16(void *out, const void *x, const int8_t *code, const float 
         }
 }
 
+/* ---- dtype conversion (the reference's cast<To>(From), types.hpp:116-139) -------------
+ * Same type: the value itself (bit copy).  Otherwise through f32 with the rules above:
+ * bf16 -> f32 and f16 -> f32 exact, f32 -> bf16 round-half-even by "+0x7FFF + lsb" with no
+ * NaN case (types.cpp:74-84), f32 -> f16 truncating (types.cpp:55). */
+void orc_cast(void *out, int out_dt, const void *in, int in_dt, size_t n) {
+    const size_t es = in_dt == ORC_F32 ? 4 : 2;
+    if (out_dt == in_dt) {
+        memcpy(out, in, n * es);
+        return;
+    }
+    for (size_t i = 0; i < n; i++) st(out, i, out_dt, ld(in, i, in_dt));
+}
+
 /* ---- random sampling (no reference kernel; rule in oracle.h) ------------------------- */
 
 uint64_t orc_splitmix64(uint64_t x) {

@@ -25,6 +25,8 @@ uint16_t orc_f32_to_bf16(float v);
 float orc_bf16_to_f32(uint16_t v);
 uint16_t orc_f32_to_f16(float v);
 float orc_f16_to_f32(uint16_t v);
+/* out[i] = cast<out type>(in[i]) as the reference's types.hpp:116-139 (through f32) */
+void orc_cast(void *out, int out_dtype, const void *in, int in_dtype, size_t n);
 
 void orc_add(void *c, const void *a, const void *b, size_t n, int dtype);
 void orc_rms_norm(void *out, const void *in, const void *w, size_t rows, size_t cols,

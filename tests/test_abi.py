@@ -179,6 +179,9 @@ def _run(code):
     ("L.Ops.kv_append_int8(t((4,2,8), L.DataType.I8), t((4,2)), t((3,2,8)), 2)", "append past the cache end"),
     ("L.Ops.quantize_int8(t((4,8), L.DataType.I8), t((3,)), t((4,8)))", "one scale per last-dim row"),
     ("L.Tensor((2,), L.DataType.F32, L.DeviceType.AMD, 0)", "invalid device id"),
+    ("L.Ops.cast(t((2,2), L.DataType.BF16), t((2,2)))", "Unsupported device"),
+    ("L.Ops.cast(t((2,3), L.DataType.BF16), t((2,2)))", "Shapes mismatch"),
+    ("L.Ops.cast(t((2,2), L.DataType.I32), t((2,2)))", "Unsupported data type"),
     # 48 query-heads of head_dim 128 need 25.6 MB of partials: beyond the fixed 24 MiB scratch
     ("I8 = L.DataType.I8; L.Ops.self_attention_int8kv_noalloc(t((48,1,128)), t((48,1,128)), t((4,1,128), I8), "
      "t((4,1)), t((4,1,128), I8), t((4,1)), 0.1)", "more than the 25165824 it holds"),

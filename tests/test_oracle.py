@@ -568,3 +568,32 @@ def test_random_sample_distribution():
         probs[order[:keep]] = pr[:keep] / pr[:keep].sum()
         counts = np.bincount([oracle.random_sample(x, T, k, p, s)[0] for s in range(n)], minlength=len(x))
         assert _chi2_ok(counts, probs, n), (T, k, p, counts, probs * n)
+
+
+def test_cast_is_the_reference_conversions_composed():
+    """orc_cast (types.hpp:116-139) against the pinned scalar rules, composed in numpy:
+    f32 -> bf16 round-half-even without a NaN case, f32 -> f16 truncation, exact widening,
+    identity for equal types; special values and ties included."""
+    rng = np.random.default_rng(51)
+    f = (rng.standard_normal(4000) * 10.0 ** rng.integers(-8, 8, 4000)).astype(np.float32)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, 1e-40, -3e-45, 65504.0, 65520.0, 1e6],
+                       np.float32)
+    raw = np.array([0x7FC00001, 0x7F800001, 0xFFC00000, 0x3F808000, 0x3F818000, 0x3F807FFF],
+                   np.uint32).view(np.float32)
+    f = np.concatenate([f, special, raw])
+    bf = oracle.cast(f, oracle.BF16)
+    assert np.array_equal(bf, f32_to_bf16(f))
+    assert np.array_equal(oracle.cast(bf, oracle.F32).view(np.uint32), bf16_to_f32(bf).view(np.uint32))
+    h = oracle.cast(f, oracle.F16)
+    exp_h = np.array([oracle.lib().orc_f32_to_f16(float(v)) for v in f], np.uint16)
+    assert np.array_equal(h.view(np.uint16), exp_h)
+    assert h.view(np.uint16)[np.where(f == np.float32(65520.0))[0][0]] == 0x7BFF  # truncates, no overflow to inf
+    wide = np.array([oracle.lib().orc_f16_to_f32(int(v)) for v in h.view(np.uint16)], np.float32)
+    assert np.array_equal(oracle.cast(h, oracle.F32).view(np.uint32), wide.view(np.uint32))
+    # bf16 <-> f16 go through f32
+    assert np.array_equal(oracle.cast(bf, oracle.F16).view(np.uint16),
+                          oracle.cast(bf16_to_f32(bf), oracle.F16).view(np.uint16))
+    assert np.array_equal(oracle.cast(h, oracle.BF16), f32_to_bf16(oracle.cast(h, oracle.F32)))
+    for a in (f, bf, h):  # same type: the bits themselves
+        code = {np.float32: oracle.F32, np.uint16: oracle.BF16, np.float16: oracle.F16}[a.dtype.type]
+        assert np.array_equal(oracle.cast(a, code).view(np.uint8), a.view(np.uint8))
