@@ -102,6 +102,27 @@ void dispatchBinary(void *out, const void *a, const void *b, size_t n, llaisysDa
 
 // ---- INT8 dequantize --------------------------------------------------------------------
 
+// One output vector of code * sc.  packQ rounds every non-NaN product like the reference;
+// with a NaN scale (caller data) every product is the same quieted NaN, whose reference
+// rounding (pack) is one value per lane, selected word by word.  Branch-free on purpose: a
+// divergent branch around the stores measured 40 % slower on the whole kernel (13.9 vs
+// 9.8 us, W[8960, 1536]).
+template <typename T>
+__device__ __forceinline__ v4u packScaled(const float *f, float sc) {
+    using F = Fmt<T>;
+    v4u r = F::packQ(f);
+    if constexpr (F::kBytes == 2) {
+        const uint32_t h = F::pack(f).x & 0xFFFFu; // the exact rounding of the lane's NaN
+        const uint32_t nanw = h | (h << 16);
+        const bool nan = sc != sc;
+        r.x = nan ? nanw : r.x;
+        r.y = nan ? nanw : r.y;
+        r.z = nan ? nanw : r.z;
+        r.w = nan ? nanw : r.w;
+    }
+    return r;
+}
+
 // N codes (one output vector) per lane: 8 bytes of codes for 16-bit outputs, 4 for f32.
 template <int N>
 __device__ __forceinline__ void loadCodes(const int8_t *q, size_t i, float *f) {
@@ -154,11 +175,39 @@ __global__ void __launch_bounds__(256)
             const float sc = scale[rowdiv.div(i)];
 #pragma unroll
             for (int e = 0; e < N; ++e) f[e] = f[e] * sc;
-            // a NaN scale is caller data whose payload packQ would not round like the
-            // reference; such vectors take the exact rounding
-            store16Stream<T>(out, i * N, sc == sc ? F::packQ(f) : F::pack(f));
+            store16Stream<T>(out, i * N, packScaled<T>(f, sc));
         }
     }
+}
+
+// 16 codes per lane (one 16-byte load, 16 / N output vectors): for rows whose length is a
+// multiple of 16.  Measured on MI355X (W[8960, 1536] bf16, >= 1 GiB of rotating sets):
+// 9.8 us against 11.3 us for 8 codes x 4 per lane; a copy kernel with the same traffic
+// (read 1 : write 2 bytes, 41 MB) takes 9.7 us, so this is the write-heavy stream's floor.
+template <typename T>
+__global__ void __launch_bounds__(256)
+    dequantVec16(DequantJobs jobs, DivU64 rowdiv) {
+    using F = Fmt<T>;
+    constexpr int N = F::kVec;
+    const bool second = blockIdx.x >= jobs.nb0; // block-uniform
+    void *__restrict__ out = second ? jobs.job[1].out : jobs.job[0].out;
+    const int8_t *__restrict__ q = second ? jobs.job[1].q : jobs.job[0].q;
+    const float *__restrict__ scale = second ? jobs.job[1].scale : jobs.job[0].scale;
+    const size_t n16 = second ? jobs.job[1].nvec : jobs.job[0].nvec; // 16-code units
+    const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
+    const size_t i = size_t(blk) * 256 + threadIdx.x;
+    if (i >= n16) return;
+    const v4u c = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(q + i * 16));
+    const float sc = scale[rowdiv.div(i)];
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    float f[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f[4 * j + e] = float(int8_t(w[j] >> (8 * e))) * sc;
+#pragma unroll
+    for (int o = 0; o < 16 / N; ++o)
+        store16Stream<T>(out, i * 16 + size_t(o) * N, packScaled<T>(f + o * N, sc));
 }
 
 template <typename T>
@@ -183,6 +232,20 @@ void launchDequant(const DequantArgs &a0, const DequantArgs &a1, size_t cols, hi
     const auto vecOk = [&](const DequantArgs &a) {
         return a.rows == 0 || (aligned16(a.out) && reinterpret_cast<uintptr_t>(a.q) % N == 0);
     };
+    if (cols % 16 == 0) {
+        const auto ok16 = [&](const DequantArgs &a) {
+            return a.rows == 0 || (aligned16(a.out) && aligned16(a.q));
+        };
+        const size_t u0 = a0.rows * cols / 16, u1 = a1.rows * cols / 16;
+        const size_t b0 = (u0 + 255) / 256, b1 = (u1 + 255) / 256;
+        if (ok16(a0) && ok16(a1) && b0 + b1 < (size_t(1) << 31)) {
+            if (b0 + b1 == 0) return;
+            const DequantJobs jobs{{DequantJob{a0.out, a0.q, a0.scale, u0}, DequantJob{a1.out, a1.q, a1.scale, u1}},
+                                   unsigned(b0)};
+            dequantVec16<T><<<unsigned(b0 + b1), 256, 0, s>>>(jobs, DivU64(cols / 16));
+            return;
+        }
+    }
     const size_t nv0 = cols % N == 0 ? a0.rows * cols / N : 0;
     const size_t nv1 = cols % N == 0 ? a1.rows * cols / N : 0;
     const size_t nb0 = (nv0 + kPerBlock - 1) / kPerBlock, nb1 = (nv1 + kPerBlock - 1) / kPerBlock;

@@ -54,8 +54,9 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// R rows per wavefront, PL 16-byte units per lane per row (units_per_row <= 64 * PL).
-template <bool kI64, int R, int PL>
+// R rows per wavefront, PL 16-byte units per lane per row (units_per_row <= 64 * PL;
+// kFull: units_per_row == 64 * PL, so no lane needs a bounds test).
+template <bool kI64, int R, int PL, bool kFull>
 __global__ void __launch_bounds__(kWave)
     gatherMulti(v4u *__restrict__ out, const void *__restrict__ index, size_t n_index,
                 const v4u *__restrict__ weight, size_t vocab, int units_per_row, int *err) {
@@ -75,7 +76,7 @@ __global__ void __launch_bounds__(kWave)
         const v4u *src = weight + (id < vocab ? id : 0) * size_t(units_per_row); // bad ids read row 0
 #pragma unroll
         for (int k = 0; k < PL; ++k)
-            if (lane + k * kWave < units_per_row) r[j][k] = src[lane + k * kWave];
+            if (kFull || lane + k * kWave < units_per_row) r[j][k] = src[lane + k * kWave];
     }
     if (bad == 0 && row0 + R <= n_index) {
 #pragma unroll
@@ -83,7 +84,7 @@ __global__ void __launch_bounds__(kWave)
             v4u *dst = out + (row0 + j) * size_t(units_per_row);
 #pragma unroll
             for (int k = 0; k < PL; ++k)
-                if (lane + k * kWave < units_per_row) __builtin_nontemporal_store(r[j][k], dst + lane + k * kWave);
+                if (kFull || lane + k * kWave < units_per_row) __builtin_nontemporal_store(r[j][k], dst + lane + k * kWave);
         }
         return;
     }
@@ -94,21 +95,30 @@ __global__ void __launch_bounds__(kWave)
         v4u *dst = out + (row0 + j) * size_t(units_per_row);
 #pragma unroll
         for (int k = 0; k < PL; ++k)
-            if (lane + k * kWave < units_per_row) __builtin_nontemporal_store(r[j][k], dst + lane + k * kWave);
+            if (kFull || lane + k * kWave < units_per_row) __builtin_nontemporal_store(r[j][k], dst + lane + k * kWave);
     }
+}
+
+template <int PL, bool kFull>
+void launchMultiAs(void *out, const void *index, bool i64, size_t n, const void *w, size_t vocab,
+                   size_t units, int *err, hipStream_t s) {
+    constexpr int R = kMultiUnits / PL;
+    const unsigned grid = blocksFor(n, R);
+    if (i64)
+        gatherMulti<true, R, PL, kFull><<<grid, kWave, 0, s>>>(static_cast<v4u *>(out), index, n,
+                                                               static_cast<const v4u *>(w), vocab, int(units), err);
+    else
+        gatherMulti<false, R, PL, kFull><<<grid, kWave, 0, s>>>(static_cast<v4u *>(out), index, n,
+                                                                static_cast<const v4u *>(w), vocab, int(units), err);
 }
 
 template <int PL>
 void launchMulti(void *out, const void *index, bool i64, size_t n, const void *w, size_t vocab,
                  size_t units, int *err, hipStream_t s) {
-    constexpr int R = kMultiUnits / PL;
-    const unsigned grid = blocksFor(n, R);
-    if (i64)
-        gatherMulti<true, R, PL><<<grid, kWave, 0, s>>>(static_cast<v4u *>(out), index, n,
-                                                        static_cast<const v4u *>(w), vocab, int(units), err);
+    if (units == size_t(PL) * kWave)
+        launchMultiAs<PL, true>(out, index, i64, n, w, vocab, units, err, s);
     else
-        gatherMulti<false, R, PL><<<grid, kWave, 0, s>>>(static_cast<v4u *>(out), index, n,
-                                                         static_cast<const v4u *>(w), vocab, int(units), err);
+        launchMultiAs<PL, false>(out, index, i64, n, w, vocab, units, err, s);
 }
 
 template <typename Unit>
