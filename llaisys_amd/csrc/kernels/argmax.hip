@@ -32,7 +32,11 @@ namespace llaisys::kernels {
 
 namespace {
 
-constexpr int kBlock = 256;
+constexpr int kBlock = 256;     // flat argmax: many blocks over one vector
+// Rows: one block per row.  512 threads measured 92.1 us against 94.0 us with 256 on
+// [2048, 151936] bf16 (MI355X, rotating sets; a read-only kernel over the same bytes takes
+// 89.2 us).
+constexpr int kRowBlock = 512;
 constexpr int kU = 4;
 constexpr int64_t kNone = INT64_MAX;
 
@@ -48,10 +52,11 @@ __device__ __forceinline__ void take(Best &b, float v, int64_t i) {
     }
 }
 
-// Merge of the whole block; the result is valid in thread 0.
+// Merge of the whole block of B threads; the result is valid in thread 0.
+template <int B = kBlock>
 __device__ Best blockMerge(Best b) {
-    __shared__ float sv[kBlock / kWave];
-    __shared__ int64_t si[kBlock / kWave];
+    __shared__ float sv[B / kWave];
+    __shared__ int64_t si[B / kWave];
 #pragma unroll
     for (int m = kWave / 2; m > 0; m >>= 1) {
         const float ov = __shfl_xor(b.v, m, kWave);
@@ -65,14 +70,14 @@ __device__ Best blockMerge(Best b) {
     }
     __syncthreads();
     if (threadIdx.x == 0)
-        for (int w = 1; w < kBlock / kWave; ++w) take(b, sv[w], si[w]);
+        for (int w = 1; w < B / kWave; ++w) take(b, sv[w], si[w]);
     return b;
 }
 
 // Scan of [begin, end) by the block; thread-local order is ascending.
 // Thread 0 reads element `begin` first (the first vector's element 0, or the first tail
 // element when there is no vector); its value is returned in *x0 for that thread.
-template <typename T>
+template <typename T, int B = kBlock>
 __device__ Best scan(const void *vals, size_t begin, size_t end, bool vec, float *x0) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
@@ -81,17 +86,17 @@ __device__ Best scan(const void *vals, size_t begin, size_t end, bool vec, float
     if (vec) {
         const size_t nv = (end - begin) / N;
         tail = begin + nv * N;
-        for (size_t k = threadIdx.x; k < nv; k += kBlock * kU) {
+        for (size_t k = threadIdx.x; k < nv; k += B * kU) {
             v4u r[kU];
 #pragma unroll
             for (int u = 0; u < kU; ++u)
-                if (k + u * kBlock < nv) r[u] = load16Stream<T>(vals, begin + (k + u * kBlock) * N);
+                if (k + u * B < nv) r[u] = load16Stream<T>(vals, begin + (k + u * B) * N);
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
-                if (k + u * kBlock < nv) {
+                if (k + u * B < nv) {
                     float f[N];
                     F::unpack(r[u], f);
-                    if (k + u * kBlock == 0) *x0 = f[0];
+                    if (k + u * B == 0) *x0 = f[0];
                     float m = -INFINITY;
 #pragma unroll
                     for (int e = 0; e < N; ++e) m = f[e] > m ? f[e] : m;
@@ -100,13 +105,13 @@ __device__ Best scan(const void *vals, size_t begin, size_t end, bool vec, float
 #pragma unroll
                         for (int e = N - 1; e >= 0; --e) first = f[e] == m ? e : first;
                         b.v = m;
-                        b.i = int64_t(begin + (k + u * kBlock) * N + first);
+                        b.i = int64_t(begin + (k + u * B) * N + first);
                     }
                 }
             }
         }
     }
-    for (size_t j = tail + threadIdx.x; j < end; j += kBlock) {
+    for (size_t j = tail + threadIdx.x; j < end; j += B) {
         const float x = F::get(vals, j);
         if (j == begin) *x0 = x;
         if (x > b.v) {
@@ -132,12 +137,12 @@ __device__ void finish(Best b, float x0, void *idx, bool i64, void *val, size_t 
 }
 
 template <typename T>
-__global__ void __launch_bounds__(kBlock)
+__global__ void __launch_bounds__(kRowBlock)
     argmaxRowsKernel(void *idx, bool i64, void *val, const void *__restrict__ vals, size_t cols,
                      bool vec) {
     const size_t first = size_t(blockIdx.x) * cols;
     float x0 = 0.0f;
-    Best b = blockMerge(scan<T>(vals, first, first + cols, vec, &x0));
+    Best b = blockMerge<kRowBlock>(scan<T, kRowBlock>(vals, first, first + cols, vec, &x0));
     if (b.i != kNone) b.i -= int64_t(first);
     if (threadIdx.x == 0) finish<T>(b, x0, idx, i64, val, blockIdx.x);
 }
@@ -256,7 +261,7 @@ void launchRows(void *idx, bool i64, void *val, const void *vals, size_t rows, s
                 hipStream_t s) {
     if (rows == 0 || cols == 0) return;
     const bool vec = aligned16(vals) && (cols * Fmt<T>::kBytes) % 16 == 0;
-    argmaxRowsKernel<T><<<unsigned(rows), kBlock, 0, s>>>(idx, i64, val, vals, cols, vec);
+    argmaxRowsKernel<T><<<unsigned(rows), kRowBlock, 0, s>>>(idx, i64, val, vals, cols, vec);
 }
 
 template <typename T>
