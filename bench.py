@@ -837,6 +837,22 @@ def _cpu_model():
     return "unknown"
 
 
+def copy_floors():
+    """Copy-kernel floors of the ops' traffic (llaisys_amd/csrc/floors/floors.cpp, built next
+    to libllaisys.so): us per launch of a plain streaming kernel moving each op's bytes, and
+    the config-4 chain with every op replaced by its copy kernel (ms).  Run as a child
+    process on the same GPU; None when the program is missing."""
+    exe = ROOT / "llaisys_amd" / "libllaisys" / "llaisys_floors"
+    if not exe.is_file():
+        return None
+    import subprocess
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        print("bench: floors failed: " + r.stderr[-500:], file=sys.stderr, flush=True)
+        return None
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def traffic_of(kernel):
     """HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by
     the counters' reading on a device copy of known size), read from profiles/traffic.txt
@@ -859,6 +875,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-chain", action="store_true")
+    ap.add_argument("--no-floors", action="store_true", help="skip the copy-kernel floors")
     ap.add_argument("--no-configs", action="store_true", help="skip configs 0, 2 and 3")
     ap.add_argument("--no-attention", action="store_true", help="skip the self-attention lines")
     ap.add_argument("--attention-only", action="store_true",
@@ -1004,6 +1021,24 @@ def main():
     if not args.no_linear:
         linear = measure_linear(L, hip, stream, e0, e1, args.steps)
         linear.update(measure_rearrange(L, hip, stream, e0, e1, args.steps))
+
+    floors = None if args.no_floors else copy_floors()
+    if floors:
+        print("bench: floors " + json.dumps(floors), file=sys.stderr, flush=True)
+        for name, r in per_op.items():
+            if name in floors:
+                r["copy_floor_us"] = floors[name]
+                r["frac_of_copy_floor"] = round(floors[name] / r["us"], 4)
+        if chain is not None and "chain_ms" in floors:
+            chain["copy_floor_ms"] = floors["chain_ms"]
+            chain["frac_of_copy_floor"] = round(floors["chain_ms"] / chain["ms"], 4)
+        if configs is not None:
+            for key in ("config3 quantize W[8960,1536]", "config3 dequantize W[8960,1536]"):
+                name = key.split(" ", 1)[1]
+                r = configs.get("config3", {}).get(name)
+                if r is not None and key in floors:
+                    r["copy_floor_us"] = floors[key]
+                    r["frac_of_copy_floor"] = round(floors[key] / r["us"], 4)
 
     dom = per_op["swiglu"]
     roof = {"kernel": "swiglu binaryVec<BF16> [8192, 8960]", "bound": "hbm",
