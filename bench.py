@@ -937,7 +937,27 @@ def main():
             for i in range(3):
                 fn(wl.sets[i % NSETS])
             api.device_synchronize()
-        print(json.dumps({"probe": "copy 256 MiB x3, then each config-1 op x3",
+        # then the chain's fused RoPE + INT8 KV append (2048 tokens) and the config-3
+        # quantize / dequantize of W[8960, 1536], 3 dispatches each
+        BF, I8, F32 = L.DataType.BF16, L.DataType.I8, L.DataType.F32
+        dev = dict(device=L.DeviceType.AMD, device_id=0)
+        rng = np.random.default_rng(5)
+        t = Chain.TOK
+        q, k, v = (L.Tensor.from_numpy(bf16(rng, shp), BF, **dev) for shp in ((t, NH, D), (t, NKV, D), (t, NKV, D)))
+        qo, pos = L.Tensor((t, NH, D), BF, **dev), L.Tensor.from_numpy(np.arange(t, dtype=np.int64), **dev)
+        kc, vc = L.Tensor((t, NKV, D), I8, **dev), L.Tensor((t, NKV, D), I8, **dev)
+        ks, vs = L.Tensor((t, NKV), F32, **dev), L.Tensor((t, NKV), F32, **dev)
+        w = L.Tensor.from_numpy(bf16(rng, (I, H), 0.02), BF, **dev)
+        wq, wsc, wd = L.Tensor((I, H), I8, **dev), L.Tensor((I,), F32, **dev), L.Tensor((I, H), BF, **dev)
+        for _ in range(3):
+            L.Ops.rope_kv_append_int8(qo, q, k, v, pos, 1e6, kc, ks, vc, vs, 0)
+        for _ in range(3):
+            L.Ops.quantize_int8(wq, wsc, w)
+        for _ in range(3):
+            L.Ops.dequantize_int8(wd, wq, wsc)
+        api.device_synchronize()
+        print(json.dumps({"probe": "copy 256 MiB x3, then each config-1 op x3, RoPE+KV append (2048 "
+                                   "tokens) x3, quantize / dequantize W[8960,1536] x3",
                           "ops": {name: b for name, b, _ in wl.ops()}}))
         return
     ops = wl.ops()
