@@ -191,6 +191,24 @@ struct Bench {
         freeAll();
         return us;
     }
+    double ropeKvFloor(size_t T) {
+        const size_t qb = T * 12 * 128 * 2, kb = T * 2 * 128 * 2;
+        const int sets = setsFor(2 * qb + 3 * kb);
+        struct S { v4u *q, *k, *v, *qo; v2u *kc, *vc; float *ks, *vs; };
+        std::vector<S> ss(sets);
+        for (auto &x : ss) {
+            x.q = static_cast<v4u *>(alloc(qb)), x.qo = static_cast<v4u *>(alloc(qb));
+            x.k = static_cast<v4u *>(alloc(kb)), x.v = static_cast<v4u *>(alloc(kb));
+            x.kc = static_cast<v2u *>(alloc(kb / 2)), x.vc = static_cast<v2u *>(alloc(kb / 2));
+            x.ks = static_cast<float *>(alloc(T * 8)), x.vs = static_cast<float *>(alloc(T * 8));
+        }
+        const double us = time(sets, [&](int i) {
+            const S &x = ss[i];
+            ropeKv<<<blocks((qb + 2 * kb) / 16), 256, 0, s>>>(x.qo, x.q, x.k, x.v, x.kc, x.vc, x.ks, x.vs, qb / 16, kb / 16);
+        });
+        freeAll();
+        return us;
+    }
     double readFloor(size_t bytes) {
         const size_t n = bytes / 16;
         const int sets = setsFor(bytes);
@@ -268,6 +286,12 @@ int main() {
     const size_t w = size_t(8960) * 1536;
     out.push_back({"config3 quantize W[8960,1536]", B.streamFloor<2, 1>(w)});
     out.push_back({"config3 dequantize W[8960,1536]", B.stream12Floor(w)});
+    // config-4 chain ops at 2048 tokens
+    const size_t ctok = 2048 * H * 2;
+    out.push_back({"chain add_rms_norm 2048", B.streamFloor<2, 2>(ctok)});
+    out.push_back({"chain swiglu 2048", B.streamFloor<2, 1>(size_t(2048) * I * 2)});
+    out.push_back({"chain rope_kv 2048", B.ropeKvFloor(2048)});
+    out.push_back({"chain argmax_rows 2048", B.readFloor(size_t(2048) * 151936 * 2)});
     // config-4 chain
     out.push_back({"chain_ms", chainFloor(B)});
     std::printf("{");

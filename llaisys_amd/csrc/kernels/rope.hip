@@ -11,10 +11,11 @@
 // float absorbs except within 2^-29 of a float tie.
 //
 // Design: HBM-bound, no MFMA (no contraction).  Two kernels:
-//  * ropeWave (most shapes): one wavefront per token, no block barrier.  The wave issues
-//    the 16-byte loads of all the token's q and k head rows, computes the token's d/2
-//    (cos, sin) pairs (one per lane) into its own LDS slice while they are in flight, and
-//    each lane then keeps the pairs of its column in registers for every head row.
+//  * ropeWave (most shapes): 2^split_log2 wavefronts per token (each a contiguous share
+//    of the token's head-row instructions), no block barrier.  A wave issues the 16-byte
+//    loads of its rows, computes the token's d/2 (cos, sin) pairs (one per lane) into its
+//    own LDS slice while they are in flight, and each lane then keeps the pairs of its
+//    column in registers for every head row it rotates.
 //  * ropeVec (few rows per token, e.g. k alone): a 256-thread block owns a run of tokens,
 //    computes their pairs into LDS behind a block barrier and rotates items that read
 //    their pairs from LDS; it packs several tokens into a block, so lanes stay busy.
@@ -22,13 +23,13 @@
 // out-of-line rare path.  Loads and stores are non-temporal (read once, written once).
 // q and k of the same tokens go through one launch.
 //
-// Measured on MI355X (rocprof kernel durations, same run): q+k of Qwen2 at 8192 tokens
-// 13.2 us with ropeWave vs 13.5 with ropeVec; q alone 12.2 vs 12.8; Llama-8B q+k at
-// 16384 tokens 58.4 vs 62.5.  A pure copy with the same access pattern takes 11.7 us
-// (q+k), so the f64 rotation (about 100 f32-op equivalents per 16-byte item, f64 ops
-// and f32<->f64 conversions issuing at half the f32 rate) costs 1.5 us.  Tried and
-// slower: a persistent double-buffered block loop (18.7-25.8 us), 8 waves/SIMD by
-// register cap (spills, 40 us).
+// Measured on MI355X (median of batched launches over >= 1 GiB of rotating sets): q+k of
+// Qwen2 at 8192 tokens 12.1 us with 2 waves per token (13.2 with one, 13.5 with ropeVec);
+// q alone 10.3 us; Llama-8B q+k at 16384 tokens 54.0 us with 4 waves per token (57.0
+// with one).  A copy kernel moving the same bytes takes 10.4 us (q+k); the rest is the
+// f64 rotation (two f32 -> f64 conversions, a multiply, an fma and the conversion back
+// per element) issuing behind the loads.  Tried and slower: a persistent double-buffered
+// block loop (18.7-25.8 us), 8 waves/SIMD by register cap (spills, 40 us).
 #include "common.hpp"
 #include "launch.hpp"
 #include "rope_common.hpp"
@@ -147,12 +148,14 @@ __global__ void __launch_bounds__(256)
 // back the N (cos, sin) pairs of its vector column into registers and uses them for every
 // head row of the token: a row is kRowVec consecutive lanes, so a wave instruction covers
 // 64 / kRowVec rows (q rows first, then k rows) and the lane's column is the same in all
-// of them.  Rows are taken in passes of IPT wave instructions.  Waves past the last token
+// of them.  Rows are taken in passes of IPT wave instructions (kOnePass: one pass, laid
+// out as straight-line code).  Waves past the last token
 // redo the last token and store nothing, so no wave leaves before the loads (a branch
 // there would serialise the kernel-argument loads ahead of the first global load).
-template <typename T, int IPT, int VPH>
+template <typename T, int IPT, int VPH, bool kOnePass>
 __global__ void __launch_bounds__(256)
-    ropeWave(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int passes, FreqTable ft) {
+    ropeWave(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int passes, int split_log2,
+             FreqTable ft) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
     constexpr int kRowVec = 2 * VPH;          // lanes per head row
@@ -168,7 +171,9 @@ __global__ void __launch_bounds__(256)
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
-    const size_t t0 = size_t(blockIdx.x) * (256 / kWave) + size_t(wave);
+    const uint32_t gw = blockIdx.x * (256 / kWave) + uint32_t(wave);
+    const uint32_t t0 = gw >> split_log2;
+    const int first_instr = int(gw & ((1u << split_log2) - 1)) * passes * IPT;
     const bool live = t0 < seq;                // waves past the end redo the last token
     const size_t t = live ? t0 : seq - 1;      // and store nothing
     const int nh0 = tp.n_heads0, rows = nh0 + tp.n_heads1;
@@ -188,12 +193,12 @@ __global__ void __launch_bounds__(256)
     const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
     __builtin_amdgcn_sched_barrier(0);
     double c[N], sn[N];
-    int pass = 0;
-    do {
+    const int npass = kOnePass ? 1 : passes;
+    for (int pass = 0; pass < npass; ++pass) {
         v4u raw[IPT];
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
-            const int r = (pass * IPT + k) * kRows + rlane;
+            const int r = (first_instr + pass * IPT + k) * kRows + rlane;
             const char *src = (r < nh0 ? in0 : (r < rows ? in1 : in0 - size_t(r) * kRowBytes)) + size_t(r) * kRowBytes;
             raw[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
         }
@@ -237,7 +242,7 @@ __global__ void __launch_bounds__(256)
             other.y = partnerOf<VPH>(raw[k].y);
             other.z = partnerOf<VPH>(raw[k].z);
             other.w = partnerOf<VPH>(raw[k].w);
-            const int r = (pass * IPT + k) * kRows + rlane;
+            const int r = (first_instr + pass * IPT + k) * kRows + rlane;
             if (live && r < rows) {
                 float x[N], q[N], y[N];
                 F::unpack(raw[k], x);
@@ -247,7 +252,7 @@ __global__ void __launch_bounds__(256)
                 __builtin_nontemporal_store(F::packQ(y), reinterpret_cast<v4u *>((r < nh0 ? out0 : out1) + size_t(r) * kRowBytes));
             }
         }
-    } while (++pass < passes);
+    }
 }
 
 // Any head_dim / alignment: one thread per (token, head, j) pair of one tensor.
@@ -274,15 +279,26 @@ __global__ void __launch_bounds__(256)
 }
 
 template <typename T, int IPT>
-void launchWaveIpt(int vph, int passes, const RopePair &tp, const int64_t *pos, size_t seq,
-                   const FreqTable &ft, hipStream_t s) {
-    const unsigned grid = blocksFor(seq, 256 / kWave);
+void launchWaveIpt(int vph, int passes, int split_log2, const RopePair &tp, const int64_t *pos,
+                   size_t seq, const FreqTable &ft, hipStream_t s) {
+    const unsigned grid = blocksFor(seq << split_log2, 256 / kWave);
+    if (passes == 1) {
+        switch (vph) {
+        case 2: ropeWave<T, IPT, 2, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+        case 4: ropeWave<T, IPT, 4, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+        case 8: ropeWave<T, IPT, 8, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+        case 16: ropeWave<T, IPT, 16, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+        case 32: ropeWave<T, IPT, 32, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+        default: break;
+        }
+        return;
+    }
     switch (vph) {
-    case 2: ropeWave<T, IPT, 2><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
-    case 4: ropeWave<T, IPT, 4><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
-    case 8: ropeWave<T, IPT, 8><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
-    case 16: ropeWave<T, IPT, 16><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
-    case 32: ropeWave<T, IPT, 32><<<grid, 256, 0, s>>>(tp, pos, seq, passes, ft); break;
+    case 2: ropeWave<T, IPT, 2, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 4: ropeWave<T, IPT, 4, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 8: ropeWave<T, IPT, 8, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 16: ropeWave<T, IPT, 16, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 32: ropeWave<T, IPT, 32, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
     default: break;
     }
 }
@@ -291,12 +307,23 @@ void launchWaveIpt(int vph, int passes, const RopePair &tp, const int64_t *pos, 
 template <typename T>
 void launchWave(int vph, int instr, const RopePair &tp, const int64_t *pos, size_t seq,
                 const FreqTable &ft, hipStream_t s) {
-    const int passes = (instr + 3) / 4, ipt = (instr + passes - 1) / passes;
+    // Waves per token: the fewest (a power of two, at least 2 from 3 instructions on) that
+    // leave each wave <= 3 row instructions.  Measured on MI355X, 16-byte items: q+k of
+    // Qwen2 at 8192 tokens (4 instructions) 12.1 us with 2 waves vs 13.2 with 1 and 13.3
+    // with 4; q alone (3) 10.3 vs 11.1 with 1; Llama-8B q+k at 16384 tokens (10) 54.0 with
+    // 4 vs 55.5 with 2 and 57.0 with 1.  More waves overlap one token's loads with
+    // another's rotation; each repeats the token's (cos, sin) work.
+    int split_log2 = instr >= 3 ? 1 : 0;
+    while ((instr + (1 << split_log2) - 1) >> split_log2 > 3) ++split_log2;
+    while (split_log2 > 0 && (seq << split_log2) >= (size_t(1) << 31)) --split_log2;
+    const int split = 1 << split_log2;
+    const int per_wave = (instr + split - 1) / split;
+    const int passes = (per_wave + 3) / 4, ipt = (per_wave + passes - 1) / passes;
     switch (ipt) {
-    case 1: launchWaveIpt<T, 1>(vph, passes, tp, pos, seq, ft, s); break;
-    case 2: launchWaveIpt<T, 2>(vph, passes, tp, pos, seq, ft, s); break;
-    case 3: launchWaveIpt<T, 3>(vph, passes, tp, pos, seq, ft, s); break;
-    default: launchWaveIpt<T, 4>(vph, passes, tp, pos, seq, ft, s); break;
+    case 1: launchWaveIpt<T, 1>(vph, passes, split_log2, tp, pos, seq, ft, s); break;
+    case 2: launchWaveIpt<T, 2>(vph, passes, split_log2, tp, pos, seq, ft, s); break;
+    case 3: launchWaveIpt<T, 3>(vph, passes, split_log2, tp, pos, seq, ft, s); break;
+    default: launchWaveIpt<T, 4>(vph, passes, split_log2, tp, pos, seq, ft, s); break;
     }
 }
 

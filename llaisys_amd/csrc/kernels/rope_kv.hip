@@ -16,14 +16,15 @@
 // writes its 8 (bf16 / f16) or 4 (f32) codes, so the group stores the whole code row
 // contiguously.
 //
-// Bound (MI355X, Qwen2 shapes, 2048 tokens, 15 MB): 5.2 us against 3.8 us for a copy
-// kernel with the same traffic.  rocprofv3 counters put the difference in VALU issue: ~690
-// VALU instructions per token-wave (the f64 rotation -- two f32->f64 conversions, a
-// multiply, an fma and the conversion back per element, which the bit-exact k codes
-// need -- the f64 sincos, and the quantizer's divisions and correctly rounded quotients),
-// i.e. ~2.3 us of issue per SIMD at 4 cycles per wave64 instruction, only partly hidden
-// behind the 1.7 us of transfer.  A block-per-2-tokens layout with block-wide (cos, sin)
-// staging took 5.3-5.45 us.
+// Bound (MI355X, Qwen2 shapes, 2048 tokens, 15.8 MB): 5.06 us against 3.92 us for a copy
+// kernel with the same traffic.  At 2048 tokens the launch has two waves per SIMD, and
+// the VALU issue of the exact f64 rotation (two f32 -> f64 conversions, two products, a
+// sum and the conversion back per element, which the bit-exact k codes need), the f64
+// sincos and the quantizer is only partly hidden behind the loads: rocprofv3 counted 600
+// VALU instructions per token-wave before the pure-q fast path and the one-pass layout
+// (5.43 -> 5.06 us).  Tried and slower: 2 or 4 waves per token (5.73 / 6.30 us; each
+// wave repeats the token's sincos), a block-per-2-tokens layout with block-wide
+// (cos, sin) staging (5.3-5.45 us).
 #include "common.hpp"
 #include "launch.hpp"
 #include "quantize.hpp"
@@ -58,7 +59,10 @@ struct RopeKvArgs {
 // instructions.  Each lane computes one (cos, sin) pair of the token into the wave's own
 // LDS slice (no block barrier) while the row loads are in flight, then keeps its column's
 // pairs in registers.  Waves past the last token redo the last token and store nothing.
-template <typename T, int IPT, int VPH>
+// An instruction whose rows are all q rows (wave-uniform) takes a rotate-and-store path
+// with no quantizer work; kOnePass (all rows in one pass, e.g. Qwen2's 16 rows) lets the
+// compiler lay the whole token out as straight-line code.
+template <typename T, int IPT, int VPH, bool kOnePass>
 __global__ void __launch_bounds__(256)
     ropeKvWave(RopeKvArgs a, const int64_t *__restrict__ pos, size_t seq, int passes, FreqTable ft) {
     using F = Fmt<T>;
@@ -92,17 +96,23 @@ __global__ void __launch_bounds__(256)
     const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
     __builtin_amdgcn_sched_barrier(0);
     double c[N], sn[N];
-    int pass = 0;
-    do {
+    const int npass = kOnePass ? 1 : passes;
+    for (int pass = 0; pass < npass; ++pass) {
         v4u raw[IPT];
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
-            const int r = (pass * IPT + k) * kRows + rlane;
-            // rows past the token's last one read its first q row and store nothing
-            const char *src = r < nq ? q_in + size_t(r) * kRowBytes
-                              : r < nq + nk ? k_in + size_t(r - nq) * kRowBytes
-                              : r < rows ? v_in + size_t(r - nq - nk) * kRowBytes
-                                         : q_in;
+            const int ins = pass * IPT + k; // wave-uniform
+            const int r = ins * kRows + rlane;
+            const char *src;
+            if ((ins + 1) * kRows <= nq) {
+                src = q_in + size_t(r) * kRowBytes;
+            } else {
+                // rows past the token's last one read its first q row and store nothing
+                src = r < nq ? q_in + size_t(r) * kRowBytes
+                      : r < nq + nk ? k_in + size_t(r - nq) * kRowBytes
+                      : r < rows ? v_in + size_t(r - nq - nk) * kRowBytes
+                                 : q_in;
+            }
             raw[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
         }
         if (pass == 0) {
@@ -145,7 +155,20 @@ __global__ void __launch_bounds__(256)
             other.y = partnerOf<VPH>(raw[k].y);
             other.z = partnerOf<VPH>(raw[k].z);
             other.w = partnerOf<VPH>(raw[k].w);
-            const int r = (pass * IPT + k) * kRows + rlane;
+            const int ins = pass * IPT + k; // wave-uniform
+            const int r = ins * kRows + rlane;
+            if ((ins + 1) * kRows <= nq) {
+                // every row of this instruction is a q row: rotation and store only, in
+                // ropeWave's form (rope.hip), so q equals llaisysROPE's
+                if (!live) continue;
+                float x[N], q[N], y[N];
+                F::unpack(raw[k], x);
+                F::unpack(other, q);
+#pragma unroll
+                for (int e = 0; e < N; ++e) y[e] = float(fma(double(q[e]), sn[e], double(x[e]) * c[e]));
+                __builtin_nontemporal_store(F::packQ(y), reinterpret_cast<v4u *>(q_out + size_t(r) * kRowBytes));
+                continue;
+            }
             const int kind = r < nq ? 0 : (r < nq + nk ? 1 : (r < rows ? 2 : 3)); // 3: none
             v4u out = raw[k];
             if (kind <= 1) {
@@ -185,19 +208,19 @@ __global__ void __launch_bounds__(256)
                 if (v_lane == 0) (kind == 1 ? k_scale : v_scale)[hr] = qz.scale;
             }
         }
-    } while (++pass < passes);
+    }
 }
 
-template <typename T, int IPT>
+template <typename T, int IPT, bool kOnePass>
 void launchKvWaveIpt(int vph, int passes, const RopeKvArgs &a, const int64_t *pos, size_t seq,
                      const FreqTable &ft, hipStream_t s) {
     const unsigned grid = blocksFor(seq, 256 / kWave);
     switch (vph) {
-    case 2: ropeKvWave<T, IPT, 2><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
-    case 4: ropeKvWave<T, IPT, 4><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
-    case 8: ropeKvWave<T, IPT, 8><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
-    case 16: ropeKvWave<T, IPT, 16><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
-    case 32: ropeKvWave<T, IPT, 32><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 2: ropeKvWave<T, IPT, 2, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 4: ropeKvWave<T, IPT, 4, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 8: ropeKvWave<T, IPT, 8, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 16: ropeKvWave<T, IPT, 16, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+    case 32: ropeKvWave<T, IPT, 32, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
     default: break;
     }
 }
@@ -208,11 +231,20 @@ void launchKvWave(int vph, const RopeKvArgs &a, const int64_t *pos, size_t seq, 
     const int rows_per_instr = kWave / (2 * vph);
     const int instr = (a.nq + 2 * a.nk + rows_per_instr - 1) / rows_per_instr;
     const int passes = (instr + 3) / 4, ipt = (instr + passes - 1) / passes;
+    if (passes == 1) {
+        switch (ipt) {
+        case 1: launchKvWaveIpt<T, 1, true>(vph, passes, a, pos, seq, ft, s); break;
+        case 2: launchKvWaveIpt<T, 2, true>(vph, passes, a, pos, seq, ft, s); break;
+        case 3: launchKvWaveIpt<T, 3, true>(vph, passes, a, pos, seq, ft, s); break;
+        default: launchKvWaveIpt<T, 4, true>(vph, passes, a, pos, seq, ft, s); break;
+        }
+        return;
+    }
     switch (ipt) {
-    case 1: launchKvWaveIpt<T, 1>(vph, passes, a, pos, seq, ft, s); break;
-    case 2: launchKvWaveIpt<T, 2>(vph, passes, a, pos, seq, ft, s); break;
-    case 3: launchKvWaveIpt<T, 3>(vph, passes, a, pos, seq, ft, s); break;
-    default: launchKvWaveIpt<T, 4>(vph, passes, a, pos, seq, ft, s); break;
+    case 1: launchKvWaveIpt<T, 1, false>(vph, passes, a, pos, seq, ft, s); break;
+    case 2: launchKvWaveIpt<T, 2, false>(vph, passes, a, pos, seq, ft, s); break;
+    case 3: launchKvWaveIpt<T, 3, false>(vph, passes, a, pos, seq, ft, s); break;
+    default: launchKvWaveIpt<T, 4, false>(vph, passes, a, pos, seq, ft, s); break;
     }
 }
 
