@@ -102,6 +102,51 @@ __global__ void __launch_bounds__(blockFor<G>())
     }
 }
 
+// A row of exactly G 16-byte vectors (G a multiple of 64) per block of G threads, one
+// vector per lane: the launch plan for few rows.  With the register plan above, 2048 rows
+// of 1536 bf16 are 2048 single-wave rows (two waves per SIMD, each waiting on 3 KB of
+// loads); here they are 6144 waves of one 1 KB load each, joined through LDS.  Measured
+// on MI355X (graph-replayed medians over >= 1 GiB of rotating sets), [2048, 1536] bf16:
+// add + rms_norm 5.83 -> 5.32 us, rms_norm 4.14 -> 3.57 us; [256, 1536] 3.97 -> 2.58 and
+// 3.17 -> 2.46 us; f32 [128, 1536] 3.78 -> 2.57 and 3.36 -> 2.47 us.  With more data the
+// register plan wins (bf16 [3072, 1536] add + rms_norm 7.69 vs 8.36 us, [2048, 4096] 11.8
+// vs 13.1 us; f32 [2048, 1536] rms_norm 5.28 vs 6.58 us), so the launcher takes this
+// kernel for inputs under kWideBytes.  Same arithmetic as rmsNormRows; only the lane tree
+// of the sum differs.
+constexpr size_t kWideBytes = size_t(8) << 20; // input bytes below which rmsNormWide runs
+
+template <typename T, int G, bool kFused>
+__global__ void __launch_bounds__(G)
+    rmsNormWide(void *__restrict__ out, void *residual_out, const void *__restrict__ in,
+                const void *residual, const void *__restrict__ weight, int cols, float eps) {
+    using F = Fmt<T>;
+    constexpr int N = F::kVec;
+    __shared__ float red[G / kWave];
+    const size_t at = size_t(blockIdx.x) * size_t(cols) + size_t(threadIdx.x) * N;
+    v4u raw = load16Stream<T>(in, at);
+    float x[N];
+    F::unpack(raw, x);
+    if constexpr (kFused) {
+        float r[N];
+        F::unpack(load16Stream<T>(residual, at), r);
+#pragma unroll
+        for (int e = 0; e < N; ++e) x[e] = x[e] + r[e];
+        raw = F::packQ(x); // h = T(x + r), the value the reference's add stores
+        store16Stream<T>(residual_out, at, raw);
+        F::unpack(raw, x);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < N; ++e) ss = fmaf(x[e], x[e], ss);
+    ss = groupReduce<G, SumOp>(ss, red);
+    const float inv = 1.0f / sqrtf(ss / float(cols) + eps);
+    float w[N], y[N];
+    F::unpack(load16<T>(weight, size_t(threadIdx.x) * N), w);
+#pragma unroll
+    for (int e = 0; e < N; ++e) y[e] = x[e] * w[e] * inv;
+    store16Stream<T>(out, at, F::packQ(y));
+}
+
 // Any shape / alignment: one 256-thread block per row, scalar accesses, two passes over
 // the row (the second pass re-reads it from cache).
 template <typename T, bool kFused>
@@ -129,6 +174,29 @@ __global__ void __launch_bounds__(256)
         F::put(out, base + j, F::get(src, base + j) * F::get(weight, j) * inv);
 }
 
+template <typename T, int G>
+void launchWideG(void *out, void *res_out, const void *in, const void *res, const void *w,
+                 size_t rows, size_t cols, float eps, hipStream_t s) {
+    if (res)
+        rmsNormWide<T, G, true><<<unsigned(rows), G, 0, s>>>(out, res_out, in, res, w, int(cols), eps);
+    else
+        rmsNormWide<T, G, false><<<unsigned(rows), G, 0, s>>>(out, nullptr, in, nullptr, w, int(cols), eps);
+}
+
+// The wide-row kernel for rows of 128..1024 vectors in steps of 64 that have an
+// instantiation (Qwen2 1536 and Llama 4096 columns in bf16 / f16 and f32); false otherwise.
+template <typename T>
+bool launchWide(void *out, void *res_out, const void *in, const void *res, const void *w,
+                size_t rows, size_t cols, float eps, hipStream_t s) {
+    switch (cols / Fmt<T>::kVec) {
+    case 192: launchWideG<T, 192>(out, res_out, in, res, w, rows, cols, eps, s); return true;
+    case 384: launchWideG<T, 384>(out, res_out, in, res, w, rows, cols, eps, s); return true;
+    case 512: launchWideG<T, 512>(out, res_out, in, res, w, rows, cols, eps, s); return true;
+    case 1024: launchWideG<T, 1024>(out, res_out, in, res, w, rows, cols, eps, s); return true;
+    default: return false;
+    }
+}
+
 template <typename T>
 void launch(void *out, void *res_out, const void *in, const void *res, const void *w,
             size_t rows, size_t cols, float eps, hipStream_t s) {
@@ -138,6 +206,9 @@ void launch(void *out, void *res_out, const void *in, const void *res, const voi
     const bool vec = cols % N == 0 && cols <= size_t(INT32_MAX) && aligned16(out) &&
                      aligned16(in) && aligned16(w) &&
                      (!fused || (aligned16(res) && aligned16(res_out)));
+    if (vec && !std::isnan(eps) && rows > 64 && rows * cols * size_t(Fmt<T>::kBytes) < kWideBytes &&
+        launchWide<T>(out, res_out, in, res, w, rows, cols, eps, s))
+        return;
     RowPlan plan = vec && !std::isnan(eps) ? planRow(cols / N) : RowPlan{};
     bool done = false;
     withPlan(plan, [&](auto g, auto v) {

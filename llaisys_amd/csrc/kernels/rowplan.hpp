@@ -48,7 +48,7 @@ inline RowPlan planRow(size_t nvec) {
 
 template <int G>
 constexpr int blockFor() {
-    return G < 256 ? 256 : G;
+    return G <= 64 ? 256 : G; // wider groups: one row per block
 }
 
 // Calls f(integral_constant<G>, integral_constant<VMAX>) for the plan.

@@ -106,6 +106,7 @@ RMS_SHAPES = [
     ((128, 1536), 1e-6),                        # config 0 (f32) / Qwen2 hidden
     ((8192, 1536), 1e-6),                       # config 1
     ((64, 8960), 1e-6),                         # 1024-lane rows
+    ((65, 1536), 1e-6), ((100, 4096), 1e-5),    # one vector per lane, one row per block
     ((33, 1000), 1e-5), ((5, 20000), 1e-5),     # ragged / wider than the register plan
     ((3, 8), 1e-5), ((2, 100000), 1e-6),        # tiny, huge rows (scalar kernel)
 ]
@@ -132,7 +133,8 @@ def test_rms_norm(dt, shape, eps):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("shape", [(8192, 1536), (2048, 1536), (7, 4096), (9, 1000), (1, 12)])
+@pytest.mark.parametrize("shape", [(8192, 1536), (2048, 1536), (300, 4096), (65, 1536), (7, 4096),
+                                   (9, 1000), (1, 12)])
 def test_add_rms_norm(dt, shape):
     rng = np.random.default_rng(11)
     x, r = sample(rng, shape, dt), sample(rng, shape, dt)
