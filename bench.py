@@ -880,7 +880,7 @@ def main():
     ap.add_argument("--no-attention", action="store_true", help="skip the self-attention lines")
     ap.add_argument("--attention-only", action="store_true",
                     help="only the self-attention lines (profiling); prints their JSON")
-    ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain (profiling)")
+    ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain: --steps graph replays (profiling), then its timing as JSON")
     ap.add_argument("--no-linear", action="store_true", help="skip the linear and rearrange lines")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode-step chain")
     ap.add_argument("--decode-only", action="store_true",
@@ -911,6 +911,10 @@ def main():
         for _ in range(args.steps):
             graph.launch()
         api.device_synchronize()
+        us, us_mean = time_launches(hip, stream, lambda i: graph.launch(), batch=4)
+        print(json.dumps({"chain_ms": round(us * 1e-3, 4), "chain_ms_mean": round(us_mean * 1e-3, 4),
+                          "tokens_per_s": round(Chain.TOK / (us * 1e-6)),
+                          "frac_peak": round(ch.bytes() / (us * 1e-6) / 1e9 / PEAK_GBS, 4)}))
         return
     if args.decode_only:
         print(json.dumps({"decode": measure_decode(L, hip, stream, hip.event(), hip.event(),

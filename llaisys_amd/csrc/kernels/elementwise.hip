@@ -25,10 +25,11 @@ namespace {
 
 // 16-byte vectors per input per lane, measured per kernel on MI355X: the binary ops
 // (two streamed inputs) are fastest with one (swiglu [8192, 8960]: 69.3 us vs 71.2 with
-// two, 75.1 with four); dequantize, whose lanes read only 8 bytes of codes per vector,
-// needs four to keep enough bytes in flight (8960x1536: 6.7 us vs 8.5 with two).
+// two, 75.1 with four); dequantize writes two output vectors per lane from 8-byte code
+// loads, in 64-thread blocks (see dequantVec).
 constexpr int kBinaryU = 1;
-constexpr int kDequantU = 4;
+constexpr int kDequantU = 2;
+constexpr int kDequantBlock = 64;
 // Threads per block of the binary ops: one wavefront.  Same work per lane, only smaller
 // blocks: swiglu [8192, 8960] 67.3 us vs 69.2 with 256 threads (a plain 2-in / 1-out
 // stream measured the same way: 65.1 vs 66.0 us).
@@ -154,8 +155,16 @@ struct DequantJobs {
     unsigned nb0;
 };
 
-template <typename T, int kU>
-__global__ void __launch_bounds__(256)
+// kU output vectors per lane, vector k of a lane at (blk * kU + k) * B + thread, so every
+// store instruction of a wavefront writes one contiguous 1 KB and every code load reads
+// one contiguous 256 / 512 B.  All loads (codes and the row scales) are issued before any
+// arithmetic, unconditionally (a lane past the end reads vector 0 and stores nothing).
+// Measured on MI355X (W[8960, 1536] bf16, graph-replayed medians over >= 1 GiB of rotating
+// sets): 8.27 us with two vectors per lane in 64-thread blocks, against 9.30 us for 16
+// codes per lane (one 16-byte code load, two stores 32 bytes apart per lane) in 256-thread
+// blocks and 8.44 us for the same layout in 256-thread blocks.
+template <typename T, int kU, int B>
+__global__ void __launch_bounds__(B)
     dequantVec(DequantJobs jobs, DivU64 rowdiv) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
@@ -165,49 +174,22 @@ __global__ void __launch_bounds__(256)
     const float *__restrict__ scale = second ? jobs.job[1].scale : jobs.job[0].scale;
     const size_t nvec = second ? jobs.job[1].nvec : jobs.job[0].nvec;
     const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
-    const size_t first = size_t(blk) * 256 * kU + threadIdx.x;
+    const size_t first = size_t(blk) * B * kU + threadIdx.x;
+    float f[kU][N], sc[kU];
 #pragma unroll
     for (int k = 0; k < kU; ++k) {
-        const size_t i = first + size_t(k) * 256;
-        if (i < nvec) {
-            float f[N];
-            loadCodes<N>(q, i * N, f);
-            const float sc = scale[rowdiv.div(i)];
-#pragma unroll
-            for (int e = 0; e < N; ++e) f[e] = f[e] * sc;
-            store16Stream<T>(out, i * N, packScaled<T>(f, sc));
-        }
+        const size_t i = first + size_t(k) * B;
+        const size_t ic = i < nvec ? i : 0;
+        loadCodes<N>(q, ic * N, f[k]);
+        sc[k] = scale[rowdiv.div(ic)];
     }
-}
-
-// 16 codes per lane (one 16-byte load, 16 / N output vectors): for rows whose length is a
-// multiple of 16.  Measured on MI355X (W[8960, 1536] bf16, >= 1 GiB of rotating sets):
-// 9.8 us against 11.3 us for 8 codes x 4 per lane; a copy kernel with the same traffic
-// (read 1 : write 2 bytes, 41 MB) takes 9.7 us, so this is the write-heavy stream's floor.
-template <typename T>
-__global__ void __launch_bounds__(256)
-    dequantVec16(DequantJobs jobs, DivU64 rowdiv) {
-    using F = Fmt<T>;
-    constexpr int N = F::kVec;
-    const bool second = blockIdx.x >= jobs.nb0; // block-uniform
-    void *__restrict__ out = second ? jobs.job[1].out : jobs.job[0].out;
-    const int8_t *__restrict__ q = second ? jobs.job[1].q : jobs.job[0].q;
-    const float *__restrict__ scale = second ? jobs.job[1].scale : jobs.job[0].scale;
-    const size_t n16 = second ? jobs.job[1].nvec : jobs.job[0].nvec; // 16-code units
-    const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
-    const size_t i = size_t(blk) * 256 + threadIdx.x;
-    if (i >= n16) return;
-    const v4u c = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(q + i * 16));
-    const float sc = scale[rowdiv.div(i)];
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    float f[16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int k = 0; k < kU; ++k) {
+        const size_t i = first + size_t(k) * B;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) f[4 * j + e] = float(int8_t(w[j] >> (8 * e))) * sc;
-#pragma unroll
-    for (int o = 0; o < 16 / N; ++o)
-        store16Stream<T>(out, i * 16 + size_t(o) * N, packScaled<T>(f + o * N, sc));
+        for (int e = 0; e < N; ++e) f[k][e] = f[k][e] * sc[k];
+        if (i < nvec) store16Stream<T>(out, i * N, packScaled<T>(f[k], sc[k]));
+    }
 }
 
 template <typename T>
@@ -228,24 +210,10 @@ struct DequantArgs {
 template <typename T>
 void launchDequant(const DequantArgs &a0, const DequantArgs &a1, size_t cols, hipStream_t s) {
     constexpr int N = Fmt<T>::kVec;
-    constexpr size_t kPerBlock = size_t(256) * kDequantU;
+    constexpr size_t kPerBlock = size_t(kDequantBlock) * kDequantU;
     const auto vecOk = [&](const DequantArgs &a) {
         return a.rows == 0 || (aligned16(a.out) && reinterpret_cast<uintptr_t>(a.q) % N == 0);
     };
-    if (cols % 16 == 0) {
-        const auto ok16 = [&](const DequantArgs &a) {
-            return a.rows == 0 || (aligned16(a.out) && aligned16(a.q));
-        };
-        const size_t u0 = a0.rows * cols / 16, u1 = a1.rows * cols / 16;
-        const size_t b0 = (u0 + 255) / 256, b1 = (u1 + 255) / 256;
-        if (ok16(a0) && ok16(a1) && b0 + b1 < (size_t(1) << 31)) {
-            if (b0 + b1 == 0) return;
-            const DequantJobs jobs{{DequantJob{a0.out, a0.q, a0.scale, u0}, DequantJob{a1.out, a1.q, a1.scale, u1}},
-                                   unsigned(b0)};
-            dequantVec16<T><<<unsigned(b0 + b1), 256, 0, s>>>(jobs, DivU64(cols / 16));
-            return;
-        }
-    }
     const size_t nv0 = cols % N == 0 ? a0.rows * cols / N : 0;
     const size_t nv1 = cols % N == 0 ? a1.rows * cols / N : 0;
     const size_t nb0 = (nv0 + kPerBlock - 1) / kPerBlock, nb1 = (nv1 + kPerBlock - 1) / kPerBlock;
@@ -253,7 +221,7 @@ void launchDequant(const DequantArgs &a0, const DequantArgs &a1, size_t cols, hi
         if (nb0 + nb1 == 0) return;
         const DequantJobs jobs{{DequantJob{a0.out, a0.q, a0.scale, nv0}, DequantJob{a1.out, a1.q, a1.scale, nv1}},
                                unsigned(nb0)};
-        dequantVec<T, kDequantU><<<unsigned(nb0 + nb1), 256, 0, s>>>(jobs, DivU64(cols / N));
+        dequantVec<T, kDequantU, kDequantBlock><<<unsigned(nb0 + nb1), kDequantBlock, 0, s>>>(jobs, DivU64(cols / N));
         return;
     }
     for (const DequantArgs *a : {&a0, &a1}) {

@@ -60,11 +60,17 @@ __global__ void __launch_bounds__(blockFor<G>())
     const int nvec = cols / N;
     const size_t base = row * size_t(cols);
 
+    // unconditional loads (a dead row or a slot past the row end reads the row's first
+    // vector; the folds below skip those): loads under a per-lane branch were issued one
+    // round trip at a time (MI355X, bf16: W[1536, 8960] 9.61 -> 9.09 us, KV pair
+    // [32768, 2, 128] 11.79 -> 11.58 us).  The fold keeps its branch: a select there
+    // measured slower on the 8960-wide rows.
+    const size_t lbase = live ? base : 0;
     v4u raw[VMAX];
 #pragma unroll
     for (int v = 0; v < VMAX; ++v) {
         const int vi = lane + v * G;
-        if (live && vi < nvec) raw[v] = load16Stream<T>(in, base + size_t(vi) * N);
+        raw[v] = load16Stream<T>(in, lbase + size_t(vi < nvec ? vi : 0) * N);
     }
     // amax: integer max of the magnitude bits; the float rule only for a row with a NaN
     // (the test is uniform over the group, so the group's lanes all take it)
@@ -113,6 +119,74 @@ __global__ void __launch_bounds__(blockFor<G>())
     }
 }
 
+// Rows of at most 64 * V vectors: one wavefront per row, four rows per block, the row's
+// vectors lane + 64 v in registers; amax by wave butterflies only (no LDS, no block
+// barrier).  Same results as quantRows.  Measured on MI355X (W[8960, 1536] bf16, graph-
+// replayed medians over >= 1 GiB of rotating sets): 8.64 us against 9.0 us for quantRows
+// with the same lane plan; V = 4 ran faster than V = 3 (8.94 us) on these 192-vector rows,
+// so the launcher uses V = 4 for rows of 65..256 vectors.
+template <typename T, int V>
+__global__ void __launch_bounds__(256)
+    quantWave(QuantJobs jobs, int nvec) {
+    using F = Fmt<T>;
+    constexpr int N = F::kVec;
+    const bool second = blockIdx.x >= jobs.nb0; // block-uniform
+    int8_t *__restrict__ q = second ? jobs.job[1].q : jobs.job[0].q;
+    float *__restrict__ scale = second ? jobs.job[1].scale : jobs.job[0].scale;
+    const v4u *__restrict__ in = static_cast<const v4u *>(second ? jobs.job[1].in : jobs.job[0].in);
+    const size_t rows = second ? jobs.job[1].rows : jobs.job[0].rows;
+    const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
+    const int lane = int(threadIdx.x) % kWave;
+    const size_t row = size_t(blk) * (256 / kWave) + threadIdx.x / kWave;
+    const bool live = row < rows;
+    const size_t base = (live ? row : 0) * size_t(nvec); // in vectors
+    v4u raw[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int vi = lane + v * kWave;
+        raw[v] = __builtin_nontemporal_load(in + base + (vi < nvec ? vi : 0));
+    }
+    // vectors past the row end fold as zeros: a select, not a branch (a branch here made
+    // the compiler wait for every load before the first fold)
+    using A = AbsBits<T>;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+        bits = A::fold(bits, lane + v * kWave < nvec ? raw[v] : v4u{0u, 0u, 0u, 0u});
+    bits = waveGroupReduce<kWave, MaxU32Op>(A::finish(bits));
+    float amax = A::value(bits);
+    if (__builtin_expect(bits > A::kInf, 0)) { // a NaN in the row: the float rule
+        amax = 0.0f;
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            float x[N];
+            F::unpack(lane + v * kWave < nvec ? raw[v] : v4u{0u, 0u, 0u, 0u}, x);
+#pragma unroll
+            for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(x[e]));
+        }
+        amax = waveGroupReduce<kWave, MaxOp>(amax);
+    }
+    const RowQuantizer qz(amax);
+    if (live && lane == 0) scale[row] = qz.scale;
+    const size_t cbase = base * N; // in codes
+    if (__builtin_expect(qz.exact_only, 0)) {
+        for (int j = lane; live && j < nvec * N; j += kWave)
+            q[cbase + j] = int8_t(codeOf(F::get(in, cbase + j), amax, qz.scale));
+        return;
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+        const int vi = lane + v * kWave;
+        if (live && vi < nvec) {
+            float x[N];
+            uint32_t c[N];
+            F::unpack(raw[v], x);
+            qz.fastCodes<N, std::is_same_v<T, F32>>(x, c);
+            storeCodes<N>(q, cbase + size_t(vi) * N, c);
+        }
+    }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256)
     quantRowsScalar(int8_t *q, float *scale, const void *in, size_t rows, size_t cols) {
@@ -135,6 +209,12 @@ void launch(const QuantJob &j0, const QuantJob &j1, size_t cols, hipStream_t s) 
         return j.rows == 0 || (aligned16(j.in) && reinterpret_cast<uintptr_t>(j.q) % N == 0);
     };
     const bool vec = cols > 0 && cols % N == 0 && cols <= size_t(INT32_MAX) && vecOk(j0) && vecOk(j1);
+    if (vec && cols / N > 64 && cols / N <= 256) {
+        const unsigned nb0 = blocksFor(j0.rows, 256 / kWave), nb1 = blocksFor(j1.rows, 256 / kWave);
+        if (nb0 + nb1 == 0) return;
+        quantWave<T, 4><<<nb0 + nb1, 256, 0, s>>>(QuantJobs{{j0, j1}, nb0}, int(cols / N));
+        return;
+    }
     RowPlan plan = vec ? planRow(cols / N) : RowPlan{};
     bool done = false;
     withPlan(plan, [&](auto g, auto v) {
