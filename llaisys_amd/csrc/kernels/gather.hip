@@ -12,8 +12,10 @@
 // per row) before any store; when every id is in range (the normal case) the stores are one
 // straight run, so each row's stores wait only for that row's loads.  R rows per wave keep
 // R * 3 KB in flight per wave behind a single id round trip: measured on MI355X (8192
-// random ids into [151936, 1536] bf16, >= 1 GiB of rotating sets) 9.1 us with R = 8,
-// against 10.2 us with one row per wave and 9.6 us with R = 4.  Other rows: one wavefront
+// random ids into [151936, 1536] bf16, >= 1 GiB of rotating sets) 9.14 us with R = 8 (1024
+// waves, one per SIMD), against 9.87 / 10.15 / 9.96 / 9.33 / 9.18 us with R = 4 / 6 / 10
+// / 12 / 16 and 9.7 us with one row per wave and a scalar id load; a copy kernel of the
+// same bytes takes 9.07 us.  Other rows: one wavefront
 // per id, UNROLL units in flight per lane.  Table rows use ordinary loads (non-temporal
 // gathers measured 6-7 % slower), output rows non-temporal stores.
 #include "common.hpp"
@@ -102,7 +104,9 @@ __global__ void __launch_bounds__(kWave)
 template <int PL, bool kFull>
 void launchMultiAs(void *out, const void *index, bool i64, size_t n, const void *w, size_t vocab,
                    size_t units, int *err, hipStream_t s) {
-    constexpr int R = kMultiUnits / PL;
+    // 8 KB rows (Llama-8B): one row per wave, 42.2 us against 44.8 us with 3 rows per
+    // wave (16384 random ids into [128256, 4096] bf16, >= 1 GiB of rotating sets)
+    constexpr int R = PL >= 8 ? 1 : kMultiUnits / PL;
     const unsigned grid = blocksFor(n, R);
     if (i64)
         gatherMulti<true, R, PL, kFull><<<grid, kWave, 0, s>>>(static_cast<v4u *>(out), index, n,
