@@ -58,6 +58,29 @@ def time_launches(hip, stream, fn, batch=64, reps=REPS, warmup=WARMUP):
     return float(np.median(t)), float(t.mean())
 
 
+def time_graph(L, hip, stream, fn, nbytes=None, batch=64, reps=REPS, warmup=2):
+    """Median and mean time in us of one call fn(i), from replays of one HIP graph that holds
+    n consecutive calls fn(0) .. fn(n - 1): n = 64, or the number of rotating buffer sets of
+    a case of `nbytes` per call if that is larger, so every replay walks each set once.  The
+    graph keeps host work out of the timed region: launched eagerly from Python, a call
+    costs ~3.7 us of host time, more than a small kernel takes."""
+    n = batch if nbytes is None else max(batch, int(min(4096, -(-FOOTPRINT // max(1, nbytes)))))
+    graph = L.Graph.capture()
+    for i in range(n):
+        fn(i)
+    graph.end()
+    for _ in range(warmup):
+        graph.launch()
+    evs = hip.events(reps + 1)
+    hip.record(evs[0], stream)
+    for r in range(reps):
+        graph.launch()
+        hip.record(evs[r + 1], stream)
+    t = np.array([hip.elapsed_ms(evs[r], evs[r + 1]) * 1e3 / n for r in range(reps)])
+    del graph
+    return float(np.median(t)), float(t.mean())
+
+
 def rate(name_us, nbytes, mean_us=None):
     gbs = nbytes / (name_us * 1e-6) / 1e9
     r = {"us": round(name_us, 3), "bytes": nbytes, "GB_s": round(gbs, 1),
@@ -617,7 +640,7 @@ def time_cases(L, hip, stream, e0, e1, steps, cases):
     stream; kind "bytes" is rated against HBM, "flops" against the bf16 MFMA peak."""
     res = {}
     for name, kind, amount, fn in cases:
-        us, mean = time_launches(hip, stream, fn)
+        us, mean = time_graph(L, hip, stream, fn)
         if kind == "bytes":
             res[name] = dict(rate(us, amount, mean), bound="hbm")
         else:
@@ -991,7 +1014,7 @@ def main():
     c1, c1pool = config1_ops(L, np.random.default_rng(3))
     per_op = {}
     for name, nbytes, fn in c1:
-        med, mean = time_launches(hip, stream, fn)
+        med, mean = time_graph(L, hip, stream, fn, nbytes)
         per_op[name] = rate(med, nbytes, mean)
     assert L.take_device_error() == 0
     del c1, c1pool
@@ -1029,7 +1052,7 @@ def main():
         cases, pool = config_ops(L, np.random.default_rng(9))
         configs = {}
         for cfg, name, nbytes, launches, fn in cases:
-            med, mean = time_launches(hip, stream, fn)
+            med, mean = time_graph(L, hip, stream, fn, nbytes)
             configs.setdefault(cfg, {})[name] = dict(rate(med, nbytes, mean), launches=launches)
         assert L.take_device_error() == 0
         del cases, pool
