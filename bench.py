@@ -35,6 +35,7 @@ T, H, V, NH, NKV, D, I = 8192, 1536, 151936, 12, 2, 128, 8960
 NSETS = 4
 REPS, WARMUP = 60, 10      # per-op timing: median of REPS launches after WARMUP
 FOOTPRINT = 1 << 30         # bytes each per-op loop rotates through (4x the 256 MB MALL)
+EAGER = False               # --eager: per-op cases launched one by one (kernel tracing)
 
 
 def time_launches(hip, stream, fn, batch=64, reps=REPS, warmup=WARMUP):
@@ -64,6 +65,8 @@ def time_graph(L, hip, stream, fn, nbytes=None, batch=64, reps=REPS, warmup=2):
     a case of `nbytes` per call if that is larger, so every replay walks each set once.  The
     graph keeps host work out of the timed region: launched eagerly from Python, a call
     costs ~3.7 us of host time, more than a small kernel takes."""
+    if EAGER:
+        return time_launches(hip, stream, fn, batch=batch, reps=reps)
     n = batch if nbytes is None else max(batch, int(min(4096, -(-FOOTPRINT // max(1, nbytes)))))
     graph = L.Graph.capture()
     for i in range(n):
@@ -912,10 +915,15 @@ def main():
                     help="with --decode-only: the fused INT8 chain only, eager launches (kernel tracing)")
     ap.add_argument("--linear-only", action="store_true",
                     help="only the linear and rearrange lines (profiling); prints their JSON")
+    ap.add_argument("--eager", action="store_true",
+                    help="time per-op cases as eager launches instead of graph replays "
+                         "(rocprofv3 kernel tracing of graph replays crashes the host process)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="3 dispatches of a 256 MiB device copy (counter calibration), then 3 of "
                          "each config-1 op, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the per-layer "
               "ops shard by rows with no exchange; see the sharding notes)", file=sys.stderr)
@@ -978,13 +986,20 @@ def main():
         wq, wsc, wd = L.Tensor((I, H), I8, **dev), L.Tensor((I,), F32, **dev), L.Tensor((I, H), BF, **dev)
         for _ in range(3):
             L.Ops.rope_kv_append_int8(qo, q, k, v, pos, 1e6, kc, ks, vc, vs, 0)
+        # the chain's add + rms_norm at 2048 rows (the one-vector-per-lane row kernel)
+        x2, r2 = (L.Tensor.from_numpy(bf16(rng, (t, H)), BF, **dev) for _ in range(2))
+        y2, h2 = L.Tensor((t, H), BF, **dev), L.Tensor((t, H), BF, **dev)
+        nw = L.Tensor.from_numpy(bf16(rng, (H,), 0.1, 1.0), BF, **dev)
+        for _ in range(3):
+            L.Ops.add_rms_norm(y2, h2, x2, r2, nw, 1e-6)
         for _ in range(3):
             L.Ops.quantize_int8(wq, wsc, w)
         for _ in range(3):
             L.Ops.dequantize_int8(wd, wq, wsc)
         api.device_synchronize()
         print(json.dumps({"probe": "copy 256 MiB x3, then each config-1 op x3, RoPE+KV append (2048 "
-                                   "tokens) x3, quantize / dequantize W[8960,1536] x3",
+                                   "tokens) x3, add+rms_norm [2048,1536] x3, quantize / dequantize "
+                                   "W[8960,1536] x3",
                           "ops": {name: b for name, b, _ in wl.ops()}}))
         return
     ops = wl.ops()
