@@ -464,6 +464,7 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
     const size_t qi = min(q0 + size_t(n), a.seq - 1); // this lane's query (clamped for loads)
     const size_t vis_q = visibleKeys(a.total, a.seq, qi);
     const size_t vis_blk = visibleKeys(a.total, a.seq, min(q0 + kMfmaQ - 1, a.seq - 1));
+    const size_t vis_first = visibleKeys(a.total, a.seq, q0); // the fewest keys any query sees
     const size_t ntiles = (vis_blk + kMfmaKT - 1) / kMfmaKT;
     const float c2 = a.scale * 1.4426950408889634f; // scores to base-2 exponents
 
@@ -557,7 +558,9 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
         if (it + 1 < tcount) loadTile(kt0 + kMfmaKT); // in flight during this step's math
         __syncthreads(); // tile ti in LDS; every wave is past the step that read buf last
         if (kSplit && it >= tcount) continue; // the shorter half idles through its last step
-        // keys of this lane's query visible in the tile: offsets < nvis
+        // keys of this lane's query visible in the tile: offsets < nvis.  A tile every query
+        // of the block sees whole (all but the causal diagonal) skips the masking.
+        const bool whole = kt0 + kMfmaKT <= vis_first; // block-uniform
         const int nvis = int(min(vis_q - min(vis_q, kt0), size_t(kMfmaKT)));
         float p[4][4];
         float mx = m;
@@ -573,21 +576,22 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int off = 32 * (t / 2) + 8 * g4 + 4 * (t % 2) + i; // key of D row 4g + i
-                p[t][i] = off < nvis ? acc[i] : -INFINITY;
+                p[t][i] = whole || off < nvis ? acc[i] : -INFINITY;
                 mx = fmaxf(mx, p[t][i]);
             }
         }
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        // key 0 is visible to every query, so m is finite after the first tile
-        const float mc = mx * c2;
+        // exp(scale * (s - max)) as 2^(s * c2 - max * c2); a masked key (-inf) gets weight 0.
+        // Key 0 is visible to every query, so mx = -inf only when every score so far is -inf;
+        // mc = 0 then keeps 2^(-inf - mc) at 0 instead of NaN, with no per-score select.
+        const float mc = mx == -INFINITY ? 0.0f : mx * c2;
         float ps = 0.0f;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                // exp(scale * (s - max)) as 2^(s * c2 - max * c2); a masked key is weight 0
-                p[t][i] = p[t][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][i], c2, -mc));
+                p[t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][i], c2, -mc));
                 ps += p[t][i];
             }
         if (__builtin_expect(__any(mx != m), 0)) { // rescale only when a max moved
@@ -600,14 +604,16 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
         lsum += ps;
 #pragma unroll
         for (int p2 = 0; p2 < 2; ++p2) {
-            bf16x8 bhi, blo;
+            // P as bf16 hi + lo, two keys per conversion: key 32 p2 + 8g + j is p[2 p2 + j / 4][j % 4]
+            uint32_t hw[4], lw[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float x = p[2 * p2 + j / 4][j % 4]; // key 32 p2 + 8g + j
-                const __bf16 hi = __bf16(x);
-                bhi[j] = hi;
-                blo[j] = __bf16(x - float(hi));
+            for (int w = 0; w < 4; ++w) {
+                const float x0 = p[2 * p2 + w / 2][2 * (w % 2)], x1 = p[2 * p2 + w / 2][2 * (w % 2) + 1];
+                hw[w] = Bf16Cvt::narrow2Q(x0, x1);
+                lw[w] = Bf16Cvt::narrow2Q(x0 - __uint_as_float(hw[w] << 16), x1 - __uint_as_float(hw[w] & 0xFFFF0000u));
             }
+            const bf16x8 bhi = asBf16x8(v4u{hw[0], hw[1], hw[2], hw[3]});
+            const bf16x8 blo = asBf16x8(v4u{lw[0], lw[1], lw[2], lw[3]});
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const v4u vv = *reinterpret_cast<const v4u *>(&vt[buf][16 * dt + n][32 * p2 + 8 * g4]);
