@@ -574,12 +574,21 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kv), qreg[kb], acc, 0, 0, 0);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int off = 32 * (t / 2) + 8 * g4 + 4 * (t % 2) + i; // key of D row 4g + i
-                p[t][i] = whole || off < nvis ? acc[i] : -INFINITY;
-                mx = fmaxf(mx, p[t][i]);
-            }
+            for (int i = 0; i < 4; ++i) p[t][i] = acc[i];
         }
+        if (!whole) { // the causal diagonal: keys past this lane's query are masked
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int off = 32 * (t / 2) + 8 * g4 + 4 * (t % 2) + i; // key of D row 4g + i
+                    p[t][i] = off < nvis ? p[t][i] : -INFINITY;
+                }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, p[t][i]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
         // exp(scale * (s - max)) as 2^(s * c2 - max * c2); a masked key (-inf) gets weight 0.
