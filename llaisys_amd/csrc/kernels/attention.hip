@@ -774,20 +774,30 @@ __global__ void __launch_bounds__(kWave * kDecWaves)
             for (int kb = 0; kb < KB; ++kb)
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(ka[t][kb]), qreg[kb], acc, 0, 0, 0);
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                p[t][ii] = 8 * g4 + 4 * t + ii < nk ? acc[ii] : -INFINITY; // key of D row 4g + ii
-                mx = fmaxf(mx, p[t][ii]);
-            }
+            for (int ii = 0; ii < 4; ++ii) p[t][ii] = acc[ii];
         }
+        if (nk < kDecKT) { // the chunk's last, partial step: keys past its end are masked
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) // key of D row 4g + ii
+                    p[t][ii] = 8 * g4 + 4 * t + ii < nk ? p[t][ii] : -INFINITY;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) mx = fmaxf(mx, p[t][ii]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
         mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-        const float mc = mx * c2;
+        // a masked key (-inf) gets weight 0; mc = 0 while every score is -inf keeps it 0
+        // rather than NaN, with no per-score select
+        const float mc = mx == -INFINITY ? 0.0f : mx * c2;
         float ps = 0.0f;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                p[t][ii] = p[t][ii] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][ii], c2, -mc));
+                p[t][ii] = __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][ii], c2, -mc));
                 ps += p[t][ii];
             }
         if (__builtin_expect(__any(mx != m), 0)) {
@@ -817,14 +827,16 @@ __global__ void __launch_bounds__(kWave * kDecWaves)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        bf16x8 bhi, blo;
+        // P as bf16 hi + lo, two keys per conversion (key 8g + j is p[j / 4][j % 4])
+        uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float x = p[j / 4][j % 4]; // key 8g + j
-            const __bf16 hi = __bf16(x);
-            bhi[j] = hi;
-            blo[j] = __bf16(x - float(hi));
+        for (int w = 0; w < 4; ++w) {
+            const float x0 = p[w / 2][2 * (w % 2)], x1 = p[w / 2][2 * (w % 2) + 1];
+            hw[w] = Bf16Cvt::narrow2Q(x0, x1);
+            lw[w] = Bf16Cvt::narrow2Q(x0 - __uint_as_float(hw[w] << 16), x1 - __uint_as_float(hw[w] & 0xFFFF0000u));
         }
+        const bf16x8 bhi = asBf16x8(v4u{hw[0], hw[1], hw[2], hw[3]});
+        const bf16x8 blo = asBf16x8(v4u{lw[0], lw[1], lw[2], lw[3]});
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             const v4u vv = *reinterpret_cast<const v4u *>(&vt[wave][16 * dt + n][8 * g4]);
