@@ -724,6 +724,10 @@ __global__ void __launch_bounds__(kWave * kDecWaves)
 
     for (size_t kt0 = k0 + size_t(wave) * kDecKT; kt0 < k1; kt0 += size_t(kDecWaves) * kDecKT) {
         const int nk = int(min(k1 - kt0, size_t(kDecKT)));
+        const bool part = nk < kDecKT; // the chunk's last, partial step (wave-uniform)
+        // Loads are unconditional: a key past the step reads the step's first key and is
+        // zeroed after the load (partial steps only).  Loads under per-lane branches were
+        // issued one round trip at a time.
         // V pieces: lane takes pairs (2kp, 2kp + 1) x 8 columns dc .. dc + 7, 4 per lane
         v4u vr[4][2];
 #pragma unroll
@@ -731,8 +735,8 @@ __global__ void __launch_bounds__(kWave * kDecWaves)
             const int idx = lane + kWave * r, kp = idx % 16, dc = 8 * (idx / 16);
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
-                vr[r][e] = v4u{0u, 0u, 0u, 0u}; // keys past the step: zeros
-                if (2 * kp + e < nk) vr[r][e] = loadRow8<kInt8>(a.v, (kt0 + 2 * kp + e) * rstride + g, dc);
+                const int key = 2 * kp + e < nk ? 2 * kp + e : 0;
+                vr[r][e] = loadRow8<kInt8>(a.v, (kt0 + key) * rstride + g, dc);
             }
         }
         // K operands: tile t, row n -> key 8(n / 4) + 4t + n % 4
@@ -740,18 +744,31 @@ __global__ void __launch_bounds__(kWave * kDecWaves)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
             const int off = 8 * (n / 4) + 4 * t + n % 4;
+            const int key = off < nk ? off : 0;
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) {
-                ka[t][kb] = v4u{0u, 0u, 0u, 0u};
-                if (off < nk) ka[t][kb] = loadRow8<kInt8>(a.k, (kt0 + off) * rstride + g, 32 * kb + 8 * g4);
+            for (int kb = 0; kb < KB; ++kb)
+                ka[t][kb] = loadRow8<kInt8>(a.k, (kt0 + key) * rstride + g, 32 * kb + 8 * g4);
+        }
+        if (part) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kp = (lane + kWave * r) % 16;
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    if (2 * kp + e >= nk) vr[r][e] = v4u{0u, 0u, 0u, 0u};
             }
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int kb = 0; kb < KB; ++kb)
+                    if (8 * (n / 4) + 4 * t + n % 4 >= nk) ka[t][kb] = v4u{0u, 0u, 0u, 0u};
         }
         if constexpr (kInt8) {
             // the step's scales, one load per lane (K for lanes 0-31, V for 32-63), handed
             // to the lanes that convert a row by lane shuffles
             const int sk = lane % kDecKT;
-            float sreg = 0.0f;
-            if (sk < nk) sreg = (lane < kDecKT ? a.ks : a.vs)[(kt0 + sk) * rstride + g];
+            float sreg = (lane < kDecKT ? a.ks : a.vs)[(kt0 + (sk < nk ? sk : 0)) * rstride + g];
+            if (sk >= nk) sreg = 0.0f;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 const float sc = __shfl(sreg, 8 * (n / 4) + 4 * t + n % 4, kWave);
