@@ -353,7 +353,10 @@ def with_outliers(rng, shape, dt, scale):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("shape", [(8960, 1536), (1536, 8960), (4096, 128), (5, 1001), (3, 20000), (7, 8)])
+@pytest.mark.parametrize("shape", [(8960, 1536), (1536, 8960), (4096, 128), (5, 1001), (3, 20000), (7, 8),
+                                   # one wave per row with a partial last lane group (125 / 129
+                                   # bf16 vectors, 250 f32), and exactly 256 bf16 vectors
+                                   (33, 1000), (17, 1032), (9, 2048)])
 def test_quantize_dequantize(dt, shape):
     rng = np.random.default_rng(shape[0])
     x = with_outliers(rng, shape, dt, 0.02)
@@ -771,8 +774,9 @@ def quant_edge_rows(dt, cols=256, seed=5):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-def test_quantize_boundary_rows(dt):
-    x = quant_edge_rows(dt)
+@pytest.mark.parametrize("cols", [256, 1536, 1000])  # lane-group plan; one wave per row (full / partial)
+def test_quantize_boundary_rows(dt, cols):
+    x = quant_edge_rows(dt, cols=cols)
     q, s = empty(x.shape, L.DataType.I8), empty(x.shape[:-1], L.DataType.F32)
     L.Ops.quantize_int8(q, s, dev(x, DTS[dt]))
     eq, es = oracle.quantize_int8(x)
