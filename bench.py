@@ -699,13 +699,14 @@ def linear_ops(L, rng):
                     lambda i, xp=xp, w=w, op_=op_: O.linear(op_, xp, w[0])))
         ops.append((f"prefill 2048 tokens, {label}, INT8 weights (W8A16)", "flops", fl,
                     lambda i, xp=xp, q=q, sc=sc, op_=op_: O.linear_w8a16(op_, xp, q[0], sc[0])))
-    # lm_head: one set (467 MB already exceeds the Infinity Cache)
-    wl, ql, scl = weights(V, H, 1)
+    # lm_head: sets sized by the INT8 codes (234 MB alone would sit in the 256 MB Infinity Cache)
+    nl = P.sets_for(V * H)
+    wl, ql, scl = weights(V, H, nl)
     xl, ol = P.fill((1, H), BF, 1)[0], P.empty((1, V), BF, 1)[0]
     ops.append(("decode 1 token, lm_head [151936, 1536], bf16 weights", "bytes", V * H * 2 + (H + V) * 2,
-                lambda i: O.linear(ol, xl, wl[0])))
+                lambda i: O.linear(ol, xl, wl[i % nl])))
     ops.append(("decode 1 token, lm_head [151936, 1536], INT8 weights (W8A16)", "bytes",
-                V * (H + 4) + (H + V) * 2, lambda i: O.linear_w8a16(ol, xl, ql[0], scl[0])))
+                V * (H + 4) + (H + V) * 2, lambda i: O.linear_w8a16(ol, xl, ql[i % nl], scl[i % nl])))
     return ops, P
 
 

@@ -9,9 +9,10 @@
 // accumulation error.
 //
 // Design, by row count M (the launcher at the end picks the kernel):
-//  - M <= 2 (decode), linearGemv: HBM-bound on the weights, one wave per output channel
-//    streaming its weight row in 1 KB load instructions, f32 FMAs, a butterfly; no LDS.
-//    INT8 weights with N >= 4096 go to linearSkinny instead.
+//  - M = 1 (decode), linearGemvRow: HBM-bound on the weights, one wave per output channel
+//    with its whole weight row requested up front in 1 KB load instructions, x in LDS, f32
+//    FMAs, a butterfly.  linearGemv (the same sum, no LDS) takes rows too long for that and
+//    M = 2 (INT8 weights with N >= 4096 and M = 2 go to linearSkinny instead).
 //  - M <= 16, linearSkinny: HBM-bound; a block owns 16 channels, its waves split K, load
 //    weight rows row-contiguously and transpose them through a per-wave LDS tile into
 //    v_mfma_f32_16x16x32 operands; partials summed in LDS in wave order.
@@ -432,6 +433,106 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// Dot product of one 16-byte weight chunk (8 bf16 / f16 weights or 16 INT8 codes) with the
+// matching x elements in LDS, in f32.
+template <typename T, bool kInt8>
+__device__ __forceinline__ float gemvChunk(const v4u &w, const uint16_t *xp) {
+    float s = 0.0f;
+    if constexpr (kInt8) {
+        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+        float xf[16];
+        Fmt<T>::unpack(*reinterpret_cast<const v4u *>(xp), xf);
+        Fmt<T>::unpack(*reinterpret_cast<const v4u *>(xp + 8), xf + 8);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s = __builtin_fmaf(xf[e], float(int8_t(ww[e / 4] >> (8 * (e % 4)))), s);
+    } else {
+        float xf[8], wf[8];
+        Fmt<T>::unpack(*reinterpret_cast<const v4u *>(xp), xf);
+        Fmt<T>::unpack(w, wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s = __builtin_fmaf(xf[e], wf[e], s);
+    }
+    return s;
+}
+
+// out[n] of one row: the per-channel scale (INT8), the bias, the reference rounding.
+template <typename T, bool kInt8>
+__device__ __forceinline__ void gemvStore(const LinearArgs &a, int n, float t) {
+    if constexpr (kInt8) t = a.scale[n] * t;
+    if (a.bias) t = t + Fmt<T>::get(a.bias, n);
+    Fmt<T>::put(a.out, n, t);
+}
+
+// One row (decode): linearGemv's sum -- per output channel one wave, lane chunks lane,
+// lane + 64, ... in one FMA chain, then the same butterfly -- with every weight chunk of the
+// wave's C channels requested before anything else (C x J per lane) and x staged once per
+// block in LDS (kLds) or read through L1 / L2, so the loads are all in flight behind one x
+// round trip.  Same bits as linearGemv (and
+// as the fused rms_norm -> projection, which sums the same way).  Measured on MI355X (M = 1,
+// >= 1 GiB of rotating weight sets): W8A16 [8960, 1536] 5.47 us against 6.79 us for
+// linearSkinny and 7.55 us for linearGemv; bf16 [8960, 1536] 6.17 against 7.39 us; W8A16
+// [1536, 8960] 6.41 against 7.00 us; bf16 [1536, 8960] 8.28 against 9.38 us.
+template <typename T, bool kInt8, int J, int C, bool kLds>
+__global__ void __launch_bounds__(256)
+    linearGemvRow(LinearArgs a) {
+    using F = Fmt<T>;
+    constexpr int E = kInt8 ? 16 : 8; // weight elements per 16-byte chunk
+    extern __shared__ __align__(16) char xs_raw[];
+    const uint16_t *xs = kLds ? reinterpret_cast<const uint16_t *>(xs_raw) : static_cast<const uint16_t *>(a.x);
+    const int lane = int(threadIdx.x) % kWave;
+    const int n0 = (int(blockIdx.x) * 4 + int(threadIdx.x) / kWave) * C; // wave-uniform
+    const int nc = a.K / E;
+    // a channel past the last loads a valid row and stores nothing (its wave still joins the
+    // block barrier); a chunk past the row end reads chunk 0 and is skipped
+    v4u wv[C][J];
+#pragma unroll
+    for (int ci = 0; ci < C; ++ci) {
+        const int n = n0 + ci;
+        const char *wrow = static_cast<const char *>(a.w) + size_t(n < a.N ? n : a.N - 1) * a.K * (kInt8 ? 1 : 2);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int c = lane + kWave * j;
+            wv[ci][j] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(wrow + size_t(c < nc ? c : 0) * 16));
+        }
+    }
+    if constexpr (kLds) {
+        for (int i = int(threadIdx.x); i < a.K / 8; i += 256)
+            reinterpret_cast<v4u *>(xs_raw)[i] = reinterpret_cast<const v4u *>(a.x)[i];
+        __syncthreads();
+    }
+#pragma unroll
+    for (int ci = 0; ci < C; ++ci) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int c = lane + kWave * j;
+            if (c >= nc) continue; // (the lane's remaining chunks are past the end too)
+            float wf[E];
+            if constexpr (kInt8) {
+                const uint32_t ww[4] = {wv[ci][j].x, wv[ci][j].y, wv[ci][j].z, wv[ci][j].w};
+#pragma unroll
+                for (int e = 0; e < E; ++e) wf[e] = float(int8_t(ww[e / 4] >> (8 * (e % 4))));
+            } else {
+                F::unpack(wv[ci][j], wf);
+            }
+#pragma unroll
+            for (int h = 0; h < E / 8; ++h) {
+                float xf[8];
+                F::unpack(*reinterpret_cast<const v4u *>(xs + c * E + 8 * h), xf);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(xf[e], wf[8 * h + e], acc);
+            }
+        }
+        float t = waveGroupReduce<kWave, SumOp>(acc);
+        const int n = n0 + ci;
+        if (lane == 0 && n < a.N) {
+            if constexpr (kInt8) t = a.scale[n] * t;
+            if (a.bias) t = t + F::get(a.bias, n);
+            F::put(a.out, n, t);
+        }
+    }
+}
+
 // Any shape and type: one thread per output, the sum in the reference's order.
 template <typename T, bool kInt8>
 __global__ void __launch_bounds__(256)
@@ -449,6 +550,41 @@ __global__ void __launch_bounds__(256)
     Fmt<T>::put(a.out, idx, sum);
 }
 
+// One row: linearGemvRow with J = ceil(chunks / 64) <= 24; false (linearGemv, the same sum)
+// otherwise.  Variants (event timings of 5-16 rotating weight sets, all bit-identical):
+//  - x staged in LDS by the block, except INT8 weights over at most 4096 channels, where the
+//    block's staging is not hidden behind its 4 rows of codes and x is read from L1 / L2:
+//    [3584, 3584] 5.54 -> 5.23 us, [1536, 8960] 6.26 -> 5.86 us, [3584, 18944] 18.7 -> 17.5 us
+//    (larger N loses: [18944, 3584] 14.4 -> 15.3 us; bf16 [1536, 8960] 8.1 -> 8.7 us);
+//  - 4 channels per wave for INT8 rows of at most 2 chunks per lane over 65536+ channels (the
+//    lm_head), which spreads the block's x staging over 16 rows: [151936, 1536] 46.0 -> 40.0 us
+//    (at [8960, 1536] it loses, 5.45 -> 6.57 us: too few blocks).
+template <typename T, bool kInt8, int C, bool kLds, int J>
+bool launchRowJ(const LinearArgs &a, int j, hipStream_t s) {
+    if constexpr (J > 0) {
+        if (j == J) {
+            const unsigned blocks = unsigned((a.N + 4 * C - 1) / (4 * C));
+            linearGemvRow<T, kInt8, J, C, kLds><<<blocks, 256, kLds ? size_t(a.K) * 2 : 0, s>>>(a);
+            return true;
+        }
+        return launchRowJ<T, kInt8, C, kLds, J - 1>(a, j, s);
+    }
+    return false;
+}
+
+template <typename T, bool kInt8>
+bool launchGemv1(const LinearArgs &a, hipStream_t s) {
+    constexpr int E = kInt8 ? 16 : 8;
+    if (a.K % E != 0 || size_t(a.K) * 2 > 64 * 1024) return false;
+    const int j = (a.K / E + kWave - 1) / kWave;
+    if (j < 1 || j > 24) return false;
+    if constexpr (kInt8) {
+        if (a.N <= 4096) return launchRowJ<T, true, 1, false, 24>(a, j, s);
+        if (a.N >= 65536 && j <= 2) return launchRowJ<T, true, 4, true, 2>(a, j, s);
+    }
+    return launchRowJ<T, kInt8, 1, true, 24>(a, j, s);
+}
+
 template <typename T, bool kInt8>
 void launch(const LinearArgs &a, hipStream_t s) {
     if (a.M == 0 || a.N == 0) return;
@@ -461,7 +597,11 @@ void launch(const LinearArgs &a, hipStream_t s) {
             // under the HBM time -- always for 16-bit weights; for INT8 weights (16 codes per
             // 16 bytes to convert) only when there are too few 16-channel tiles for the MFMA
             // kernel to occupy the chip
-            if (a.M <= 2 && (!kInt8 || (a.N + 15) / 16 < 256)) {
+            // one row: the VALU sum of linearGemv (linearGemvRow when the row fits its
+            // registers) -- also for INT8 weights, whatever N, so that the fused rms_norm ->
+            // projection, which sums the same way, matches it bit for bit
+            if (a.M == 1 && launchGemv1<T, kInt8>(a, s)) return;
+            if (a.M == 1 || (a.M == 2 && (!kInt8 || (a.N + 15) / 16 < 256))) {
                 const unsigned blocks = unsigned((a.N + 3) / 4);
                 if (a.M == 1)
                     linearGemv<T, kInt8, 1><<<blocks, 256, 0, s>>>(a);

@@ -10,10 +10,8 @@
 //        same FMAs as the one-row linearGemv kernel, then the same butterfly,
 //   out = y, or swiglu(T(gate), T(up)) as src/ops/swiglu/cpu/swiglu_cpu.cpp:15-20 over the
 //        weight rows [0, N) (gate) and [N, 2N) (up).
-//   (INT8 weights over 4096 or more channels: the skinny MFMA loop the separate linear takes
-//   there, with the same K split and the same order of the waves' partials.)
 // So the fused output equals rmsNorm -> linear -> swiglu launched separately, bit for bit, for
-// one row (with the skinny form when the norm group is one wave, i.e. hidden <= 2048).
+// one row (the separate linear of one row always sums this way, INT8 weights included).
 //
 // Design (HBM-bound on the weights, one launch instead of three): a block of 4 waves; each
 // wave owns one output channel (with swiglu: its gate and up rows).  The waves first
@@ -137,80 +135,6 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// INT8 weights with N >= 4096 (where the separate linear takes the skinny MFMA kernel): the
-// same skinny loop (linear_common.hpp) over the 16 channels of the block -- and with swiglu
-// their 16 up rows as a second set -- with the normalised row (formed by wave 0, a 64-lane
-// norm group) as the activation operand from LDS.  Before the norm every wave requests its
-// first group's weight rows, so that the loop finds them in L2; the waves' partials are then
-// summed in LDS in wave order, as the separate kernel sums them.
-template <typename T, int VMAX, bool kSwiglu>
-__global__ void __launch_bounds__(1024)
-    linearNormSkinny(NormLinArgs a) {
-    constexpr int R = kSwiglu ? 2 : 1;
-    constexpr int kPitch = lin::skinnyPitch(true);
-    // dynamic LDS: the normalised row (K x 2 bytes), nw transpose tiles of R x 16 rows, nw
-    // partial tiles of R x 256 floats
-    extern __shared__ __align__(16) char smem[];
-    __shared__ float red_n[256 / kWave];
-    const int nw = int(blockDim.x) / kWave;
-    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
-    const int lane = int(threadIdx.x) % kWave;
-    const int r16 = lane % 16, g4 = lane / 16;
-    const int n0 = int(blockIdx.x) * 16;
-    char *xs = smem;
-    char *tile = smem + size_t(a.K) * 2 + size_t(wave) * R * 16 * kPitch;
-    float *red = reinterpret_cast<float *>(smem + size_t(a.K) * 2 + size_t(nw) * R * 16 * kPitch);
-    const char *wbase = static_cast<const char *>(a.w);
-    int rows0[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) rows0[r] = n0 + r * a.N;
-    const int nrows = R * a.N;
-    // the wave's first group of weights is requested before the norm and only consumed after
-    // it (an empty asm use), so that the loop below finds those rows in L2; handing the
-    // registers themselves to the loop measured slower
-    v4u warm[R][lin::SkinnyLoads<true>::kLoads];
-    lin::skinnyLoad<true, R>(warm, wbase, rows0, nrows, a.K, wave, lane);
-    if (threadIdx.x < kWave)
-        lin::normRow<T, kWave, VMAX>(xs, a.in, a.res, a.res_out, a.norm_w, a.eps, a.K, red_n, blockIdx.x == 0);
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int j = 0; j < lin::SkinnyLoads<true>::kLoads; ++j) asm volatile("" ::"v"(warm[r][j]));
-    __syncthreads();
-    const v4u z4 = {0u, 0u, 0u, 0u};
-    const auto xop = [&](int k) {
-        const v4u v = *reinterpret_cast<const v4u *>(xs + size_t(k < a.K ? k : 0) * 2);
-        return r16 == 0 && k < a.K ? v : z4;
-    };
-    lin::f32x4 acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = lin::f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    lin::skinnyGroups<T, true, R>(acc, wbase, rows0, nrows, a.K, tile, wave, nw, lane, xop);
-    // D[m = 4 g + e][n = r16]; one activation row: m = 0
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) red[(size_t(wave) * R + r) * 256 + (4 * g4 + e) * 16 + r16] = acc[r][e];
-    __syncthreads();
-    const int t = int(threadIdx.x);
-    if (t < 16 && n0 + t < a.N) {
-        float y[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int n = rows0[r] + t;
-            float s = 0.0f;
-            for (int w = 0; w < nw; ++w) s += red[(size_t(w) * R + r) * 256 + t];
-            s = a.scale[n] * s;
-            if (a.bias) s = s + Fmt<T>::get(a.bias, n);
-            y[r] = s;
-        }
-        if constexpr (kSwiglu)
-            Fmt<T>::put(a.out, n0 + t, SwigluOp::apply(Fmt<T>::round(y[0]), Fmt<T>::round(y[1])));
-        else
-            Fmt<T>::put(a.out, n0 + t, y[0]);
-    }
-}
-
 template <typename T, bool kInt8, bool kSwiglu, int U>
 void launchU(const NormLinArgs &a, const RowPlan &plan, hipStream_t s) {
     const unsigned blocks = unsigned((a.N + 3) / 4);
@@ -233,25 +157,8 @@ void launchNorm(const NormLinArgs &a, const RowPlan &plan, hipStream_t s) {
         launchU<T, kInt8, kSwiglu, 4>(a, plan, s);
 }
 
-template <typename T, bool kSwiglu>
-void launchSkinny(const NormLinArgs &a, const RowPlan &plan, hipStream_t s) {
-    const int nw = lin::skinnyWaves(a.N, a.K), R = kSwiglu ? 2 : 1;
-    const size_t lds = size_t(a.K) * 2 + size_t(nw) * R * (16 * lin::skinnyPitch(true) + 256 * sizeof(float));
-    const unsigned blocks = unsigned((a.N + 15) / 16);
-    if (plan.vmax == 4)
-        linearNormSkinny<T, 4, kSwiglu><<<blocks, unsigned(nw * kWave), lds, s>>>(a);
-    else
-        linearNormSkinny<T, 8, kSwiglu><<<blocks, unsigned(nw * kWave), lds, s>>>(a);
-}
-
 template <typename T>
 void dispatch(const NormLinArgs &a, const RowPlan &plan, bool int8, bool swiglu, hipStream_t s) {
-    // INT8 weights over 256 or more 16-channel tiles: the skinny MFMA kernel, as the separate
-    // linear of one row takes it
-    if (int8 && (a.N + 15) / 16 >= 256 && plan.group == kWave) {
-        swiglu ? launchSkinny<T, true>(a, plan, s) : launchSkinny<T, false>(a, plan, s);
-        return;
-    }
     if (int8)
         swiglu ? launchNorm<T, true, true>(a, plan, s) : launchNorm<T, true, false>(a, plan, s);
     else

@@ -54,6 +54,9 @@ SHAPES = [
     (256, 1536, 1536), (129, 264, 200), (17, 40, 130), (3, 77, 9), (64, 1536, 1), (1, 8, 1),
     # few rows over few output tiles: K split across blocks (ragged last split, 16 rows)
     (16, 4096, 300), (2, 2056, 40),
+    # one row with partly used chunk slots: two rows per wave (INT8) / one (16-bit) over 1024
+    # inputs, odd channel counts; a 4-wave split row of 3000 / 16384 inputs
+    (1, 1024, 33), (1, 3000, 77), (1, 16384, 3),
 ]
 
 
