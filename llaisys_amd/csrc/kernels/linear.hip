@@ -10,9 +10,10 @@
 //
 // Design, by row count M (the launcher at the end picks the kernel):
 //  - M = 1 (decode), linearGemvRow: HBM-bound on the weights, one wave per output channel
-//    with its whole weight row requested up front in 1 KB load instructions, x in LDS, f32
-//    FMAs, a butterfly.  linearGemv (the same sum, no LDS) takes rows too long for that and
-//    M = 2 (INT8 weights with N >= 4096 and M = 2 go to linearSkinny instead).
+//    (4 for the INT8 lm_head) with its whole weight row requested up front in 1 KB load
+//    instructions, x in LDS or L1 / L2, f32 FMAs, a butterfly.  linearGemv (the same sum,
+//    no LDS) takes rows too long for that and M = 2 (INT8 weights with N >= 4096 and M = 2
+//    go to linearSkinny instead).
 //  - M <= 16, linearSkinny: HBM-bound; a block owns 16 channels, its waves split K, load
 //    weight rows row-contiguously and transpose them through a per-wave LDS tile into
 //    v_mfma_f32_16x16x32 operands; partials summed in LDS in wave order.

@@ -13,9 +13,9 @@
 // So the fused output equals rmsNorm -> linear -> swiglu launched separately, bit for bit, for
 // one row (the separate linear of one row always sums this way, INT8 weights included).
 //
-// Design (HBM-bound on the weights, one launch instead of three): a block of 4 waves; each
-// wave owns one output channel (with swiglu: its gate and up rows).  The waves first
-// request their weight rows' first pass, then the block forms the normalised row in LDS
+// Design (HBM-bound on the weights, one launch instead of three): a block of 4 or 8 waves;
+// each wave owns one output channel (with swiglu: its gate and up rows).  The waves first
+// request their weight rows' first pass (the whole row up to 128 chunks), then the block forms the normalised row in LDS
 // (wave 0 alone for a 64-lane norm group, all 4 waves for a 256-lane one) while those loads
 // are in flight, joins on an LDS-only barrier (the weight loads stay outstanding), and
 // streams the rest of the rows with the activations read from LDS.  Every block re-forms
@@ -45,17 +45,19 @@ struct NormLinArgs {
 };
 
 
-template <typename T, bool kInt8, int G, int VMAX, bool kSwiglu, int U>
-__global__ void __launch_bounds__(256)
+template <typename T, bool kInt8, int G, int VMAX, bool kSwiglu, int U, int NW>
+__global__ void __launch_bounds__(NW * kWave)
     linearNormGemv(NormLinArgs a) {
     using F = Fmt<T>;
     constexpr int E = kInt8 ? 16 : 8;  // weight elements per 16-byte chunk
     constexpr int R = kSwiglu ? 2 : 1; // weight rows per wave; U: chunks per lane and row per pass
-    static_assert(G == kWave || G == 256, "norm group: one wave or the whole block");
+    static_assert(G == kWave || G == 256, "norm group: one wave or 4 waves");
+    // a 4-wave norm group reduces through block-wide barriers, which every wave must reach
+    static_assert(G == kWave || NW == 4, "a 256-lane norm group spans the whole block");
     extern __shared__ __align__(16) char xs[]; // the normalised row, K elements of T
     __shared__ float red[256 / kWave];
     const int lane = int(threadIdx.x) % kWave;
-    const int n = int(blockIdx.x) * 4 + int(threadIdx.x) / kWave; // wave-uniform
+    const int n = int(blockIdx.x) * NW + int(threadIdx.x) / kWave; // wave-uniform
     const bool live = n < a.N; // a wave past the last channel loads a valid row, stores nothing
     const int nc = a.K / E;    // K % E == 0
     const size_t rowB = size_t(a.K) * (kInt8 ? 1 : 2);
@@ -71,12 +73,13 @@ __global__ void __launch_bounds__(256)
         for (int u = 0; u < U; ++u) {
             const int c = c0 + kWave * u < nc ? c0 + kWave * u : 0;
 #pragma unroll
-            for (int r = 0; r < R; ++r) wv[r][u] = *reinterpret_cast<const v4u *>(wrow[r] + size_t(c) * 16);
+            for (int r = 0; r < R; ++r)
+                wv[r][u] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(wrow[r] + size_t(c) * 16));
         }
     };
     loadPass(lane);
 
-    if (G == 256 || threadIdx.x < G)
+    if (threadIdx.x < G)
         lin::normRow<T, G, VMAX>(xs, a.in, a.res, a.res_out, a.norm_w, a.eps, a.K, red, blockIdx.x == 0);
     // the row in LDS is complete (LDS-only barrier: the weight loads stay in flight)
     ldsBarrier();
@@ -135,26 +138,34 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// Waves per block: 8 for up to 4096 channels with a one-wave norm group (twice the channels
+// per norm; q/k/v [2048, 1536] 4.01 -> 3.68 us INT8, 4.66 -> 4.00 us bf16), else 4 (with 8:
+// gate/up + swiglu [2 x 8960, 1536] 9.99 -> 10.46 us INT8, 16 waves 12.67 us).
 template <typename T, bool kInt8, bool kSwiglu, int U>
 void launchU(const NormLinArgs &a, const RowPlan &plan, hipStream_t s) {
-    const unsigned blocks = unsigned((a.N + 3) / 4);
     const size_t lds = size_t(a.K) * 2;
-    if (plan.group == kWave)
-        linearNormGemv<T, kInt8, kWave, 4, kSwiglu, U><<<blocks, 256, lds, s>>>(a);
+    const unsigned b4 = unsigned((a.N + 3) / 4);
+    if (plan.group == kWave && a.N <= 4096)
+        linearNormGemv<T, kInt8, kWave, 4, kSwiglu, U, 8><<<unsigned((a.N + 7) / 8), 512, lds, s>>>(a);
+    else if (plan.group == kWave)
+        linearNormGemv<T, kInt8, kWave, 4, kSwiglu, U, 4><<<b4, 256, lds, s>>>(a);
     else if (plan.vmax == 4)
-        linearNormGemv<T, kInt8, 256, 4, kSwiglu, U><<<blocks, 256, lds, s>>>(a);
+        linearNormGemv<T, kInt8, 256, 4, kSwiglu, U, 4><<<b4, 256, lds, s>>>(a);
     else
-        linearNormGemv<T, kInt8, 256, 8, kSwiglu, U><<<blocks, 256, lds, s>>>(a);
+        linearNormGemv<T, kInt8, 256, 8, kSwiglu, U, 4><<<b4, 256, lds, s>>>(a);
 }
 
-// Chunks per lane and pass: a row of at most 128 chunks (INT8 K <= 2048, 16-bit K <= 1024)
-// in one pass of 2, else passes of 4 (the chunk order per lane is the same either way).
+// Chunks per lane and pass: the whole row in one pass while it is at most 4 chunks per lane
+// (INT8 K <= 4096, 16-bit K <= 2048), else passes of 4 (the chunk order per lane is the
+// same either way).
 template <typename T, bool kInt8, bool kSwiglu>
 void launchNorm(const NormLinArgs &a, const RowPlan &plan, hipStream_t s) {
-    if (a.K / (kInt8 ? 16 : 8) <= 2 * kWave)
-        launchU<T, kInt8, kSwiglu, 2>(a, plan, s);
-    else
-        launchU<T, kInt8, kSwiglu, 4>(a, plan, s);
+    switch ((a.K / (kInt8 ? 16 : 8) + kWave - 1) / kWave) {
+    case 1: launchU<T, kInt8, kSwiglu, 1>(a, plan, s); break;
+    case 2: launchU<T, kInt8, kSwiglu, 2>(a, plan, s); break;
+    case 3: launchU<T, kInt8, kSwiglu, 3>(a, plan, s); break;
+    default: launchU<T, kInt8, kSwiglu, 4>(a, plan, s); break;
+    }
 }
 
 template <typename T>
