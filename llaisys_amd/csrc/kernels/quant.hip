@@ -11,8 +11,10 @@
 // once; amax is an integer max over the packed magnitude bits and the codes come from the
 // division-free correctly rounded quotient of quantize.hpp, ~7 VALU operations per bf16
 // element in all; codes are written as 8-byte (bf16/f16 input) or 4-byte (f32) stores per lane and
-// the scale by the group's first lane.  A KV-cache append is this kernel pointed at the
-// cache rows pos .. pos + n_tok, so the codes go straight into the cache; k and v of an
+// the scale by the group's first lane.  Rows of at most 32 vectors (KV cache rows) take
+// quantGroup (one vector per lane, one-wavefront blocks), rows of 65..1152 vectors
+// quantWave (one wavefront per row), others quantRows.  A KV-cache append is this kernel
+// pointed at the cache rows pos .. pos + n_tok, so the codes go straight into the cache; k and v of an
 // append go through one launch (two jobs), which saves a launch's fixed cost of about
 // 2 us (fill, first-load latency, drain) on a 25 MB job.
 #include "common.hpp"
@@ -124,9 +126,12 @@ __global__ void __launch_bounds__(blockFor<G>())
 // barrier).  Same results as quantRows.  Measured on MI355X (W[8960, 1536] bf16, graph-
 // replayed medians over >= 1 GiB of rotating sets): 8.64 us against 9.0 us for quantRows
 // with the same lane plan; V = 4 ran faster than V = 3 (8.94 us) on these 192-vector rows,
-// so the launcher uses V = 4 for rows of 65..256 vectors.
-template <typename T, int V>
-__global__ void __launch_bounds__(256)
+// so the launcher uses V = 4 for rows of 65..256 vectors.  Rows of 257..1152 vectors take
+// V = 8 / 12 / 18 in one-wavefront blocks: W[1536, 8960] 8.74 us against 9.15 us for
+// quantRows (256 lanes per row) and 9.01 / 10.18 us for 2 / 4 rows per block (at
+// W[8960, 1536] one-wavefront blocks made no difference: 8.63 against 8.67 us).
+template <typename T, int V, int B>
+__global__ void __launch_bounds__(B)
     quantWave(QuantJobs jobs, int nvec) {
     using F = Fmt<T>;
     constexpr int N = F::kVec;
@@ -137,7 +142,7 @@ __global__ void __launch_bounds__(256)
     const size_t rows = second ? jobs.job[1].rows : jobs.job[0].rows;
     const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
     const int lane = int(threadIdx.x) % kWave;
-    const size_t row = size_t(blk) * (256 / kWave) + threadIdx.x / kWave;
+    const size_t row = size_t(blk) * (B / kWave) + threadIdx.x / kWave;
     const bool live = row < rows;
     const size_t base = (live ? row : 0) * size_t(nvec); // in vectors
     v4u raw[V];
@@ -187,6 +192,60 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// Rows of at most G <= 32 vectors (KV cache rows: head_dim 64 / 128 / 256 in 16-bit
+// types): G lanes per row, one vector per lane, blocks of one wavefront (64 / G rows).
+// Same results as quantRows.  Measured on MI355X (KV append pair [32768, 2, 128] bf16,
+// graph-replayed medians over >= 1 GiB of rotating sets): 10.27 us against 11.65 us for
+// quantRows (G = 16 in 256-thread blocks); the same kernel in blocks of 128 / 256 / 512
+// threads took 11.05 / 11.08 / 11.25 us, and 2 or 4 rows per lane group 11.09 / 11.34 us.
+template <typename T, int G>
+__global__ void __launch_bounds__(kWave)
+    quantGroup(QuantJobs jobs, int nvec) {
+    using F = Fmt<T>;
+    constexpr int N = F::kVec;
+    const bool second = blockIdx.x >= jobs.nb0; // block-uniform
+    int8_t *__restrict__ q = second ? jobs.job[1].q : jobs.job[0].q;
+    float *__restrict__ scale = second ? jobs.job[1].scale : jobs.job[0].scale;
+    const v4u *__restrict__ in = static_cast<const v4u *>(second ? jobs.job[1].in : jobs.job[0].in);
+    const size_t rows = second ? jobs.job[1].rows : jobs.job[0].rows;
+    const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
+    const int lane = int(threadIdx.x) % G;
+    const size_t row = size_t(blk) * (kWave / G) + threadIdx.x / G;
+    const bool live = row < rows;
+    const bool inrow = lane < nvec;
+    const size_t base = (live ? row : 0) * size_t(nvec); // in vectors
+    // unconditional load (a dead row or a lane past the row end reads a valid vector and
+    // folds as zero)
+    const v4u raw = __builtin_nontemporal_load(in + base + (inrow ? lane : 0));
+    const v4u val = inrow ? raw : v4u{0u, 0u, 0u, 0u};
+    using A = AbsBits<T>;
+    const uint32_t bits = waveGroupReduce<G, MaxU32Op>(A::finish(A::fold(0u, val)));
+    float amax = A::value(bits);
+    if (__builtin_expect(bits > A::kInf, 0)) { // a NaN in the row: the float rule
+        float x[N];
+        F::unpack(val, x);
+        amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(x[e]));
+        amax = waveGroupReduce<G, MaxOp>(amax);
+    }
+    const RowQuantizer qz(amax);
+    if (live && lane == 0) scale[row] = qz.scale;
+    const size_t cbase = base * N; // in codes
+    if (__builtin_expect(qz.exact_only, 0)) {
+        for (int j = lane; live && j < nvec * N; j += G)
+            q[cbase + j] = int8_t(codeOf(F::get(in, cbase + j), amax, qz.scale));
+        return;
+    }
+    if (live && inrow) {
+        float x[N];
+        uint32_t c[N];
+        F::unpack(raw, x);
+        qz.fastCodes<N, std::is_same_v<T, F32>>(x, c);
+        storeCodes<N>(q, cbase + size_t(lane) * N, c);
+    }
+}
+
 template <typename T>
 __global__ void __launch_bounds__(256)
     quantRowsScalar(int8_t *q, float *scale, const void *in, size_t rows, size_t cols) {
@@ -209,10 +268,37 @@ void launch(const QuantJob &j0, const QuantJob &j1, size_t cols, hipStream_t s) 
         return j.rows == 0 || (aligned16(j.in) && reinterpret_cast<uintptr_t>(j.q) % N == 0);
     };
     const bool vec = cols > 0 && cols % N == 0 && cols <= size_t(INT32_MAX) && vecOk(j0) && vecOk(j1);
+    if (vec && cols / N <= 32) {
+        const int nvec = int(cols / N);
+        const auto go = [&](auto g) {
+            constexpr int G = decltype(g)::value;
+            const unsigned nb0 = blocksFor(j0.rows, kWave / G), nb1 = blocksFor(j1.rows, kWave / G);
+            if (nb0 + nb1 == 0) return;
+            quantGroup<T, G><<<nb0 + nb1, kWave, 0, s>>>(QuantJobs{{j0, j1}, nb0}, nvec);
+        };
+        if (nvec <= 4) go(std::integral_constant<int, 4>{});
+        else if (nvec <= 8) go(std::integral_constant<int, 8>{});
+        else if (nvec <= 16) go(std::integral_constant<int, 16>{});
+        else go(std::integral_constant<int, 32>{});
+        return;
+    }
     if (vec && cols / N > 64 && cols / N <= 256) {
         const unsigned nb0 = blocksFor(j0.rows, 256 / kWave), nb1 = blocksFor(j1.rows, 256 / kWave);
         if (nb0 + nb1 == 0) return;
-        quantWave<T, 4><<<nb0 + nb1, 256, 0, s>>>(QuantJobs{{j0, j1}, nb0}, int(cols / N));
+        quantWave<T, 4, 256><<<nb0 + nb1, 256, 0, s>>>(QuantJobs{{j0, j1}, nb0}, int(cols / N));
+        return;
+    }
+    if (vec && cols / N > 256 && cols / N <= 18 * 64) {
+        const int nvec = int(cols / N);
+        const unsigned nb0 = unsigned(j0.rows), nb1 = unsigned(j1.rows); // rows < 2^30
+        if (nb0 + nb1 == 0) return;
+        const QuantJobs jobs{{j0, j1}, nb0};
+        if (nvec <= 8 * 64)
+            quantWave<T, 8, kWave><<<nb0 + nb1, kWave, 0, s>>>(jobs, nvec);
+        else if (nvec <= 12 * 64)
+            quantWave<T, 12, kWave><<<nb0 + nb1, kWave, 0, s>>>(jobs, nvec);
+        else
+            quantWave<T, 18, kWave><<<nb0 + nb1, kWave, 0, s>>>(jobs, nvec);
         return;
     }
     RowPlan plan = vec ? planRow(cols / N) : RowPlan{};
@@ -234,7 +320,7 @@ void launch(const QuantJob &j0, const QuantJob &j1, size_t cols, hipStream_t s) 
 template <typename T>
 void launchAny(const QuantJob &j0, const QuantJob &j1, size_t cols, hipStream_t s) {
     // a job too large for the block index space is split; real KV / weight shapes never are
-    constexpr size_t kMaxRows = size_t(1) << 30;
+    constexpr size_t kMaxRows = size_t(1) << 29; // both jobs' blocks fit a 31-bit grid
     if (j0.rows > kMaxRows || j1.rows > kMaxRows) {
         for (const QuantJob *j : {&j0, &j1})
             for (size_t r = 0; r < j->rows; r += kMaxRows) {

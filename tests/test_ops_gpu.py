@@ -356,7 +356,13 @@ def with_outliers(rng, shape, dt, scale):
 @pytest.mark.parametrize("shape", [(8960, 1536), (1536, 8960), (4096, 128), (5, 1001), (3, 20000), (7, 8),
                                    # one wave per row with a partial last lane group (125 / 129
                                    # bf16 vectors, 250 f32), and exactly 256 bf16 vectors
-                                   (33, 1000), (17, 1032), (9, 2048)])
+                                   (33, 1000), (17, 1032), (9, 2048),
+                                   # one-wavefront blocks of 4 / 8 / 16 / 32-lane groups with
+                                   # partial groups (bf16: 4, 25, 9, 1 vectors; f32: 8, 50, 18, 2)
+                                   (301, 32), (65, 200), (130, 72), (3, 8),
+                                   # one wave per row in one-wavefront blocks, 8 / 12 / 18
+                                   # vectors per lane (bf16: 512, 750, 1025 vectors)
+                                   (5, 4096), (3, 6000), (4, 8200)])
 def test_quantize_dequantize(dt, shape):
     rng = np.random.default_rng(shape[0])
     x = with_outliers(rng, shape, dt, 0.02)
@@ -774,7 +780,8 @@ def quant_edge_rows(dt, cols=256, seed=5):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-@pytest.mark.parametrize("cols", [256, 1536, 1000])  # lane-group plan; one wave per row (full / partial)
+# one-wavefront lane groups (128, 200), lane-group plan, one wave per row (full / partial)
+@pytest.mark.parametrize("cols", [128, 200, 256, 1536, 1000, 8960])
 def test_quantize_boundary_rows(dt, cols):
     x = quant_edge_rows(dt, cols=cols)
     q, s = empty(x.shape, L.DataType.I8), empty(x.shape[:-1], L.DataType.F32)
