@@ -286,36 +286,52 @@ __global__ void __launch_bounds__(kWave * kWaves)
 
 // Merge of the chunk partials of a split launch: one 1024-thread block per (query, head,
 // slab of 32 output columns); thread t takes column t % 32 of the slab for the chunks c =
-// t / 32 (mod 32), so a thread reads at most nchunks / 32 partial values (one round of
-// independent loads for up to 256 chunks) and the (query, head) pairs of a decode launch
-// spread over D / 32 times as many blocks.  Every block of a pair forms the same maximum and
-// sum from the chunks' (m, l).
+// t / 32 (mod 32), so a thread reads at most nchunks / 32 partial values and the (query,
+// head) pairs of a decode launch spread over D / 32 times as many blocks.  Every block of a
+// pair forms the same maximum and sum from the chunks' (m, l).  Up to 256 chunks (kPer = 8
+// per thread) the partial values are requested together with the (m, l) loads, so the
+// merge waits for one round of loads rather than two; the sum runs in the same order
+// either way.
 constexpr int kCombineThreads = 1024;
 constexpr int kCombineCols = 32; // output columns per block (head_dim is 64 or 128)
 
-template <typename T>
+template <typename T, int kPer>
 __global__ void __launch_bounds__(kCombineThreads)
     attnCombine(void *out, const float *part, int nchunks, int D) {
     __shared__ float w[1024];  // per-chunk factor exp(m_c - M), nchunks <= 1024
     __shared__ float red[kCombineThreads];
     __shared__ float wred[kCombineThreads / kWave];
+    constexpr int kGroups = kCombineThreads / kCombineCols;
     const int slabs = D / kCombineCols;
     const size_t ih = blockIdx.x / unsigned(slabs); // i * nh + h
     const int col0 = int(blockIdx.x % unsigned(slabs)) * kCombineCols;
     const float *pp = part + ih * size_t(nchunks) * (D + 2);
     const int t = threadIdx.x;
+    const int e = col0 + t % kCombineCols, grp = t / kCombineCols;
     const float mc = t < nchunks ? pp[size_t(t) * (D + 2) + D] : -INFINITY;
     const float lc = t < nchunks ? pp[size_t(t) * (D + 2) + D + 1] : 0.0f;
+    float v[kPer > 0 ? kPer : 1];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) { // unconditional (clamped) loads, used only for k < nchunks
+        const int k = grp + j * kGroups;
+        v[j] = pp[size_t(k < nchunks ? k : 0) * (D + 2) + e];
+    }
     const float M = groupReduce<kCombineThreads, MaxOp>(mc, wred); // every thread gets it
     const float f = mc == M ? 1.0f : __expf(mc - M);                // mc = -inf: l = o = 0
     if (t < nchunks) w[t] = f;
     const float L = groupReduce<kCombineThreads, SumOp>(t < nchunks ? lc * f : 0.0f, wred);
     __syncthreads();
-    constexpr int kGroups = kCombineThreads / kCombineCols;
-    const int e = col0 + t % kCombineCols, grp = t / kCombineCols;
     float acc = 0.0f;
+    if constexpr (kPer > 0) {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int k = grp + j * kGroups;
+            if (k < nchunks) acc += v[j] * w[k];
+        }
+    } else {
 #pragma unroll 8
-    for (int k = grp; k < nchunks; k += kGroups) acc += pp[size_t(k) * (D + 2) + e] * w[k];
+        for (int k = grp; k < nchunks; k += kGroups) acc += pp[size_t(k) * (D + 2) + e] * w[k];
+    }
     red[t] = acc;
     __syncthreads();
     if (t < kCombineCols) {
@@ -323,6 +339,15 @@ __global__ void __launch_bounds__(kCombineThreads)
         for (int g = 0; g < kGroups; ++g) O += red[g * kCombineCols + t];
         Fmt<T>::put(out, ih * D + col0 + t, L > 0.0f ? O / L : 0.0f);
     }
+}
+
+template <typename T>
+void launchCombine(void *out, const float *part, int nchunks, int D, size_t pairs, hipStream_t s) {
+    const unsigned blocks = unsigned(pairs) * unsigned(D / kCombineCols);
+    if (nchunks <= 8 * (kCombineThreads / kCombineCols))
+        attnCombine<T, 8><<<blocks, kCombineThreads, 0, s>>>(out, part, nchunks, D);
+    else
+        attnCombine<T, 0><<<blocks, kCombineThreads, 0, s>>>(out, part, nchunks, D);
 }
 
 // Any head_dim / v_head_dim / group: one wave per (query, head), keys one at a time with an
@@ -982,7 +1007,7 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
             const unsigned blocks = unsigned(a.seq * size_t(a.nkvh) * nchunks);
             attnDecodeMfma<kInt8><<<blocks, kWave * kDecWaves, 0, s>>>(a);
             if (nchunks > 1)
-                attnCombine<T><<<unsigned(pairs) * unsigned(d / kCombineCols), kCombineThreads, 0, s>>>(a.out, a.part, a.nchunks, d);
+                launchCombine<T>(a.out, a.part, a.nchunks, d, pairs, s);
             return;
         }
     }
@@ -1008,7 +1033,7 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
     else
         launchD<T, kInt8, 128>(a, G, blocks, s);
     if (nchunks > 1)
-        attnCombine<T><<<unsigned(a.seq * size_t(a.nh)) * unsigned(d / kCombineCols), kCombineThreads, 0, s>>>(a.out, a.part, a.nchunks, d);
+        launchCombine<T>(a.out, a.part, a.nchunks, d, a.seq * size_t(a.nh), s);
 }
 
 template <bool kInt8>
