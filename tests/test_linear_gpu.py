@@ -54,8 +54,8 @@ SHAPES = [
     (256, 1536, 1536), (129, 264, 200), (17, 40, 130), (3, 77, 9), (64, 1536, 1), (1, 8, 1),
     # few rows over few output tiles: K split across blocks (ragged last split, 16 rows)
     (16, 4096, 300), (2, 2056, 40),
-    # one row with partly used chunk slots: two rows per wave (INT8) / one (16-bit) over 1024
-    # inputs, odd channel counts; a 4-wave split row of 3000 / 16384 inputs
+    # one row with partly used chunk slots (1024 / 3000 inputs, odd channel counts) and a
+    # row longer than 24 chunks per lane (16384 inputs, 16-bit weights: the streaming GEMV)
     (1, 1024, 33), (1, 3000, 77), (1, 16384, 3),
 ]
 
@@ -105,6 +105,19 @@ def test_linear_w8a16_matches_oracle(shape, dt, bias):
     b = sample(rng, (out_f,), dt) if bias else None
     assert_linear_close(linear_w8a16(x, codes, scale, b, dt), oracle.linear_w8a16(x, codes, scale, b),
                         x, codes, f"w8a16 {dt} {shape}", w_scale=scale)
+
+
+@pytest.mark.parametrize("in_f, out_f", [(1536, 65541), (2048, 65600), (1024, 4100)])
+def test_w8a16_one_row_over_many_channels(in_f, out_f):
+    # INT8 rows of at most 2 chunks per lane over 65536+ channels take 4 channels per wave (the
+    # lm_head form), with channels past the end clamped; 4100 channels read x from L1 / L2 in
+    # one-channel waves.  Same per-channel sum either way, checked against the oracle.
+    rng = np.random.default_rng(zlib.crc32(repr(("w8 rows", in_f, out_f)).encode()))
+    x = sample(rng, (1, in_f), "bf16")
+    codes, scale = int8_weights(rng, out_f, in_f)
+    b = sample(rng, (out_f,), "bf16")
+    assert_linear_close(linear_w8a16(x, codes, scale, b, "bf16"), oracle.linear_w8a16(x, codes, scale, b),
+                        x, codes, f"w8a16 1 x {in_f} -> {out_f}", w_scale=scale)
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
