@@ -434,36 +434,6 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// Dot product of one 16-byte weight chunk (8 bf16 / f16 weights or 16 INT8 codes) with the
-// matching x elements in LDS, in f32.
-template <typename T, bool kInt8>
-__device__ __forceinline__ float gemvChunk(const v4u &w, const uint16_t *xp) {
-    float s = 0.0f;
-    if constexpr (kInt8) {
-        const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-        float xf[16];
-        Fmt<T>::unpack(*reinterpret_cast<const v4u *>(xp), xf);
-        Fmt<T>::unpack(*reinterpret_cast<const v4u *>(xp + 8), xf + 8);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s = __builtin_fmaf(xf[e], float(int8_t(ww[e / 4] >> (8 * (e % 4)))), s);
-    } else {
-        float xf[8], wf[8];
-        Fmt<T>::unpack(*reinterpret_cast<const v4u *>(xp), xf);
-        Fmt<T>::unpack(w, wf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s = __builtin_fmaf(xf[e], wf[e], s);
-    }
-    return s;
-}
-
-// out[n] of one row: the per-channel scale (INT8), the bias, the reference rounding.
-template <typename T, bool kInt8>
-__device__ __forceinline__ void gemvStore(const LinearArgs &a, int n, float t) {
-    if constexpr (kInt8) t = a.scale[n] * t;
-    if (a.bias) t = t + Fmt<T>::get(a.bias, n);
-    Fmt<T>::put(a.out, n, t);
-}
-
 // One row (decode): linearGemv's sum -- per output channel one wave, lane chunks lane,
 // lane + 64, ... in one FMA chain, then the same butterfly -- with every weight chunk of the
 // wave's C channels requested before anything else (C x J per lane) and x staged once per
