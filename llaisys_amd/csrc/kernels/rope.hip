@@ -6,9 +6,10 @@
 // rounded double -> float -> element type.  freq_j is computed on the host with the same
 // libm pow the reference calls, so the angles are bit-identical; cos/sin come from
 // sincos.hpp (within an ulp of glibc's, which the final float rounding absorbs).  The
-// wave kernel forms x*c +- p*s as one f64 product and one f64 fma (the reference rounds
-// both products); the double results differ by at most an ulp, which the rounding to
-// float absorbs except within 2^-29 of a float tie.
+// wave kernel of several instructions per token forms x*c +- p*s as one f64 product and
+// one f64 fma (the reference rounds both products); the double results differ by at most
+// an ulp, which the rounding to float absorbs except within 2^-29 of a float tie.  The
+// one-instruction wave kernel (kExact) and ropeVec round both products as the reference.
 //
 // Design: HBM-bound, no MFMA (no contraction).  Two kernels:
 //  * ropeWave (most shapes): 2^split_log2 wavefronts per token (each a contiguous share
@@ -16,7 +17,7 @@
 //    loads of its rows, computes the token's d/2 (cos, sin) pairs (one per lane) into its
 //    own LDS slice while they are in flight, and each lane then keeps the pairs of its
 //    column in registers for every head row it rotates.
-//  * ropeVec (few rows per token, e.g. k alone): a 256-thread block owns a run of tokens,
+//  * ropeVec (at most 1/8 of a wave's lanes per token, e.g. one 64-wide head): a 256-thread block owns a run of tokens,
 //    computes their pairs into LDS behind a block barrier and rotates items that read
 //    their pairs from LDS; it packs several tokens into a block, so lanes stay busy.
 // The trig is the ~40-instruction routine of sincos.hpp, the device library only on an
@@ -152,7 +153,7 @@ __global__ void __launch_bounds__(256)
 // out as straight-line code).  Waves past the last token
 // redo the last token and store nothing, so no wave leaves before the loads (a branch
 // there would serialise the kernel-argument loads ahead of the first global load).
-template <typename T, int IPT, int VPH, bool kOnePass>
+template <typename T, int IPT, int VPH, bool kOnePass, bool kExact>
 __global__ void __launch_bounds__(256)
     ropeWave(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int passes, int split_log2,
              FreqTable ft) {
@@ -247,8 +248,13 @@ __global__ void __launch_bounds__(256)
                 float x[N], q[N], y[N];
                 F::unpack(raw[k], x);
                 F::unpack(other, q);
+                if constexpr (kExact) { // the reference's two rounded products and their sum
 #pragma unroll
-                for (int e = 0; e < N; ++e) y[e] = float(fma(double(q[e]), sn[e], double(x[e]) * c[e]));
+                    for (int e = 0; e < N; ++e) y[e] = float(double(x[e]) * c[e] + double(q[e]) * sn[e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < N; ++e) y[e] = float(fma(double(q[e]), sn[e], double(x[e]) * c[e]));
+                }
                 __builtin_nontemporal_store(F::packQ(y), reinterpret_cast<v4u *>((r < nh0 ? out0 : out1) + size_t(r) * kRowBytes));
             }
         }
@@ -278,29 +284,27 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+template <typename T, int IPT, bool kOnePass, bool kExact>
+void launchWaveVph(int vph, int passes, int split_log2, const RopePair &tp, const int64_t *pos,
+                   size_t seq, const FreqTable &ft, hipStream_t s) {
+    const unsigned grid = blocksFor(seq << split_log2, 256 / kWave);
+    switch (vph) {
+    case 2: ropeWave<T, IPT, 2, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 4: ropeWave<T, IPT, 4, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 8: ropeWave<T, IPT, 8, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 16: ropeWave<T, IPT, 16, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 32: ropeWave<T, IPT, 32, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    default: break;
+    }
+}
+
 template <typename T, int IPT>
 void launchWaveIpt(int vph, int passes, int split_log2, const RopePair &tp, const int64_t *pos,
                    size_t seq, const FreqTable &ft, hipStream_t s) {
-    const unsigned grid = blocksFor(seq << split_log2, 256 / kWave);
-    if (passes == 1) {
-        switch (vph) {
-        case 2: ropeWave<T, IPT, 2, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-        case 4: ropeWave<T, IPT, 4, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-        case 8: ropeWave<T, IPT, 8, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-        case 16: ropeWave<T, IPT, 16, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-        case 32: ropeWave<T, IPT, 32, true><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-        default: break;
-        }
-        return;
-    }
-    switch (vph) {
-    case 2: ropeWave<T, IPT, 2, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 4: ropeWave<T, IPT, 4, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 8: ropeWave<T, IPT, 8, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 16: ropeWave<T, IPT, 16, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 32: ropeWave<T, IPT, 32, false><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    default: break;
-    }
+    if (passes == 1)
+        launchWaveVph<T, IPT, true, false>(vph, passes, split_log2, tp, pos, seq, ft, s);
+    else
+        launchWaveVph<T, IPT, false, false>(vph, passes, split_log2, tp, pos, seq, ft, s);
 }
 
 // `instr` wave instructions per token, taken in passes of at most 4 (registers).
@@ -362,12 +366,21 @@ bool launchVec(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, con
     };
     const uint32_t magic0 = magicOf(tp.n_heads0), magic1 = magicOf(tp.n_heads1);
     // One wave per token when its instructions keep >= 3/4 of the lanes busy (q+k of Qwen2:
-    // 14 of 16 rows, q alone and Llama-8B q+k: all); a launch of few rows per token (k
-    // alone) packs several tokens per block with ropeVec instead.
+    // 14 of 16 rows, q alone and Llama-8B q+k: all).  One token of one instruction with at
+    // least 1/4 of the lanes busy (k alone) also takes one wave, with the reference's two
+    // rounded products (the exact form of ropeVec); measured on MI355X, bf16, 8192 tokens:
+    // k [2 heads, 128] 6.02 -> 4.56 us, [1, 128] 4.68 -> 4.39 us, [2, 64] 5.20 -> 4.89 us,
+    // [4, 64] 4.96 -> 4.91 us; at 1/8 ([1, 64]) ropeVec's packed tokens win, 3.96 against
+    // 5.06 us.  Fewer rows per token pack several tokens per block with ropeVec.
     const int rpi = int(kWave / (2 * vph));
-    const int instr = int((size_t(tp.n_heads0 + tp.n_heads1) + rpi - 1) / rpi);
-    if (size_t(tp.n_heads0 + tp.n_heads1) * 4 >= size_t(instr) * rpi * 3) {
+    const size_t rows = size_t(tp.n_heads0 + tp.n_heads1);
+    const int instr = int((rows + rpi - 1) / rpi);
+    if (rows * 4 >= size_t(instr) * rpi * 3) {
         launchWave<T>(int(vph), instr, tp, pos, seq, ft, s);
+        return true;
+    }
+    if (instr == 1 && rows * 4 >= size_t(rpi)) {
+        launchWaveVph<T, 1, true, true>(int(vph), 1, 0, tp, pos, seq, ft, s);
         return true;
     }
     switch (ipt) {

@@ -181,6 +181,11 @@ ROPE = [
     ((64, 32, 128), 16320, 5e5),    # config 2 heads, late positions
     ((7, 3, 6), 3, 1e4),            # odd half-dim
     ((5, 4, 64), 100000, 1e6),
+    # one wave per token over one instruction, 1/4 of the lanes busy (one 128-wide head, two
+    # 64-wide heads), and 1/8 (one 64-wide head: tokens packed per block)
+    ((33, 1, 128), 70, 1e4),
+    ((40, 2, 64), 0, 1e6),
+    ((41, 1, 64), 5, 1e4),
 ]
 
 
