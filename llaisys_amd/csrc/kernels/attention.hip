@@ -18,7 +18,8 @@
 //  - attnMfma (bf16, head_dim 128, >= 16 queries: prefill): MFMA-bound; 16 queries x one kv
 //    head's q heads per block, S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16
 //    with K / V tiles staged through LDS one tile ahead; with few blocks per CU, two wave
-//    sets per block split the key tiles (kSplit).
+//    sets per block split the key tiles (kSplit).  An INT8 cache whose bf16 form fits the
+//    workspace is dequantized once into it and attended as bf16 (the same operands).
 //  - attnDecodeMfma (bf16 q, head_dim 128, fewer queries: decode, cache in bf16 or INT8):
 //    HBM-bound; the key range is cut into chunks, one block per (query, kv head, chunk) with
 //    the kv head's q heads as the MFMA columns; attnCombine merges the chunk partials.
@@ -972,6 +973,24 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
         if (d == 128 && a.total > 0 && a.seq >= size_t(kMfmaQ) && mblocks < (size_t(1) << 31) &&
             a.scale > 0.0f && std::isfinite(a.scale)) {
             a.nchunks = 1;
+            if constexpr (kInt8) {
+                // An INT8 cache whose bf16 form fits the workspace is dequantized once (both
+                // caches in one launch, bf16(code * scale) as the tiles would be staged) and
+                // attended as bf16: the tile staging of every query block no longer converts
+                // the same codes again.  Same operands, so the same bits.
+                const size_t cache_el = a.total * size_t(a.nkvh) * size_t(d);
+                if (2 * cache_el * sizeof(uint16_t) <= ws_bytes) {
+                    uint16_t *kd = static_cast<uint16_t *>(ws), *vd = kd + cache_el;
+                    dequantizeInt8Pair(kd, static_cast<const int8_t *>(a.k), a.ks, a.total * size_t(a.nkvh), vd,
+                                       static_cast<const int8_t *>(a.v), a.vs, a.total * size_t(a.nkvh),
+                                       size_t(d), LLAISYS_DTYPE_BF16, s);
+                    AttnArgs b = a;
+                    b.k = kd;
+                    b.v = vd;
+                    b.ks = b.vs = nullptr;
+                    return launch<T, false>(b, d, dv, nullptr, 0, s);
+                }
+            }
             // few blocks per CU: the causal imbalance is not averaged out across blocks, so
             // the key tiles of each block are split over two wave sets
             // (groups of 8 keep one wave per head: 16 waves of 8 heads would spill registers)

@@ -10,7 +10,7 @@ import pytest
 import llaisys_amd as L
 import oracle
 from llaisys_amd.hostfmt import f32_to_bf16
-from numerics import assert_attention_close
+from numerics import assert_attention_close, assert_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -116,8 +116,10 @@ def test_self_attention_empty_cache_gives_zeros():
                          ids=lambda s: "x".join(map(str, s)))
 def test_self_attention_int8kv(dt, shape):
     """INT8 cache (1% outliers x20, as config 3) against dequantize-then-attend on the GPU
-    (the same values in another key tiling, so within the attention tolerance rather than bit
-    for bit) and against the oracle's composition."""
+    and against the oracle's composition.  A bf16 prefill (16+ queries, head_dim 128) over a
+    cache whose bf16 form fits the workspace dequantizes the cache and runs the bf16 kernel,
+    so it equals the composition bit for bit; the other forms convert codes in their own key
+    tiling, within the attention tolerance."""
     seq, total, nh, nkvh, d = shape
     rng = np.random.default_rng(zlib.crc32(repr(("int8", dt, shape)).encode()))
     x = rng.standard_normal((2, total, nkvh, d), dtype=np.float32)
@@ -138,6 +140,8 @@ def test_self_attention_int8kv(dt, shape):
     L.Ops.self_attention(ref, tq, kd, vd, scale)
     vdq = oracle.dequantize_int8(vq, vs, NP[dt])
     assert_attention_close(out.numpy(), ref.numpy(), vdq, "int8 vs dequantize + attend")
+    if dt == "bf16" and seq >= 16 and d == 128:
+        assert_exact(out.numpy(), ref.numpy(), "int8 prefill vs dequantize + attend")
     exp = oracle.self_attention_int8kv(q, kq, ks, vq, vs, scale)
     assert_attention_close(out.numpy(), exp, vdq, f"int8 {dt} {shape}")
 
