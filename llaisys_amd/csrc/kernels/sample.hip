@@ -90,55 +90,78 @@ struct SmpArgs {
     uint32_t *ties;  // rows x kTieCap indices with the threshold key
 };
 
-// Largest bin b of h[0..n) whose suffix count reaches `need`; returns b and, in *inside,
-// need minus the count above b.  All kSmpBlock threads of the block call it; the histogram
-// is first staged in `lh` (LDS, n words); `sc` is LDS scratch of kSmpBlock + 1 words.
-__device__ int chooseBin(const uint32_t *h, int n, uint32_t need, uint32_t *inside, uint32_t *lh,
-                         uint32_t *sc) {
-    const int t = int(threadIdx.x);
-    for (int b = t; b < n; b += kSmpBlock) lh[b] = h[b];
-    __syncthreads();
-    const int per = n / kSmpBlock; // thread t owns bins [t*per, (t+1)*per)
+// Inclusive suffix sum within the wavefront (lane l: the sum over lanes l .. 63).
+__device__ __forceinline__ uint32_t waveSuffix(uint32_t v) {
+    const int lane = int(threadIdx.x) % kWave;
+#pragma unroll
+    for (int d = 1; d < kWave; d *= 2) {
+        const uint32_t o = __shfl_down(v, d, kWave);
+        if (lane + d < kWave) v += o;
+    }
+    return v;
+}
+
+// LDS scratch of one radix decision: the wave totals and the (bin, inside) result.
+struct BinScratch {
+    uint32_t wtot[kSmpBlock / kWave];
+    uint32_t bin, in;
+};
+
+// Largest bin b of lh[0..n) (a histogram already in LDS) whose suffix count reaches `need`;
+// returns b and, in *inside, need minus the count above b.  All kSmpBlock threads call it.
+// Thread t owns bins [t*per, (t+1)*per); the suffix sums over the threads come from wave
+// shuffles and one exchange of the wave totals (two block barriers in all).
+__device__ int chooseBin(const uint32_t *lh, int n, uint32_t need, uint32_t *inside, BinScratch &bs) {
+    const int t = int(threadIdx.x), w = t / kWave;
+    const int per = n / kSmpBlock;
     uint32_t s = 0;
     for (int j = 0; j < per; ++j) s += lh[t * per + j];
-    sc[t] = s;
+    const uint32_t v = waveSuffix(s);
+    if (t % kWave == 0) bs.wtot[w] = v;
     __syncthreads();
-    // suffix sums over the threads' totals
-    for (int d = 1; d < kSmpBlock; d *= 2) {
-        const uint32_t v = t + d < kSmpBlock ? sc[t + d] : 0u;
-        __syncthreads();
-        sc[t] += v;
-        __syncthreads();
-    }
-    // sc[t] = count in bins >= t*per; the thread whose range holds the crossing resolves it
-    __shared__ int bin;
-    __shared__ uint32_t in;
-    const uint32_t above = t + 1 < kSmpBlock ? sc[t + 1] : 0u;
-    if (above < need && sc[t] >= need) {
+    uint32_t suf = v; // count in bins >= t*per
+    for (int x = w + 1; x < kSmpBlock / kWave; ++x) suf += bs.wtot[x];
+    const uint32_t above = suf - s; // count in bins >= (t+1)*per
+    // the thread whose range holds the crossing resolves it
+    if (above < need && suf >= need) {
         uint32_t acc = above;
         for (int j = per - 1; j >= 0; --j) {
             const uint32_t c = lh[t * per + j];
             if (acc + c >= need) {
-                bin = t * per + j;
-                in = need - acc;
+                bs.bin = uint32_t(t * per + j);
+                bs.in = need - acc;
                 break;
             }
             acc += c;
         }
     }
     __syncthreads();
-    *inside = in;
-    return bin;
+    *inside = bs.in;
+    return int(bs.bin);
 }
 
+// LDS for decide(): the row's three histograms and one BinScratch per level
+struct DecideLds {
+    uint32_t h[2048 + 2048 + 1024];
+    BinScratch bs[3];
+};
+
 // the digits chosen after `level` histograms: prefix (the key's top bits) and the count
-// still needed among keys with that prefix
+// still needed among keys with that prefix.  The histograms are final when this runs, so
+// all the levels' are staged in one round of loads.
 __device__ void decide(const SmpRow &st, int level, uint32_t k, uint32_t *prefix, uint32_t *need,
-                       uint32_t *lh, uint32_t *sc) {
+                       DecideLds &L) {
+    const int t = int(threadIdx.x);
+    for (int b = t; b < 2048; b += kSmpBlock) L.h[b] = st.h1[b];
+    if (level >= 2)
+        for (int b = t; b < 2048; b += kSmpBlock) L.h[2048 + b] = st.h2[b];
+    if (level >= 3)
+        for (int b = t; b < 1024; b += kSmpBlock) L.h[4096 + b] = st.h3[b];
+    __syncthreads();
     uint32_t nd = k, p = 0;
-    if (level >= 1) p = uint32_t(chooseBin(st.h1, 2048, nd, &nd, lh, sc));
-    if (level >= 2) p = (p << 11) | uint32_t(chooseBin(st.h2, 2048, nd, &nd, lh, sc));
-    if (level >= 3) p = (p << 10) | uint32_t(chooseBin(st.h3, 1024, nd, &nd, lh, sc));
+    if (level >= 1) p = uint32_t(chooseBin(L.h, 2048, nd, &nd, L.bs[0]));
+    if (level >= 2) p = (p << 11) | uint32_t(chooseBin(L.h + 2048, 2048, nd, &nd, L.bs[1]));
+    if (level >= 3) p = (p << 10) | uint32_t(chooseBin(L.h + 4096, 1024, nd, &nd, L.bs[2]));
     *prefix = p;
     *need = nd;
 }
@@ -153,15 +176,10 @@ template <typename T, int LEVEL>
 __global__ void __launch_bounds__(kSmpBlock)
     sampleHist(SmpArgs a) {
     __shared__ uint32_t hist[2048];
-    __shared__ uint32_t sc[kSmpBlock + 1];
     const int row = int(blockIdx.y);
     SmpRow &st = a.st[row];
-    uint32_t prefix = 0, need = 0;
-    if constexpr (LEVEL > 1) decide(st, LEVEL - 1, uint32_t(a.k), &prefix, &need, hist, sc);
-    constexpr int kBins = LEVEL == 3 ? 1024 : 2048;
-    __syncthreads(); // hist held the staged histograms
-    for (int b = int(threadIdx.x); b < kBins; b += kSmpBlock) hist[b] = 0;
-    __syncthreads();
+    // the block's keys first: their loads and the histogram staging of decide() share one
+    // round trip
     const int base = int(blockIdx.x) * kSmpChunk;
     constexpr int kPer = kSmpChunk / kSmpBlock;
     uint32_t keys[kPer];
@@ -170,6 +188,14 @@ __global__ void __launch_bounds__(kSmpBlock)
         const int i = base + j * kSmpBlock + int(threadIdx.x);
         keys[j] = keyAt<T>(a, row, i < a.V ? i : a.V - 1);
     }
+    uint32_t prefix = 0, need = 0;
+    if constexpr (LEVEL > 1) {
+        __shared__ DecideLds dl;
+        decide(st, LEVEL - 1, uint32_t(a.k), &prefix, &need, dl);
+    }
+    constexpr int kBins = LEVEL == 3 ? 1024 : 2048;
+    for (int b = int(threadIdx.x); b < kBins; b += kSmpBlock) hist[b] = 0;
+    __syncthreads();
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int i = base + j * kSmpBlock + int(threadIdx.x);
@@ -193,12 +219,19 @@ __global__ void __launch_bounds__(kSmpBlock)
 template <typename T>
 __global__ void __launch_bounds__(kSmpBlock)
     sampleGather(SmpArgs a) {
-    __shared__ uint32_t sc[kSmpBlock + 1];
-    __shared__ uint32_t lh[2048];
+    __shared__ DecideLds dl;
     const int row = int(blockIdx.y);
     SmpRow &st = a.st[row];
+    const int base = int(blockIdx.x) * kSmpChunk;
+    constexpr int kPer = kSmpChunk / kSmpBlock;
+    uint32_t keys[kPer]; // loaded before the decision (one round trip with its staging)
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = base + j * kSmpBlock + int(threadIdx.x);
+        keys[j] = keyAt<T>(a, row, i < a.V ? i : a.V - 1);
+    }
     uint32_t theta = 0, need = 0;
-    decide(st, 3, uint32_t(a.k), &theta, &need, lh, sc);
+    decide(st, 3, uint32_t(a.k), &theta, &need, dl);
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         st.theta = theta;
         st.need = need;
@@ -208,8 +241,6 @@ __global__ void __launch_bounds__(kSmpBlock)
     __shared__ uint32_t nG, nT, baseG, baseT;
     if (threadIdx.x == 0) nG = nT = 0;
     __syncthreads();
-    const int base = int(blockIdx.x) * kSmpChunk;
-    constexpr int kPer = kSmpChunk / kSmpBlock;
     uint32_t slot[kPer]; // bit 31: tie; else candidate; position within the block's list
     int cls[kPer];       // 0 none, 1 above theta, 2 tie
 #pragma unroll
@@ -217,7 +248,7 @@ __global__ void __launch_bounds__(kSmpBlock)
         const int i = base + j * kSmpBlock + int(threadIdx.x);
         cls[j] = 0;
         if (i < a.V) {
-            const uint32_t key = keyAt<T>(a, row, i);
+            const uint32_t key = keys[j];
             if (key > theta) {
                 cls[j] = 1;
                 slot[j] = atomicAdd(&nG, 1u);
@@ -265,22 +296,27 @@ __device__ void bitonic(uint64_t *v, int n) {
 
 constexpr int kFinThreads = 256;
 
-// exclusive prefix sums of v (one value per thread, kFinThreads threads) in `buf`; returns
-// this thread's exclusive sum and, in *total, the block total
+// exclusive prefix sums of v (one value per thread, kFinThreads threads): inclusive scans
+// within each wavefront by shuffles, the wave totals through `buf` (kFinThreads / 64 words);
+// returns this thread's exclusive sum and, in *total, the block total
 __device__ uint64_t blockExclusive(uint64_t v, uint64_t *buf, uint64_t *total) {
-    const int t = int(threadIdx.x);
-    buf[t] = v;
-    __syncthreads();
-    for (int d = 1; d < kFinThreads; d *= 2) {
-        const uint64_t add = t >= d ? buf[t - d] : 0ull;
-        __syncthreads();
-        buf[t] += add;
-        __syncthreads();
+    const int t = int(threadIdx.x), lane = t % kWave, w = t / kWave;
+    uint64_t inc = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d *= 2) {
+        const uint64_t o = __shfl_up(inc, d, kWave);
+        if (lane >= d) inc += o;
     }
-    const uint64_t inc = buf[t];
-    *total = buf[kFinThreads - 1];
+    if (lane == kWave - 1) buf[w] = inc;
     __syncthreads();
-    return inc - v;
+    uint64_t before = 0, all = 0;
+    for (int x = 0; x < kFinThreads / kWave; ++x) {
+        if (x < w) before += buf[x];
+        all += buf[x];
+    }
+    *total = all;
+    __syncthreads(); // buf is free for the next call
+    return before + inc - v;
 }
 
 template <typename T>
