@@ -33,6 +33,7 @@ CASES = [
     (1, 151936, 3.0, 1.0, 1024, 0.95),
     (1, 151936, 3.0, 0.7, 40, 1.0),     # top-k only
     (4, 32000, 1.0, 1.3, 200, 0.9),
+    (2, 20000, 1.0, 1.0, 300, 0.9),     # k > 256: the 512-thread finish, a 512-item sort
     (20, 5000, 2.0, 0.9, 64, 0.7),      # more than 16 rows: two launches
     (3, 100, 1.0, 1.0, 500, 0.9),       # k > V
     (2, 4097, 5.0, 0.5, 2, 0.0),        # top_p <= 0: the top token
