@@ -16,8 +16,10 @@
 //                      match the digits chosen so far; the choice of every earlier digit is
 //                      recomputed by each block from the previous histograms (integer
 //                      atomics: exact and order-free).  HBM / L2-bound, one read of the row.
-//   sampleGather     : the keys above the k-th largest (< k of them) and the ties at it.
-//   sampleFinish     : one 256-thread block per row: the k candidates (ties by index) sorted by
+//   sampleGather     : the keys above the k-th largest (< k of them, stored as sort items
+//                      (~key << 32) | index) and the ties at it (indices).
+//   sampleFinish     : one 256-thread block per row (512 when k > 256): the k candidates
+//                      (ties by index) sorted by
 //                      (key desc, index asc) in LDS, weights, prefix sums, the top-p cut,
 //                      the draw; then re-zeroes the row's histograms and counters.
 #include "common.hpp"
@@ -86,7 +88,7 @@ struct SmpArgs {
     float inv, topP;
     uint64_t seed;
     SmpRow *st;      // rows entries, reserved scratch
-    uint32_t *gt;    // rows x kMaxK candidate indices (key above the threshold)
+    uint64_t *gt;    // rows x kMaxK candidates above the threshold: (~key << 32) | index
     uint32_t *ties;  // rows x kTieCap indices with the threshold key
 };
 
@@ -269,7 +271,7 @@ __global__ void __launch_bounds__(kSmpBlock)
         const uint32_t i = uint32_t(base + j * kSmpBlock + int(threadIdx.x));
         if (cls[j] == 1) {
             const uint32_t pos = baseG + slot[j];
-            if (pos < uint32_t(kMaxK)) a.gt[size_t(row) * kMaxK + pos] = i;
+            if (pos < uint32_t(kMaxK)) a.gt[size_t(row) * kMaxK + pos] = (uint64_t(~keys[j]) << 32) | i;
         } else if (cls[j] == 2) {
             const uint32_t pos = baseT + slot[j];
             if (pos < uint32_t(kTieCap)) a.ties[size_t(row) * kTieCap + pos] = i;
@@ -362,23 +364,17 @@ __global__ void __launch_bounds__(NT)
     // 2. the k candidates sorted by (key desc, index asc): ascending on (~key, index)
     int nk = 2;
     while (nk < k) nk *= 2;
-    // loads unconditional (clamped), the padding selected after them: loads under per-lane
-    // branches were issued one round trip at a time
-    uint32_t idx4[4];
+    // the gather stored the candidates as sort items; the ties carry the threshold key.
+    // Loads unconditional (clamped), the padding selected after them: loads under per-lane
+    // branches were issued one round trip at a time.
+    uint64_t x4[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int j = min(4 * t + e, k - 1);
-        const uint32_t g = a.gt[size_t(row) * kMaxK + min(j, kMaxK - 1)];
-        const uint32_t ti = tieIdx[max(j - int(nGt), 0)];
-        idx4[e] = j < int(nGt) ? g : ti;
+        const uint64_t g = a.gt[size_t(row) * kMaxK + min(j, kMaxK - 1)];
+        const uint64_t ti = (uint64_t(~theta) << 32) | tieIdx[max(j - int(nGt), 0)];
+        x4[e] = 4 * t + e < k ? (j < int(nGt) ? g : ti) : ~0ull;
     }
-    uint32_t key4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) key4[e] = keyAt<T>(a, row, int(min(idx4[e], uint32_t(a.V - 1))));
-    uint64_t x4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-        x4[e] = 4 * t + e < k ? (uint64_t(~key4[e]) << 32) | idx4[e] : ~0ull;
 #pragma unroll
     for (int e = 0; e < 4; ++e) item[4 * t + e] = x4[e];
     __syncthreads();
@@ -461,7 +457,7 @@ size_t greedyValueOffset(size_t V, llaisysDataType_t dt) {
 
 size_t randomSampleWorkspaceBytes(size_t rows, size_t V, llaisysDataType_t dt) {
     // sampling: candidate and tie lists of up to kSampleRows rows
-    const size_t lists = kSampleRows * (size_t(kMaxK) + size_t(kTieCap)) * sizeof(uint32_t);
+    const size_t lists = kSampleRows * (size_t(kMaxK) * sizeof(uint64_t) + size_t(kTieCap) * sizeof(uint32_t));
     const size_t greedy = greedyValueOffset(V, dt) - kScratchReserved + rows * sizeof(float);
     return std::max(lists, greedy);
 }
@@ -495,8 +491,8 @@ void randomSample(void *out_idx, bool i64, const void *logits, size_t rows, size
         a.topP = top_p;
         a.seed = seed + r0;
         a.st = reinterpret_cast<SmpRow *>(base + kSampleStateOffset);
-        a.gt = reinterpret_cast<uint32_t *>(base + kScratchReserved);
-        a.ties = a.gt + kSampleRows * kMaxK;
+        a.gt = reinterpret_cast<uint64_t *>(base + kScratchReserved);
+        a.ties = reinterpret_cast<uint32_t *>(a.gt + kSampleRows * kMaxK);
         const dim3 grid(unsigned((V + kSmpChunk - 1) / kSmpChunk), unsigned(nr));
         switch (dt) {
         case LLAISYS_DTYPE_F32:
