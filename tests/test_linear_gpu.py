@@ -57,6 +57,8 @@ SHAPES = [
     # one row with partly used chunk slots (1024 / 3000 inputs, odd channel counts) and a
     # row longer than 24 chunks per lane (16384 inputs, 16-bit weights: the streaming GEMV)
     (1, 1024, 33), (1, 3000, 77), (1, 16384, 3),
+    # 192..255 tiles of 128 x 128: the 96 x 128 tile (full and ragged last channel tile)
+    (2048, 64, 1536), (2048, 128, 1530),
 ]
 
 
