@@ -131,6 +131,7 @@ __global__ void __launch_bounds__(NWW * NWX * 64)
     constexpr int kWRows = kInt8 ? NT / 4 : NT / 8; // INT8 rows: 4 lanes x 16 codes
     constexpr int kWLoads = BW / kWRows;
     static_assert(kXLoads >= 1 && kWLoads >= 1 && TW >= 1 && TX >= 1, "tile too small for the block");
+    static_assert(BX % kXRows == 0 && BW % kWRows == 0, "the load passes must cover the tile rows");
     __shared__ __align__(16) char lds[2][(BW + BX) * kTPitch];
     const int tid = int(threadIdx.x);
     const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
