@@ -65,7 +65,7 @@ void argmaxRows(void *idx, bool idx_i64, void *val, const void *vals, size_t row
 // histograms and counters; both stay zero between launches.  Other users of the scratch
 // start at kScratchReserved.
 constexpr size_t kSampleRows = 16;            // rows per sampler launch
-constexpr size_t kSampleRowStateBytes = 20496;
+constexpr size_t kSampleRowStateBytes = 16400;
 constexpr size_t kSampleStateOffset = 256;
 constexpr size_t kScratchReserved =
     (kSampleStateOffset + kSampleRows * kSampleRowStateBytes + 255) / 256 * 256;

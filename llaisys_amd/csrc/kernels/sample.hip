@@ -11,17 +11,22 @@
 // bit-identical to the CPU statement of the rule whatever the thread order.
 //
 // Kernels per launch of up to kSampleRows rows (all on the context stream):
-//   sampleHist<1..3> : top-k radix select over the order-preserving u32 key of z -- each
-//                      level histograms one digit (11 / 11 / 10 bits) of the keys that
-//                      match the digits chosen so far; the choice of every earlier digit is
-//                      recomputed by each block from the previous histograms (integer
-//                      atomics: exact and order-free).  HBM / L2-bound, one read of the row.
-//   sampleGather     : the keys above the k-th largest (< k of them, stored as sort items
-//                      (~key << 32) | index) and the ties at it (indices).
-//   sampleFinish     : one 256-thread block per row (512 when k > 256): the k candidates
-//                      (ties by index) sorted by
-//                      (key desc, index asc) in LDS, weights, prefix sums, the top-p cut,
-//                      the draw; then re-zeroes the row's histograms and counters.
+//   sampleHist<1..2> : top-k radix select over the order-preserving u32 key of z -- each
+//                      level histograms one 11-bit digit of the keys that match the digits
+//                      chosen so far; the choice of every earlier digit is recomputed by
+//                      each block from the previous histograms (integer atomics: exact and
+//                      order-free).  HBM / L2-bound, one read of the row.
+//   sampleGather     : after the two digits, the 22-bit prefix P of the k-th largest key:
+//                      the keys whose prefix is above P (< k of them) and the "bucket" of
+//                      keys with prefix P (about one on real logits), both stored as sort
+//                      items (~key << 32) | index.
+//   sampleFinish     : one 256-thread block per row (512 when k > 256): the best `need`
+//                      bucket members by (key desc, index asc) -- sorted in LDS, or, for a
+//                      bucket larger than its list, by the key's last 10 bits resolved in a
+//                      scan of the row --; then the k candidates sorted by (key desc, index
+//                      asc) in LDS, weights, prefix sums, the top-p cut, the draw; then
+//                      re-zeroes the row's histograms and counters.
+// The selection is that of a full 32-bit radix select: the same k candidates.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -75,8 +80,7 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
 struct SmpRow {
     uint32_t h1[2048];
     uint32_t h2[2048];
-    uint32_t h3[1024];
-    uint32_t nGt, nTie, theta, need; // counters; the threshold key and the ties it takes
+    uint32_t nGt, nTie, theta, need; // counters; the 22-bit prefix P and the bucket members it takes
 };
 static_assert(sizeof(SmpRow) == kSampleRowStateBytes, "sampler state layout");
 
@@ -88,8 +92,8 @@ struct SmpArgs {
     float inv, topP;
     uint64_t seed;
     SmpRow *st;      // rows entries, reserved scratch
-    uint64_t *gt;    // rows x kMaxK candidates above the threshold: (~key << 32) | index
-    uint32_t *ties;  // rows x kTieCap indices with the threshold key
+    uint64_t *gt;    // rows x kMaxK candidates with a prefix above P: (~key << 32) | index
+    uint64_t *ties;  // rows x kTieCap bucket members (prefix P), as the same items
 };
 
 // Inclusive suffix sum within the wavefront (lane l: the sum over lanes l .. 63).
@@ -105,7 +109,7 @@ __device__ __forceinline__ uint32_t waveSuffix(uint32_t v) {
 
 // LDS scratch of one radix decision: the wave totals and the (bin, inside) result.
 struct BinScratch {
-    uint32_t wtot[kSmpBlock / kWave];
+    uint32_t wtot[512 / kWave];
     uint32_t bin, in;
 };
 
@@ -113,16 +117,18 @@ struct BinScratch {
 // returns b and, in *inside, need minus the count above b.  All kSmpBlock threads call it.
 // Thread t owns bins [t*per, (t+1)*per); the suffix sums over the threads come from wave
 // shuffles and one exchange of the wave totals (two block barriers in all).
+template <int NB = kSmpBlock>
 __device__ int chooseBin(const uint32_t *lh, int n, uint32_t need, uint32_t *inside, BinScratch &bs) {
+    static_assert(NB / kWave <= int(sizeof(BinScratch::wtot) / sizeof(uint32_t)), "wave totals");
     const int t = int(threadIdx.x), w = t / kWave;
-    const int per = n / kSmpBlock;
+    const int per = n / NB;
     uint32_t s = 0;
     for (int j = 0; j < per; ++j) s += lh[t * per + j];
     const uint32_t v = waveSuffix(s);
     if (t % kWave == 0) bs.wtot[w] = v;
     __syncthreads();
     uint32_t suf = v; // count in bins >= t*per
-    for (int x = w + 1; x < kSmpBlock / kWave; ++x) suf += bs.wtot[x];
+    for (int x = w + 1; x < NB / kWave; ++x) suf += bs.wtot[x];
     const uint32_t above = suf - s; // count in bins >= (t+1)*per
     // the thread whose range holds the crossing resolves it
     if (above < need && suf >= need) {
@@ -142,10 +148,10 @@ __device__ int chooseBin(const uint32_t *lh, int n, uint32_t need, uint32_t *ins
     return int(bs.bin);
 }
 
-// LDS for decide(): the row's three histograms and one BinScratch per level
+// LDS for decide(): the row's two histograms and one BinScratch per level
 struct DecideLds {
-    uint32_t h[2048 + 2048 + 1024];
-    BinScratch bs[3];
+    uint32_t h[2048 + 2048];
+    BinScratch bs[2];
 };
 
 // the digits chosen after `level` histograms: prefix (the key's top bits) and the count
@@ -157,13 +163,10 @@ __device__ void decide(const SmpRow &st, int level, uint32_t k, uint32_t *prefix
     for (int b = t; b < 2048; b += kSmpBlock) L.h[b] = st.h1[b];
     if (level >= 2)
         for (int b = t; b < 2048; b += kSmpBlock) L.h[2048 + b] = st.h2[b];
-    if (level >= 3)
-        for (int b = t; b < 1024; b += kSmpBlock) L.h[4096 + b] = st.h3[b];
     __syncthreads();
     uint32_t nd = k, p = 0;
     if (level >= 1) p = uint32_t(chooseBin(L.h, 2048, nd, &nd, L.bs[0]));
     if (level >= 2) p = (p << 11) | uint32_t(chooseBin(L.h + 2048, 2048, nd, &nd, L.bs[1]));
-    if (level >= 3) p = (p << 10) | uint32_t(chooseBin(L.h + 4096, 1024, nd, &nd, L.bs[2]));
     *prefix = p;
     *need = nd;
 }
@@ -195,7 +198,8 @@ __global__ void __launch_bounds__(kSmpBlock)
         __shared__ DecideLds dl;
         decide(st, LEVEL - 1, uint32_t(a.k), &prefix, &need, dl);
     }
-    constexpr int kBins = LEVEL == 3 ? 1024 : 2048;
+    static_assert(LEVEL == 1 || LEVEL == 2, "two 11-bit digits");
+    constexpr int kBins = 2048;
     for (int b = int(threadIdx.x); b < kBins; b += kSmpBlock) hist[b] = 0;
     __syncthreads();
 #pragma unroll
@@ -203,16 +207,13 @@ __global__ void __launch_bounds__(kSmpBlock)
         const int i = base + j * kSmpBlock + int(threadIdx.x);
         if (i >= a.V) break;
         const uint32_t key = keys[j];
-        if constexpr (LEVEL == 1) {
+        if constexpr (LEVEL == 1)
             atomicAdd(&hist[key >> 21], 1u);
-        } else if constexpr (LEVEL == 2) {
-            if ((key >> 21) == prefix) atomicAdd(&hist[(key >> 10) & 0x7FFu], 1u);
-        } else {
-            if ((key >> 10) == prefix) atomicAdd(&hist[key & 0x3FFu], 1u);
-        }
+        else if ((key >> 21) == prefix)
+            atomicAdd(&hist[(key >> 10) & 0x7FFu], 1u);
     }
     __syncthreads();
-    uint32_t *g = LEVEL == 1 ? st.h1 : (LEVEL == 2 ? st.h2 : st.h3);
+    uint32_t *g = LEVEL == 1 ? st.h1 : st.h2;
     for (int b = int(threadIdx.x); b < kBins; b += kSmpBlock)
         if (hist[b]) atomicAdd(g + b, hist[b]);
 }
@@ -233,7 +234,7 @@ __global__ void __launch_bounds__(kSmpBlock)
         keys[j] = keyAt<T>(a, row, i < a.V ? i : a.V - 1);
     }
     uint32_t theta = 0, need = 0;
-    decide(st, 3, uint32_t(a.k), &theta, &need, dl);
+    decide(st, 2, uint32_t(a.k), &theta, &need, dl); // theta: the 22-bit prefix P
     if (blockIdx.x == 0 && threadIdx.x == 0) {
         st.theta = theta;
         st.need = need;
@@ -244,17 +245,17 @@ __global__ void __launch_bounds__(kSmpBlock)
     if (threadIdx.x == 0) nG = nT = 0;
     __syncthreads();
     uint32_t slot[kPer]; // bit 31: tie; else candidate; position within the block's list
-    int cls[kPer];       // 0 none, 1 above theta, 2 tie
+    int cls[kPer];       // 0 none, 1 prefix above P, 2 prefix P (the bucket)
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int i = base + j * kSmpBlock + int(threadIdx.x);
         cls[j] = 0;
         if (i < a.V) {
-            const uint32_t key = keys[j];
-            if (key > theta) {
+            const uint32_t pre = keys[j] >> 10;
+            if (pre > theta) {
                 cls[j] = 1;
                 slot[j] = atomicAdd(&nG, 1u);
-            } else if (key == theta) {
+            } else if (pre == theta) {
                 cls[j] = 2;
                 slot[j] = atomicAdd(&nT, 1u);
             }
@@ -274,7 +275,7 @@ __global__ void __launch_bounds__(kSmpBlock)
             if (pos < uint32_t(kMaxK)) a.gt[size_t(row) * kMaxK + pos] = (uint64_t(~keys[j]) << 32) | i;
         } else if (cls[j] == 2) {
             const uint32_t pos = baseT + slot[j];
-            if (pos < uint32_t(kTieCap)) a.ties[size_t(row) * kTieCap + pos] = i;
+            if (pos < uint32_t(kTieCap)) a.ties[size_t(row) * kTieCap + pos] = (uint64_t(~keys[j]) << 32) | i;
         }
     }
 }
@@ -333,47 +334,65 @@ __global__ void __launch_bounds__(NT)
     __shared__ uint64_t item[kTieCap];
     __shared__ uint64_t cum[kMaxK];
     __shared__ uint64_t sbuf[NT];
-    __shared__ uint32_t tieIdx[kMaxK];
+    __shared__ uint64_t sel[kMaxK]; // the bucket members taken, as sort items
     __shared__ int kept, pick;
     const int row = int(blockIdx.x);
     const int t = int(threadIdx.x);
     SmpRow &st = a.st[row];
-    const uint32_t theta = st.theta, need = st.need, nTie = st.nTie;
+    const uint32_t prefix = st.theta, need = st.need, nB = st.nTie;
     const uint32_t nGt = min(st.nGt, uint32_t(kMaxK));
     const int k = a.k; // == nGt + need
-    // 1. the `need` smallest indices whose key equals theta
-    if (nTie <= uint32_t(kTieCap)) {
+    // 1. the `need` best bucket members (prefix P) by (key desc, index asc)
+    if (nB <= uint32_t(kTieCap)) {
         int n2 = 2;
-        while (n2 < int(nTie)) n2 *= 2;
-        for (int i = t; i < n2; i += NT)
-            item[i] = i < int(nTie) ? uint64_t(a.ties[size_t(row) * kTieCap + i]) : ~0ull;
+        while (n2 < int(nB)) n2 *= 2;
+        for (int i = t; i < n2; i += NT) item[i] = i < int(nB) ? a.ties[size_t(row) * kTieCap + i] : ~0ull;
         __syncthreads();
         bitonic(item, n2);
-        for (int i = t; i < int(need); i += NT) tieIdx[i] = uint32_t(item[i]);
+        for (int i = t; i < int(need); i += NT) sel[i] = item[i];
     } else {
-        // more ties than the list holds: rank them in index order (contiguous segments)
+        // more bucket members than the list holds: the last 10 bits of the k-th largest key
+        // from a histogram of the bucket over a scan of the row, then the members above that
+        // key (any order) and the smallest indices of its ties (contiguous segments)
+        __shared__ uint32_t h3[1024];
+        __shared__ BinScratch bs;
+        __shared__ uint32_t nAbove;
+        for (int b = t; b < 1024; b += NT) h3[b] = 0;
+        if (t == 0) nAbove = 0;
+        __syncthreads();
         const int seg = (a.V + NT - 1) / NT, lo = t * seg, hi = min(a.V, lo + seg);
+        for (int i = lo; i < hi; ++i) {
+            const uint32_t key = keyAt<T>(a, row, i);
+            if ((key >> 10) == prefix) atomicAdd(&h3[key & 0x3FFu], 1u);
+        }
+        __syncthreads();
+        uint32_t need3 = 0;
+        const uint32_t theta = (prefix << 10) | uint32_t(chooseBin<NT>(h3, 1024, need, &need3, bs));
+        for (int i = lo; i < hi; ++i) {
+            const uint32_t key = keyAt<T>(a, row, i);
+            if ((key >> 10) == prefix && key > theta) sel[atomicAdd(&nAbove, 1u)] = (uint64_t(~key) << 32) | uint32_t(i);
+        }
         uint32_t c = 0;
         for (int i = lo; i < hi; ++i) c += keyAt<T>(a, row, i) == theta;
         uint64_t tot;
-        uint32_t r = uint32_t(blockExclusive<NT>(c, sbuf, &tot));
-        for (int i = lo; i < hi && r < need; ++i)
-            if (keyAt<T>(a, row, i) == theta) tieIdx[r++] = uint32_t(i);
+        uint32_t r = uint32_t(blockExclusive<NT>(c, sbuf, &tot)); // (its barriers also order nAbove)
+        const uint32_t above = need - need3;
+        for (int i = lo; i < hi && r < need3; ++i)
+            if (keyAt<T>(a, row, i) == theta) sel[above + r++] = (uint64_t(~theta) << 32) | uint32_t(i);
     }
     __syncthreads();
     // 2. the k candidates sorted by (key desc, index asc): ascending on (~key, index)
     int nk = 2;
     while (nk < k) nk *= 2;
-    // the gather stored the candidates as sort items; the ties carry the threshold key.
-    // Loads unconditional (clamped), the padding selected after them: loads under per-lane
+    // the gather stored the candidates as sort items.  Loads unconditional (clamped), the padding selected after them: loads under per-lane
     // branches were issued one round trip at a time.
     uint64_t x4[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int j = min(4 * t + e, k - 1);
         const uint64_t g = a.gt[size_t(row) * kMaxK + min(j, kMaxK - 1)];
-        const uint64_t ti = (uint64_t(~theta) << 32) | tieIdx[max(j - int(nGt), 0)];
-        x4[e] = 4 * t + e < k ? (j < int(nGt) ? g : ti) : ~0ull;
+        const uint64_t b = sel[max(j - int(nGt), 0)];
+        x4[e] = 4 * t + e < k ? (j < int(nGt) ? g : b) : ~0ull;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) item[4 * t + e] = x4[e];
@@ -439,7 +458,6 @@ __global__ void __launch_bounds__(NT)
     for (int b = t; b < 2048; b += NT) {
         st.h1[b] = 0;
         st.h2[b] = 0;
-        if (b < 1024) st.h3[b] = 0;
     }
     if (t == 0) st.nGt = st.nTie = st.theta = st.need = 0;
 }
@@ -457,7 +475,7 @@ size_t greedyValueOffset(size_t V, llaisysDataType_t dt) {
 
 size_t randomSampleWorkspaceBytes(size_t rows, size_t V, llaisysDataType_t dt) {
     // sampling: candidate and tie lists of up to kSampleRows rows
-    const size_t lists = kSampleRows * (size_t(kMaxK) * sizeof(uint64_t) + size_t(kTieCap) * sizeof(uint32_t));
+    const size_t lists = kSampleRows * (size_t(kMaxK) + size_t(kTieCap)) * sizeof(uint64_t);
     const size_t greedy = greedyValueOffset(V, dt) - kScratchReserved + rows * sizeof(float);
     return std::max(lists, greedy);
 }
@@ -492,13 +510,12 @@ void randomSample(void *out_idx, bool i64, const void *logits, size_t rows, size
         a.seed = seed + r0;
         a.st = reinterpret_cast<SmpRow *>(base + kSampleStateOffset);
         a.gt = reinterpret_cast<uint64_t *>(base + kScratchReserved);
-        a.ties = reinterpret_cast<uint32_t *>(a.gt + kSampleRows * kMaxK);
+        a.ties = a.gt + kSampleRows * kMaxK;
         const dim3 grid(unsigned((V + kSmpChunk - 1) / kSmpChunk), unsigned(nr));
         switch (dt) {
         case LLAISYS_DTYPE_F32:
             sampleHist<F32, 1><<<grid, kSmpBlock, 0, s>>>(a);
             sampleHist<F32, 2><<<grid, kSmpBlock, 0, s>>>(a);
-            sampleHist<F32, 3><<<grid, kSmpBlock, 0, s>>>(a);
             sampleGather<F32><<<grid, kSmpBlock, 0, s>>>(a);
             if (k > 256)
                 sampleFinish<F32, kFinThreadsWide><<<unsigned(nr), kFinThreadsWide, 0, s>>>(a);
@@ -508,7 +525,6 @@ void randomSample(void *out_idx, bool i64, const void *logits, size_t rows, size
         case LLAISYS_DTYPE_BF16:
             sampleHist<BF16, 1><<<grid, kSmpBlock, 0, s>>>(a);
             sampleHist<BF16, 2><<<grid, kSmpBlock, 0, s>>>(a);
-            sampleHist<BF16, 3><<<grid, kSmpBlock, 0, s>>>(a);
             sampleGather<BF16><<<grid, kSmpBlock, 0, s>>>(a);
             if (k > 256)
                 sampleFinish<BF16, kFinThreadsWide><<<unsigned(nr), kFinThreadsWide, 0, s>>>(a);
@@ -518,7 +534,6 @@ void randomSample(void *out_idx, bool i64, const void *logits, size_t rows, size
         case LLAISYS_DTYPE_F16:
             sampleHist<F16, 1><<<grid, kSmpBlock, 0, s>>>(a);
             sampleHist<F16, 2><<<grid, kSmpBlock, 0, s>>>(a);
-            sampleHist<F16, 3><<<grid, kSmpBlock, 0, s>>>(a);
             sampleGather<F16><<<grid, kSmpBlock, 0, s>>>(a);
             if (k > 256)
                 sampleFinish<F16, kFinThreadsWide><<<unsigned(nr), kFinThreadsWide, 0, s>>>(a);

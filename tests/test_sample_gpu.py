@@ -67,6 +67,22 @@ def test_random_sample_ties_and_tie_overflow():
                 assert np.array_equal(gpu_sample(x, "f32", 1.0, k, p, seed), exp), (x.shape, k, p, seed)
 
 
+def test_random_sample_bucket_overflow_with_distinct_keys():
+    # more than 4096 logits share the top 22 bits of the k-th key (1 + j ulp, 1024 distinct
+    # values, about five copies each, scattered): the finish resolves the last 10 bits in a
+    # scan of the row, then takes the members above that key and the ties at it by index
+    rng = np.random.default_rng(8)
+    x = np.full((2, 20000), -1.0, np.float32)
+    for r in range(2):
+        pos = rng.choice(20000, 5000, replace=False)
+        x[r, pos] = (np.float32(1.0) + (np.arange(5000) % 1024).astype(np.float32) * np.float32(2.0 ** -23))
+    x[1, 123] = 2.0  # one key above the bucket
+    for seed in (3, 77):
+        for k, p in ((100, 0.9), (1024, 1.0), (9, 0.5)):
+            exp = oracle.random_sample(x, 1.0, k, p, seed)
+            assert np.array_equal(gpu_sample(x, "f32", 1.0, k, p, seed), exp), (k, p, seed)
+
+
 def test_random_sample_repeats_and_int32_output():
     rng = np.random.default_rng(5)
     x = conv(rng.standard_normal((2, 151936)) * 3, "bf16")
