@@ -444,15 +444,15 @@ __global__ void __launch_bounds__(256)
 // >= 1 GiB of rotating weight sets): W8A16 [8960, 1536] 5.47 us against 6.79 us for
 // linearSkinny and 7.55 us for linearGemv; bf16 [8960, 1536] 6.17 against 7.39 us; W8A16
 // [1536, 8960] 6.41 against 7.00 us; bf16 [1536, 8960] 8.28 against 9.38 us.
-template <typename T, bool kInt8, int J, int C, bool kLds>
-__global__ void __launch_bounds__(256)
+template <typename T, bool kInt8, int J, int C, bool kLds, int NW>
+__global__ void __launch_bounds__(NW * kWave)
     linearGemvRow(LinearArgs a) {
     using F = Fmt<T>;
     constexpr int E = kInt8 ? 16 : 8; // weight elements per 16-byte chunk
     extern __shared__ __align__(16) char xs_raw[];
     const uint16_t *xs = kLds ? reinterpret_cast<const uint16_t *>(xs_raw) : static_cast<const uint16_t *>(a.x);
     const int lane = int(threadIdx.x) % kWave;
-    const int n0 = (int(blockIdx.x) * 4 + int(threadIdx.x) / kWave) * C; // wave-uniform
+    const int n0 = (int(blockIdx.x) * NW + int(threadIdx.x) / kWave) * C; // wave-uniform
     const int nc = a.K / E;
     // a channel past the last loads a valid row and stores nothing (its wave still joins the
     // block barrier); a chunk past the row end reads chunk 0 and is skipped
@@ -468,7 +468,7 @@ __global__ void __launch_bounds__(256)
         }
     }
     if constexpr (kLds) {
-        for (int i = int(threadIdx.x); i < a.K / 8; i += 256)
+        for (int i = int(threadIdx.x); i < a.K / 8; i += NW * kWave)
             reinterpret_cast<v4u *>(xs_raw)[i] = reinterpret_cast<const v4u *>(a.x)[i];
         __syncthreads();
     }
@@ -530,16 +530,20 @@ __global__ void __launch_bounds__(256)
 //    (larger N loses: [18944, 3584] 14.4 -> 15.3 us; bf16 [1536, 8960] 8.1 -> 8.7 us);
 //  - 4 channels per wave for INT8 rows of at most 2 chunks per lane over 65536+ channels (the
 //    lm_head), which spreads the block's x staging over 16 rows: [151936, 1536] 46.0 -> 40.0 us
-//    (at [8960, 1536] it loses, 5.45 -> 6.57 us: too few blocks).
-template <typename T, bool kInt8, int C, bool kLds, int J>
+//    (at [8960, 1536] it loses, 5.45 -> 6.57 us: too few blocks);
+//  - waves per block: 8 where x is staged (the staging shared by more rows: bf16 [1536, 8960]
+//    8.19 -> 7.70 us, [1536, 1536] 3.10 -> 2.95 us, [8960, 1536] 6.17 -> 6.09 us; 16 waves
+//    10.5 us), 2 where it is read from L1 / L2 (INT8 [1536, 8960] 5.88 -> 5.68 us), 4 for
+//    the 4-channel lm_head waves (8: 40.7 -> 42.6 us).
+template <typename T, bool kInt8, int C, bool kLds, int NW, int J>
 bool launchRowJ(const LinearArgs &a, int j, hipStream_t s) {
     if constexpr (J > 0) {
         if (j == J) {
-            const unsigned blocks = unsigned((a.N + 4 * C - 1) / (4 * C));
-            linearGemvRow<T, kInt8, J, C, kLds><<<blocks, 256, kLds ? size_t(a.K) * 2 : 0, s>>>(a);
+            const unsigned blocks = unsigned((a.N + NW * C - 1) / (NW * C));
+            linearGemvRow<T, kInt8, J, C, kLds, NW><<<blocks, NW * kWave, kLds ? size_t(a.K) * 2 : 0, s>>>(a);
             return true;
         }
-        return launchRowJ<T, kInt8, C, kLds, J - 1>(a, j, s);
+        return launchRowJ<T, kInt8, C, kLds, NW, J - 1>(a, j, s);
     }
     return false;
 }
@@ -551,10 +555,10 @@ bool launchGemv1(const LinearArgs &a, hipStream_t s) {
     const int j = (a.K / E + kWave - 1) / kWave;
     if (j < 1 || j > 24) return false;
     if constexpr (kInt8) {
-        if (a.N <= 4096) return launchRowJ<T, true, 1, false, 24>(a, j, s);
-        if (a.N >= 65536 && j <= 2) return launchRowJ<T, true, 4, true, 2>(a, j, s);
+        if (a.N <= 4096) return launchRowJ<T, true, 1, false, 2, 24>(a, j, s);
+        if (a.N >= 65536 && j <= 2) return launchRowJ<T, true, 4, true, 4, 2>(a, j, s);
     }
-    return launchRowJ<T, kInt8, 1, true, 24>(a, j, s);
+    return launchRowJ<T, kInt8, 1, true, 8, 24>(a, j, s);
 }
 
 template <typename T, bool kInt8>
