@@ -623,6 +623,49 @@ def test_graph_replays_match_eager():
     no_device_error()
 
 
+def test_graph_replays_sampling_and_int8_prefill():
+    """Random sampling (histogram state left zero by each launch, top_k 50 and 1024) and a
+    bf16 prefill over an INT8 cache (the caches dequantized into the workspace, then the bf16
+    kernel) captured in one graph: three replays with eager work between them must equal
+    the eager results."""
+    BF, I64 = L.DataType.BF16, L.DataType.I64
+    rng = np.random.default_rng(41)
+    logits = dev(sample(rng, (2, 151936), "bf16"), BF)
+    kv = f32_to_bf16(rng.standard_normal((2, 300, 2, 128)).astype(np.float32))
+    kq, ks = oracle.quantize_int8(kv[0])
+    vq, vs = oracle.quantize_int8(kv[1])
+    tq = dev(sample(rng, (64, 12, 128), "bf16"), BF)
+    tkq, tks, tvq, tvs = dev(kq), dev(ks), dev(vq), dev(vs)
+    s50, s1k, att = empty((2,), I64), empty((2,), I64), empty((64, 12, 128), BF)
+
+    def ops():
+        L.Ops.random_sample(s50, logits, 0.8, 50, 0.8, 1234)
+        L.Ops.random_sample(s1k, logits, 1.0, 1024, 0.95, 99)
+        L.Ops.self_attention_int8kv(att, tq, tkq, tks, tvq, tvs, 0.0883883)
+
+    ops()
+    eager = [t.numpy() for t in (s50, s1k, att)]
+    graph = L.Graph.capture()
+    ops()
+    graph.end()
+    api = L.RuntimeAPI(L.DeviceType.AMD)
+    for replay in range(3):
+        # eager work between replays: other samples and a decode attention
+        L.Ops.random_sample(empty((2,), I64), logits, 0.7, 40, 1.0, replay)
+        L.Ops.self_attention_int8kv(empty((1, 12, 128), BF), dev(sample(rng, (1, 12, 128), "bf16"), BF),
+                                    tkq, tks, tvq, tvs, 0.0883883)
+        api.device_synchronize()
+        for t in (s50, s1k, att):
+            z = np.zeros(t.shape(), dtype=t.numpy().dtype)
+            api.memcpy_sync(t.data_ptr(), z.ctypes.data, z.nbytes, L.MemcpyKind.H2D)
+        graph.launch()
+        api.device_synchronize()
+        for name, t, e in zip(("top_k 50", "top_k 1024", "int8 prefill"), (s50, s1k, att), eager):
+            assert_exact(t.numpy(), e, f"replay {replay}: {name}")
+    del graph
+    no_device_error()
+
+
 def test_graph_keeps_its_workspace_after_growth(monkeypatch):
     """A graph whose kernels use the library scratch (the flat argmax's counter, the
     decode attention's partials) stays valid after a later eager op grows the scratch:
