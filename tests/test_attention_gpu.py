@@ -112,7 +112,10 @@ def test_self_attention_empty_cache_gives_zeros():
 @pytest.mark.parametrize("shape", [(1, 4097, 12, 2, 128), (128, 128, 12, 2, 128), (5, 11, 4, 2, 8), (7, 33, 4, 2, 64),
                                    # bf16 prefill over the INT8 cache on the MFMA kernel: a prefix
                                    # cache, GQA 4 with ragged tiles, unsplit (> 512 blocks)
-                                   (200, 1000, 12, 2, 128), (48, 70, 32, 8, 128), (300, 300, 168, 28, 128)],
+                                   (200, 1000, 12, 2, 128), (48, 70, 32, 8, 128), (300, 300, 168, 28, 128),
+                                   # a cache whose bf16 form exceeds the workspace of 16 x 2
+                                   # query-heads: the INT8 MFMA kernel converts the codes itself
+                                   (16, 20000, 2, 2, 128)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_self_attention_int8kv(dt, shape):
     """INT8 cache (1% outliers x20, as config 3) against dequantize-then-attend on the GPU
@@ -121,6 +124,9 @@ def test_self_attention_int8kv(dt, shape):
     so it equals the composition bit for bit; the other forms convert codes in their own key
     tiling, within the attention tolerance."""
     seq, total, nh, nkvh, d = shape
+    if total > 16384 and dt == "f32":
+        pytest.skip("f32 sums over 20000 keys: two f32 summation orders differ beyond the fixed "
+                    "2^-16 max|v| floor; the shape is here for the bf16 / f16 MFMA fallback")
     rng = np.random.default_rng(zlib.crc32(repr(("int8", dt, shape)).encode()))
     x = rng.standard_normal((2, total, nkvh, d), dtype=np.float32)
     x[rng.random(x.shape) < 0.01] *= 20
