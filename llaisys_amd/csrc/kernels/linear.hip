@@ -472,13 +472,20 @@ __global__ void __launch_bounds__(NW * kWave)
             reinterpret_cast<v4u *>(xs_raw)[i] = reinterpret_cast<const v4u *>(a.x)[i];
         __syncthreads();
     }
+    // chunk-major: the lane's x chunk is unpacked once for the wave's C channels; each
+    // channel still sums its chunks and elements in the same order (one FMA chain)
+    float acc[C];
 #pragma unroll
-    for (int ci = 0; ci < C; ++ci) {
-        float acc = 0.0f;
+    for (int ci = 0; ci < C; ++ci) acc[ci] = 0.0f;
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int c = lane + kWave * j;
-            if (c >= nc) continue; // (the lane's remaining chunks are past the end too)
+    for (int j = 0; j < J; ++j) {
+        const int c = lane + kWave * j;
+        if (c >= nc) continue; // (the lane's remaining chunks are past the end too)
+        float xf[E];
+#pragma unroll
+        for (int h = 0; h < E / 8; ++h) F::unpack(*reinterpret_cast<const v4u *>(xs + c * E + 8 * h), xf + 8 * h);
+#pragma unroll
+        for (int ci = 0; ci < C; ++ci) {
             float wf[E];
             if constexpr (kInt8) {
                 const uint32_t ww[4] = {wv[ci][j].x, wv[ci][j].y, wv[ci][j].z, wv[ci][j].w};
@@ -488,14 +495,12 @@ __global__ void __launch_bounds__(NW * kWave)
                 F::unpack(wv[ci][j], wf);
             }
 #pragma unroll
-            for (int h = 0; h < E / 8; ++h) {
-                float xf[8];
-                F::unpack(*reinterpret_cast<const v4u *>(xs + c * E + 8 * h), xf);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(xf[e], wf[8 * h + e], acc);
-            }
+            for (int e = 0; e < E; ++e) acc[ci] = __builtin_fmaf(xf[e], wf[e], acc[ci]);
         }
-        float t = waveGroupReduce<kWave, SumOp>(acc);
+    }
+#pragma unroll
+    for (int ci = 0; ci < C; ++ci) {
+        float t = waveGroupReduce<kWave, SumOp>(acc[ci]);
         const int n = n0 + ci;
         if (lane == 0 && n < a.N) {
             if constexpr (kInt8) t = a.scale[n] * t;
