@@ -98,6 +98,9 @@ __global__ void __launch_bounds__(NW * kWave)
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             if (c0 + kWave * u >= nc) continue;
+            float xf[E]; // unpacked once for the wave's R rows; each row's sum keeps its order
+#pragma unroll
+            for (int h = 0; h < E / 8; ++h) F::unpack(xv[u][h], xf + 8 * h);
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 float wf[E];
@@ -109,12 +112,7 @@ __global__ void __launch_bounds__(NW * kWave)
                     F::unpack(wv[r][u], wf);
                 }
 #pragma unroll
-                for (int h = 0; h < E / 8; ++h) {
-                    float xf[8];
-                    F::unpack(xv[u][h], xf);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[r] = __builtin_fmaf(xf[e], wf[8 * h + e], acc[r]);
-                }
+                for (int e = 0; e < E; ++e) acc[r] = __builtin_fmaf(xf[e], wf[e], acc[r]);
             }
         }
         c0 += kWave * U;
