@@ -712,12 +712,12 @@ constexpr int kDecWaves = 4;
 constexpr int kDecKT = 32;   // keys per wave step
 constexpr int kDecVtLd = 40; // V^T row stride (bf16): 16-byte reads of rows 16 apart hit distinct banks
 
-template <bool kInt8>
-__global__ void __launch_bounds__(kWave * kDecWaves)
+template <bool kInt8, int NW>
+__global__ void __launch_bounds__(kWave * NW)
     attnDecodeMfma(AttnArgs a) {
     constexpr int D = 128, KB = D / 32, DT = D / 16;
-    __shared__ uint16_t vt[kDecWaves][D][kDecVtLd];
-    __shared__ float st[kDecWaves][16][D + 2];
+    __shared__ uint16_t vt[NW][D][kDecVtLd];
+    __shared__ float st[NW][16][D + 2];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
     const int n = lane % 16, g4 = lane / 16;
@@ -748,7 +748,7 @@ __global__ void __launch_bounds__(kWave * kDecWaves)
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    for (size_t kt0 = k0 + size_t(wave) * kDecKT; kt0 < k1; kt0 += size_t(kDecWaves) * kDecKT) {
+    for (size_t kt0 = k0 + size_t(wave) * kDecKT; kt0 < k1; kt0 += size_t(NW) * kDecKT) {
         const int nk = int(min(k1 - kt0, size_t(kDecKT)));
         const bool part = nk < kDecKT; // the chunk's last, partial step (wave-uniform)
         // Loads are unconditional: a key past the step reads the step's first key and is
@@ -900,14 +900,14 @@ __global__ void __launch_bounds__(kWave * kDecWaves)
         }
     }
     __syncthreads();
-    for (int pi = threadIdx.x; pi < a.group * D; pi += kWave * kDecWaves) {
+    for (int pi = threadIdx.x; pi < a.group * D; pi += kWave * NW) {
         const int j = pi / D, e = pi % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, st[w][j][D]);
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, st[w][j][D]);
         float L = 0.0f, O = 0.0f;
 #pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float mw = st[w][j][D];
             const float f = mw == M ? 1.0f : __builtin_amdgcn_exp2f((mw - M) * c2); // 1 for M = -inf, where l = o = 0
             L += st[w][j][D + 1] * f;
@@ -1016,7 +1016,11 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
     if constexpr (std::is_same_v<T, BF16>) {
         if (d == 128 && a.total > 0 && a.seq < size_t(kMfmaQ) && a.group <= 16 && a.scale > 0.0f &&
             std::isfinite(a.scale)) {
-            const size_t bk = size_t(kDecWaves) * kDecKT; // keys per block step
+            // waves per block: 8 for caches of 16K+ keys (half the partials to merge: 32K
+            // decode 14.6 -> 13.3 us INT8 KV, 14.4 -> 13.8 us bf16 KV), 4 below (more blocks for the
+            // shorter chains: the 4096-key decode step lost with 8)
+            const int nw = a.total >= 16384 ? 8 : kDecWaves;
+            const size_t bk = size_t(nw) * kDecKT; // keys per block step
             const size_t pairs = a.seq * size_t(a.nh);
             size_t nchunks = std::min<size_t>((a.total + bk - 1) / bk, 1024);
             nchunks = std::max<size_t>(1, std::min(nchunks, ws_bytes / (size_t(d + 2) * sizeof(float) * pairs)));
@@ -1024,7 +1028,10 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
             a.chunk = int(std::min<size_t>((a.total + nchunks - 1) / nchunks, size_t(INT32_MAX)));
             a.part = static_cast<float *>(ws);
             const unsigned blocks = unsigned(a.seq * size_t(a.nkvh) * nchunks);
-            attnDecodeMfma<kInt8><<<blocks, kWave * kDecWaves, 0, s>>>(a);
+            if (nw == 8)
+                attnDecodeMfma<kInt8, 8><<<blocks, kWave * 8, 0, s>>>(a);
+            else
+                attnDecodeMfma<kInt8, kDecWaves><<<blocks, kWave * kDecWaves, 0, s>>>(a);
             if (nchunks > 1)
                 launchCombine<T>(a.out, a.part, a.nchunks, d, pairs, s);
             return;

