@@ -36,8 +36,10 @@ namespace llaisys::kernels {
 
 namespace {
 
-constexpr int kSmpBlock = 256;
-constexpr int kSmpChunk = kSmpBlock * 8; // elements per histogram block
+// histogram / gather blocks: 1024 threads, 2 keys each (75 blocks over 151936 logits):
+// top_k 50 22.9 -> 20.6 us against 256 threads x 8 keys (512 x 4: 21.3 us; 1024 x 1: 20.9 us)
+constexpr int kSmpBlock = 1024;
+constexpr int kSmpChunk = kSmpBlock * 2; // elements per histogram block
 constexpr int kMaxK = 1024;
 constexpr int kTieCap = 4096;
 
@@ -109,7 +111,7 @@ __device__ __forceinline__ uint32_t waveSuffix(uint32_t v) {
 
 // LDS scratch of one radix decision: the wave totals and the (bin, inside) result.
 struct BinScratch {
-    uint32_t wtot[512 / kWave];
+    uint32_t wtot[1024 / kWave];
     uint32_t bin, in;
 };
 
