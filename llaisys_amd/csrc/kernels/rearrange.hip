@@ -9,10 +9,11 @@
 //  - rowCopy:   the innermost dimension is contiguous in both layouts: rows of R bytes are
 //               copied in the widest unit (16 / 8 / 4 / 2 / 1 B) that divides R and the
 //               base addresses; HBM-bound, 1 read + 1 write per byte.
-//  - tileCopyVec / tileCopy: the output's contiguous dimension is strided in the input, and
-//               another dimension is contiguous there (a transpose): tiles through LDS, both
-//               sides coalesced, in 16-byte vectors when the shape and alignment allow, else
-//               32 x 32 elements one per thread; HBM-bound.
+//  - tileCopy128 / tileCopyVec / tileCopy: the output's contiguous dimension is strided in
+//               the input, and another dimension is contiguous there (a transpose): tiles
+//               through LDS, both sides coalesced, in 16-byte vectors when the shape and
+//               alignment allow (128 x 128 tiles for 2-byte elements), else 32 x 32 elements
+//               one per thread; HBM-bound.
 //  - gatherCopy: anything else, one thread per element.
 #include "common.hpp"
 #include "launch.hpp"
@@ -128,6 +129,50 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// 2-byte elements, 16-byte vectors on both sides: 128 x 128 tiles (8 vectors per thread in
+// flight), loads unconditional (clamped at ragged edges) and non-temporal, the tile written
+// as 16-byte rows with chunk c of row r at c ^ ((r / 8) % 16) so that the transposed 2-byte
+// reads of rows 8 apart fall in different banks, and the blocks ordered with the output's
+// contiguous dimension fastest.  Measured on MI355X (8192 x 8192 bf16, rotating sets):
+// 56.8 us against 62.6 us for tileCopyVec's 64 x 64 tiles (59.8 us with the input's
+// contiguous dimension fastest; 63.5 us with padded rows instead of the swizzle).
+__global__ void __launch_bounds__(256)
+    tileCopy128(uint16_t *out, const uint16_t *in, Dims rest, int64_t np, int64_t nq, int64_t sp_out,
+                int64_t sq_in) {
+    constexpr int VE = 8, T = 128, VR = T / VE, NV = T * VR / 256;
+    __shared__ __align__(16) uint16_t tile[T * T];
+    int64_t oi, oo;
+    offsets(rest, rest.nd, blockIdx.z, oi, oo);
+    const int64_t q0 = int64_t(blockIdx.x) * T, p0 = int64_t(blockIdx.y) * T;
+    v4u x[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) { // tile row r = q offset, vector v along p
+        const int k = int(threadIdx.x) + 256 * i, r = k / VR, v = k % VR;
+        const int64_t q = min(q0 + r, nq - 1), p = min(p0 + int64_t(v) * VE, np - VE);
+        x[i] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(in + oi + p + q * sq_in));
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int k = int(threadIdx.x) + 256 * i, r = k / VR, v = k % VR;
+        *reinterpret_cast<v4u *>(&tile[r * T + (v ^ ((r >> 3) & (VR - 1))) * VE]) = x[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NV; ++i) { // output row p0 + r, vector v along q
+        const int k = int(threadIdx.x) + 256 * i, r = k / VR, v = k % VR;
+        uint16_t e[VE];
+#pragma unroll
+        for (int j = 0; j < VE; ++j) {
+            const int row = v * VE + j;
+            e[j] = tile[row * T + ((r / VE) ^ ((row >> 3) & (VR - 1))) * VE + r % VE];
+        }
+        const int64_t p = p0 + r, q = q0 + int64_t(v) * VE;
+        v4u y;
+        __builtin_memcpy(&y, e, 16);
+        if (p < np && q < nq) __builtin_nontemporal_store(y, reinterpret_cast<v4u *>(out + oo + q + p * sp_out));
+    }
+}
+
 template <typename E>
 __global__ void __launch_bounds__(256)
     gatherCopy(E *out, const E *in, Dims d, int64_t n) {
@@ -222,6 +267,12 @@ void rearrange(void *out, const void *in, size_t ndim, const size_t *shape, cons
                    (reinterpret_cast<uintptr_t>(o) | reinterpret_cast<uintptr_t>(i)) % 16 == 0;
         for (int k = 0; vec && k < rest.nd; ++k) vec = rest.sin[k] % ve == 0 && rest.sout[k] % ve == 0;
         const int64_t tv = esize == 4 ? 32 : 64;
+        if (vec && esize == 2 && nz <= 65535 && (np + 127) / 128 <= 65535) {
+            const dim3 grid(unsigned((nq + 127) / 128), unsigned((np + 127) / 128), unsigned(nz));
+            tileCopy128<<<grid, 256, 0, s>>>(reinterpret_cast<uint16_t *>(o), reinterpret_cast<const uint16_t *>(i), rest,
+                                            np, nq, spo, sqi);
+            return;
+        }
         if (vec && nz <= 65535 && (nq + tv - 1) / tv <= 65535) {
             const dim3 grid(unsigned((np + tv - 1) / tv), unsigned((nq + tv - 1) / tv), unsigned(nz));
             switch (esize) {

@@ -37,13 +37,15 @@ CASES = [
     ((6, 4, 10), (1, 0, 2), L.DataType.I64),          # 8-byte elements, rows of 80 B
     ((1, 1, 64), (2, 0, 1), L.DataType.F32),          # size-1 dims collapse to a row copy
     ((8, 1, 3), (2, 1, 0), L.DataType.BF16),
-    # 16-byte-vector transpose tiles: ragged edges of the 64 x 64 (2-byte), 64 x 64 (1-byte)
-    # and 32 x 32 (4-byte) tiles, outer dims on z, and a full multiple
+    # 16-byte-vector transpose tiles: ragged edges of the 128 x 128 (2-byte), 64 x 64 (1-byte)
+    # and 32 x 32 (4-byte) tiles, outer dims on z, and full multiples
     ((200, 72), (1, 0), L.DataType.BF16),
     ((3, 40, 136), (0, 2, 1), L.DataType.BF16),
     ((48, 80), (1, 0), L.DataType.I8),
     ((100, 36), (1, 0), L.DataType.F32),
     ((256, 512), (1, 0), L.DataType.BF16),
+    ((1000, 264), (1, 0), L.DataType.BF16),           # 2-byte tiles ragged on both sides
+    ((2, 3, 384, 136), (0, 1, 3, 2), L.DataType.BF16),  # two outer dims on z
     # vector-eligible in shape but one side's extent not a whole vector: element tiles
     ((200, 70), (1, 0), L.DataType.BF16),
 ]
