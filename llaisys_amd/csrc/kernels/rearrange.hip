@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 
 namespace llaisys::kernels {
 
@@ -46,16 +47,40 @@ __device__ __forceinline__ void offsets(const Dims &d, int nd, int64_t idx, int6
     }
 }
 
-template <typename U>
+// the offsets of `offsets` in 32-bit index arithmetic (every extent and the index < 2^32)
+__device__ __forceinline__ void offsets32(const Dims &d, int nd, uint32_t idx, int64_t &oi, int64_t &oo) {
+    oi = 0;
+    oo = 0;
+    for (int k = nd - 1; k >= 0; --k) {
+        const uint32_t sh = uint32_t(d.shape[k]);
+        const uint32_t c = idx % sh;
+        idx /= sh;
+        oi += int64_t(c) * d.sin[k];
+        oo += int64_t(c) * d.sout[k];
+    }
+}
+
+template <typename U, bool k32>
 __global__ void __launch_bounds__(256)
     rowCopy(char *out, const char *in, Dims d, int64_t rows, int64_t units, int esize) {
-    // d covers the outer dims (the row index); a row is `units` units of U, contiguous in both
+    // d covers the outer dims (the row index); a row is `units` units of U, contiguous in both.
+    // k32: rows * units < 2^31, so the index arithmetic runs in 32 bits (64-bit division is
+    // a long instruction sequence on the GPU)
     const int64_t total = rows * units;
     for (int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x; t < total; t += int64_t(gridDim.x) * 256) {
-        const int64_t r = t / units, u = t % units;
-        int64_t oi, oo;
-        offsets(d, d.nd, r, oi, oo);
-        reinterpret_cast<U *>(out + oo * esize)[u] = reinterpret_cast<const U *>(in + oi * esize)[u];
+        int64_t r, u, oi, oo;
+        if constexpr (k32) {
+            const uint32_t t32 = uint32_t(t), un = uint32_t(units);
+            r = int64_t(t32 / un);
+            u = int64_t(t32 % un);
+            offsets32(d, d.nd, uint32_t(r), oi, oo);
+        } else {
+            r = t / units;
+            u = t % units;
+            offsets(d, d.nd, r, oi, oo);
+        }
+        __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const U *>(in + oi * esize) + u),
+                                    reinterpret_cast<U *>(out + oo * esize) + u);
     }
 }
 
@@ -235,13 +260,21 @@ void rearrange(void *out, const void *in, size_t ndim, const size_t *shape, cons
         while (ub > 1 && !fits(ub)) ub /= 2;
         const int64_t units = rowBytes / ub;
         const unsigned g = gridFor(rows * units);
-        switch (ub) {
-        case 16: rowCopy<v4u><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
-        case 8: rowCopy<uint64_t><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
-        case 4: rowCopy<uint32_t><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
-        case 2: rowCopy<uint16_t><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
-        default: rowCopy<uint8_t><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
-        }
+        const auto go = [&](auto k32) {
+            constexpr bool K = decltype(k32)::value;
+            switch (ub) {
+            case 16: rowCopy<v4u, K><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+            case 8: rowCopy<uint64_t, K><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+            case 4: rowCopy<uint32_t, K><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+            case 2: rowCopy<uint16_t, K><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+            default: rowCopy<uint8_t, K><<<g, 256, 0, s>>>(o, i, outer, rows, units, int(esize)); break;
+            }
+        };
+        // (the grid-stride index stays below total + grid * 256 <= total + 2^22)
+        if (rows * units < (int64_t(1) << 31) - (int64_t(1) << 23))
+            go(std::true_type{});
+        else
+            go(std::false_type{});
         return;
     }
     // transpose: output contiguous in dim q = last, input contiguous in some dim p != q
