@@ -698,6 +698,225 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
     }
 }
 
+// ---- prefill on MFMA over a bf16 cache: tiles HBM -> LDS with no register staging -------
+// The arithmetic of attnMfma (same operands, same MFMA order, same bits), with the K and V
+// tiles moved by global_load_lds_dwordx4: one instruction fills 1 KB of LDS (4 key rows of
+// 256 bytes) straight from memory, so a step spends no VALU on staging and holds no tile in
+// registers.  V stays row-major in LDS and the Vᵀ operand of O^T += V^T P^T comes from two
+// ds_read_b64_tr_b16: within each 16 lanes, lane j's element e is element j % 4 of the 8
+// bytes lane 4e + j / 4 addresses (measured on MI355X), so lanes i reading 4 columns
+// 4(i % 4) .. of key row 8g + i / 4 (then + 4) hand lane j of group g the 8 consecutive keys
+// 8g .. 8g + 7 of column j.  Rows cannot be padded (the load fills LDS contiguously), so
+// the 16-byte chunks of each row are XOR-swizzled by row bits: K by (r & 3) | (r >> 3 & 3) << 2,
+// which spreads the 16 rows one ds_read_b128 of an A operand touches over all banks, V by
+// 2 ((r & 3) | (r >> 3 & 1) << 2), which spreads the 8 rows of 32 lanes' transposing reads.
+// Two LDS stages: the loads of tile t + 1 are issued after the barrier that ends every
+// wave's reads of tile t - 1 and land while tile t is computed.  Keys past the cache load
+// row 0 (finite wherever the reference's own output is; masked keys weigh 0).
+typedef short v4s __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int swzK(int r) { return (r & 3) | (((r >> 3) & 3) << 2); }
+__device__ __forceinline__ int swzV(int r) { return ((r & 3) | (((r >> 3) & 1) << 2)) << 1; }
+__device__ __forceinline__ uint64_t ldsReadTr16(const char *p) {
+    const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s *)(p));
+    return __builtin_bit_cast(uint64_t, r);
+}
+
+template <int W, bool kSplit>
+__global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
+    attnMfmaLds(AttnArgs a) {
+    constexpr int D = 128, KB = D / 32, DT = D / 16;
+    constexpr int NHALF = kSplit ? 2 : 1;
+    constexpr int kRowB = 2 * D;              // bytes of a key row
+    constexpr int kTileB = kMfmaKT * kRowB;   // one K or V tile
+    constexpr int kLoads = 2 * kTileB / 1024; // 1 KB load instructions per stage
+    constexpr int kPer = (kLoads + W - 1) / W;
+    __shared__ __align__(16) char lds_all[NHALF][2][2 * kTileB]; // [half][stage][K tile | V tile]
+    const int wave_all = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int half = kSplit ? wave_all / W : 0;
+    const int wave = wave_all % W;
+    const int lane = int(threadIdx.x) % kWave;
+    const int n = lane % 16, g4 = lane / 16;
+
+    const size_t nqb = (a.seq + kMfmaQ - 1) / kMfmaQ;
+    unsigned b = blockIdx.x;
+    const int sl = int(b % unsigned(a.slices));
+    b /= unsigned(a.slices);
+    const int g = int(b % unsigned(a.nkvh));
+    const size_t qb = nqb - 1 - size_t(b / unsigned(a.nkvh)); // latest queries first
+    const int h = g * a.group + sl * W + wave;
+    const size_t q0 = qb * kMfmaQ;
+    const size_t qi = min(q0 + size_t(n), a.seq - 1);
+    const size_t vis_q = visibleKeys(a.total, a.seq, qi);
+    const size_t vis_blk = visibleKeys(a.total, a.seq, min(q0 + kMfmaQ - 1, a.seq - 1));
+    const size_t vis_first = visibleKeys(a.total, a.seq, q0);
+    const size_t ntiles = (vis_blk + kMfmaKT - 1) / kMfmaKT;
+    const float c2 = a.scale * 1.4426950408889634f;
+
+    bf16x8 qreg[KB];
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        const uint16_t *qp = static_cast<const uint16_t *>(a.q) + (qi * a.nh + h) * D + 32 * kb + 8 * g4;
+        qreg[kb] = asBf16x8(*reinterpret_cast<const v4u *>(qp));
+    }
+    float m = -INFINITY, lsum = 0.0f;
+    f32x4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // load instruction j of this wave is stage load q = wave + W j (K rows for q < 16, then
+    // V rows): rows 4 (q % 16) + lane / 16 of the tile, LDS slot lane % 16 receiving chunk
+    // slot ^ swizzle(row) of the kv head's row
+    const size_t rowB = size_t(a.nkvh) * kRowB; // bytes between consecutive keys
+    const char *cache[2] = {static_cast<const char *>(a.k), static_cast<const char *>(a.v)};
+    int lrow[kPer];
+    size_t loff[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int q = wave + W * j;
+        const int row = 4 * (q % 16) + lane / 16, slot = lane % 16;
+        const int chunk = slot ^ (q < 16 ? swzK(row) : swzV(row));
+        lrow[j] = row;
+        loff[j] = size_t(g) * kRowB + size_t(chunk) * 16;
+    }
+    const auto issue = [&](size_t t0, int stage) {
+        char *dst = &lds_all[half][stage][0];
+        const size_t left = a.total - t0; // keys of the cache from t0 on (> 0)
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int q = wave + W * j;
+            if (q >= kLoads) break;
+            const size_t key = size_t(lrow[j]) < left ? t0 + size_t(lrow[j]) : 0;
+            __builtin_amdgcn_global_load_lds(
+                (const void __attribute__((address_space(1))) *)(cache[q / 16] + key * rowB + loff[j]),
+                (void __attribute__((address_space(3))) *)(dst + q * 1024), 16, 0, 0);
+        }
+    };
+
+    const size_t nsteps = kSplit ? (ntiles + 1) / 2 : ntiles;
+    const size_t tbeg = half ? nsteps : 0;
+    const size_t tcount = half ? ntiles - nsteps : nsteps;
+    if (tcount > 0) issue(tbeg * kMfmaKT, 0);
+    for (size_t it = 0; it < nsteps; ++it) {
+        const int buf = int(it & 1);
+        const size_t kt0 = (tbeg + it) * kMfmaKT;
+        waitVmcnt<0>(); // this wave's loads of tile it have landed
+        ldsBarrier();   // every wave's have; every wave is past the step that read the other stage
+        if (it + 1 < tcount) issue(kt0 + kMfmaKT, buf ^ 1);
+        if (kSplit && it >= tcount) continue;
+        const char *kt = &lds_all[half][buf][0], *vt = kt + kTileB;
+        const bool whole = kt0 + kMfmaKT <= vis_first;
+        const int nvis = int(min(vis_q - min(vis_q, kt0), size_t(kMfmaKT)));
+        float p[4][4];
+        float mx = m;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int krow = 32 * (t / 2) + 8 * (n / 4) + 4 * (t % 2) + n % 4; // A row n
+            const char *kr = kt + krow * kRowB;
+            const int sw = swzK(krow);
+            f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) {
+                const v4u kv = *reinterpret_cast<const v4u *>(kr + 16 * ((4 * kb + g4) ^ sw));
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(kv), qreg[kb], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[t][i] = acc[i];
+        }
+        if (!whole) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int off = 32 * (t / 2) + 8 * g4 + 4 * (t % 2) + i;
+                    p[t][i] = off < nvis ? p[t][i] : -INFINITY;
+                }
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, p[t][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+        const float mc = mx == -INFINITY ? 0.0f : mx * c2;
+        float ps = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                p[t][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(p[t][i], c2, -mc));
+                ps += p[t][i];
+            }
+        if (__builtin_expect(__any(mx != m), 0)) {
+            const float corr = mx == m ? 1.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m, c2, -mc));
+            lsum *= corr;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) o[dt] *= corr;
+        }
+        m = mx;
+        lsum += ps;
+        // the transposing reads' rows and column offset: keys 32 p2 + 8 g + n / 4 (and + 4),
+        // columns 16 dt + 4 (n % 4) .. + 3, i.e. half n % 2 of chunk 2 dt + (n % 4) / 2
+#pragma unroll
+        for (int p2 = 0; p2 < 2; ++p2) {
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float x0 = p[2 * p2 + w / 2][2 * (w % 2)], x1 = p[2 * p2 + w / 2][2 * (w % 2) + 1];
+                hw[w] = Bf16Cvt::narrow2Q(x0, x1);
+                lw[w] = Bf16Cvt::narrow2Q(x0 - __uint_as_float(hw[w] << 16), x1 - __uint_as_float(hw[w] & 0xFFFF0000u));
+            }
+            const bf16x8 bhi = asBf16x8(v4u{hw[0], hw[1], hw[2], hw[3]});
+            const bf16x8 blo = asBf16x8(v4u{lw[0], lw[1], lw[2], lw[3]});
+            const int r0 = 32 * p2 + 8 * g4 + n / 4;
+            const char *v0 = vt + r0 * kRowB + 8 * (n % 2), *v1 = v0 + 4 * kRowB;
+            const int sw = swzV(r0); // rows r0 and r0 + 4 share it
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const int cofs = 16 * ((2 * dt + (n % 4) / 2) ^ sw);
+                const uint64_t e0 = ldsReadTr16(v0 + cofs), e1 = ldsReadTr16(v1 + cofs);
+                const v4u vv = v4u{uint32_t(e0), uint32_t(e0 >> 32), uint32_t(e1), uint32_t(e1 >> 32)};
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vv), bhi, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vv), blo, o[dt], 0, 0, 0);
+            }
+        }
+    }
+    float lt = lsum + __shfl_xor(lsum, 16, kWave);
+    lt += __shfl_xor(lt, 32, kWave);
+    if constexpr (kSplit) {
+        float *xch = reinterpret_cast<float *>(&lds_all[0][0][0]) + size_t(wave) * kWave * (2 + 4 * DT);
+        __syncthreads();
+        if (half == 1) {
+            xch[lane] = m;
+            xch[kWave + lane] = lt;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xch[(2 + 4 * dt + i) * kWave + lane] = o[dt][i];
+        }
+        __syncthreads();
+        if (half == 1) return;
+        const float m1 = xch[lane], l1 = xch[kWave + lane];
+        const float M = fmaxf(m, m1);
+        const float f0 = m == M ? 1.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m, c2, -M * c2));
+        const float f1 = m1 == M ? 1.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(m1, c2, -M * c2));
+        lt = lt * f0 + l1 * f1;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[dt][i] = o[dt][i] * f0 + xch[(2 + 4 * dt + i) * kWave + lane] * f1;
+    }
+    if (q0 + size_t(n) >= a.seq) return;
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    uint16_t *op = static_cast<uint16_t *>(a.out) + (qi * a.nh + h) * D + 4 * g4;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+        const uint32_t w0 = f32ToBf16(o[dt][0] * inv) | (f32ToBf16(o[dt][1] * inv) << 16);
+        const uint32_t w1 = f32ToBf16(o[dt][2] * inv) | (f32ToBf16(o[dt][3] * inv) << 16);
+        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<v2u *>(op + 16 * dt) = v2u{w0, w1};
+    }
+}
+
 // ---- decode on MFMA (bf16 q / out, head_dim 128, cache in bf16 or INT8) ---------------
 // Few queries, long cache.  Block = (query, kv head, key chunk), 4 waves; each wave takes
 // 32-key steps of the chunk on its own.  The MFMA columns are the G (<= 16) q heads of the
@@ -994,6 +1213,24 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
             // few blocks per CU: the causal imbalance is not averaged out across blocks, so
             // the key tiles of each block are split over two wave sets
             // (groups of 8 keep one wave per head: 16 waves of 8 heads would spill registers)
+            if constexpr (!kInt8) {
+                // bf16 cache: the tiles go HBM -> LDS directly (attnMfmaLds)
+                if (mblocks <= 512 && G <= 6) {
+                    switch (G) {
+                    case 6: attnMfmaLds<6, true><<<unsigned(mblocks), kWave * 12, 0, s>>>(a); return;
+                    case 4: attnMfmaLds<4, true><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
+                    case 2: attnMfmaLds<2, true><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
+                    default: attnMfmaLds<1, true><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
+                    }
+                }
+                switch (G) {
+                case 8: attnMfmaLds<8, false><<<unsigned(mblocks), kWave * 8, 0, s>>>(a); return;
+                case 6: attnMfmaLds<6, false><<<unsigned(mblocks), kWave * 6, 0, s>>>(a); return;
+                case 4: attnMfmaLds<4, false><<<unsigned(mblocks), kWave * 4, 0, s>>>(a); return;
+                case 2: attnMfmaLds<2, false><<<unsigned(mblocks), kWave * 2, 0, s>>>(a); return;
+                default: attnMfmaLds<1, false><<<unsigned(mblocks), kWave, 0, s>>>(a); return;
+                }
+            }
             if (mblocks <= 512 && G <= 6) {
                 switch (G) {
                 case 6: attnMfma<6, true, kInt8><<<unsigned(mblocks), kWave * 12, 0, s>>>(a); return;

@@ -221,6 +221,13 @@ __device__ __forceinline__ V waveGroupReduce(V v) {
 // counts stores too) -- that would drain loads issued ahead of the barrier to overlap it.
 __device__ __forceinline__ void ldsBarrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Wait until at most VM of this wave's vector-memory loads are outstanding.
+template <int VM>
+__device__ __forceinline__ void waitVmcnt() {
+    // s_waitcnt fields: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8] (15: no wait)
+    __builtin_amdgcn_s_waitcnt((VM & 0xF) | (0x7 << 4) | (0xF << 8) | ((VM >> 4) << 14));
+}
+
 template <int G, typename Op, typename V>
 __device__ __forceinline__ V groupReduce(V v, V *red) {
     v = waveGroupReduce<(G < kWave ? G : kWave), Op>(v);

@@ -245,12 +245,6 @@ __global__ void __launch_bounds__(NWW * NWX * 64)
 // c ^ ((r >> 1) & 7), and the MFMA-operand reads apply the same XOR (bank-conflict-free,
 // measured).  Waits count this wave's loads (vmcnt) and one LDS-only barrier per stage
 // makes every wave's loads visible and frees the stage read two steps ago.
-template <int VM>
-__device__ __forceinline__ void waitVmcnt() {
-    // s_waitcnt fields: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8] (15: no wait)
-    __builtin_amdgcn_s_waitcnt((VM & 0xF) | (0x7 << 4) | (0xF << 8) | ((VM >> 4) << 14));
-}
-
 template <typename T, int BW, int BX, int NWW, int NWX, int S>
 __global__ void __launch_bounds__(NWW * NWX * 64)
     linearDirect(LinearArgs a) {
