@@ -768,27 +768,31 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
     // slot ^ swizzle(row) of the kv head's row
     const size_t rowB = size_t(a.nkvh) * kRowB; // bytes between consecutive keys
     const char *cache[2] = {static_cast<const char *>(a.k), static_cast<const char *>(a.v)};
+    // (byte offsets within a tile fit 32 bits: the launcher checks 64 rows * rowB < 2^31)
     int lrow[kPer];
-    size_t loff[kPer];
+    uint32_t loff[kPer], lcol[kPer];
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
         const int q = wave + W * j;
         const int row = 4 * (q % 16) + lane / 16, slot = lane % 16;
         const int chunk = slot ^ (q < 16 ? swzK(row) : swzV(row));
         lrow[j] = row;
-        loff[j] = size_t(g) * kRowB + size_t(chunk) * 16;
+        lcol[j] = uint32_t(g * kRowB + chunk * 16);
+        loff[j] = uint32_t(row) * uint32_t(rowB) + lcol[j];
     }
     const auto issue = [&](size_t t0, int stage) {
         char *dst = &lds_all[half][stage][0];
         const size_t left = a.total - t0; // keys of the cache from t0 on (> 0)
+        const bool full = left >= size_t(kMfmaKT);
 #pragma unroll
         for (int j = 0; j < kPer; ++j) {
             const int q = wave + W * j;
             if (q >= kLoads) break;
-            const size_t key = size_t(lrow[j]) < left ? t0 + size_t(lrow[j]) : 0;
-            __builtin_amdgcn_global_load_lds(
-                (const void __attribute__((address_space(1))) *)(cache[q / 16] + key * rowB + loff[j]),
-                (void __attribute__((address_space(3))) *)(dst + q * 1024), 16, 0, 0);
+            // the tile's rows from the tile base; in the cache's last tile, rows past it read row 0
+            const char *src = full || size_t(lrow[j]) < left ? cache[q / 16] + t0 * rowB + loff[j]
+                                                            : cache[q / 16] + lcol[j];
+            __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *)(src),
+                                             (void __attribute__((address_space(3))) *)(dst + q * 1024), 16, 0, 0);
         }
     };
 
@@ -1212,9 +1216,10 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
             }
             // few blocks per CU: the causal imbalance is not averaged out across blocks, so
             // the key tiles of each block are split over two wave sets
-            // (groups of 8 keep one wave per head: 16 waves of 8 heads would spill registers)
-            if constexpr (!kInt8) {
-                // bf16 cache: the tiles go HBM -> LDS directly (attnMfmaLds)
+            // (groups of 8 keep one wave per head: 16 waves of 8 heads would spill registers).
+            // A bf16 cache's tiles go HBM -> LDS directly (attnMfmaLds; its byte offsets
+            // within a tile take 32 bits, so beyond 2^17 kv heads the register-staged kernel).
+            if (!kInt8 && size_t(a.nkvh) * 256 * kMfmaKT < (size_t(1) << 31)) {
                 if (mblocks <= 512 && G <= 6) {
                     switch (G) {
                     case 6: attnMfmaLds<6, true><<<unsigned(mblocks), kWave * 12, 0, s>>>(a); return;
