@@ -15,11 +15,13 @@
 // tests bound the difference by the f32 accumulation error of the reference itself.
 //
 // Design, three kernels (the launcher at the end picks one):
-//  - attnMfma (bf16, head_dim 128, >= 16 queries: prefill): MFMA-bound; 16 queries x one kv
-//    head's q heads per block, S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32_bf16
-//    with K / V tiles staged through LDS one tile ahead; with few blocks per CU, two wave
-//    sets per block split the key tiles (kSplit).  An INT8 cache whose bf16 form fits the
-//    workspace is dequantized once into it and attended as bf16 (the same operands).
+//  - attnMfmaLds / attnMfma (bf16, head_dim 128, >= 16 queries: prefill): MFMA-bound; 16
+//    queries x one kv head's q heads per block, S^T = K Q^T and O^T += V^T P^T on
+//    v_mfma_f32_16x16x32_bf16 with K / V tiles in LDS one tile ahead; with few blocks per CU,
+//    two wave sets per block split the key tiles (kSplit).  attnMfmaLds moves bf16 tiles
+//    HBM -> LDS directly; an INT8 cache whose bf16 form fits the workspace is dequantized
+//    once into it and attended by it as bf16 (the same operands), and attnMfma stages other
+//    INT8 caches through registers, converting the codes on the way.
 //  - attnDecodeMfma (bf16 q, head_dim 128, fewer queries: decode, cache in bf16 or INT8):
 //    HBM-bound; the key range is cut into chunks, one block per (query, kv head, chunk) with
 //    the kv head's q heads as the MFMA columns; attnCombine merges the chunk partials.
