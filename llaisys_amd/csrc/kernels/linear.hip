@@ -601,8 +601,13 @@ void launch(const LinearArgs &a, hipStream_t s) {
                 // 16-bit weights: 96 x 128 tiles (4 waves of 96 x 32, 4 stages) when 128 x 128
                 // tiles leave CUs idle in a single round and the narrower tiles still fit one:
                 // prefill 2048 x 8960 -> 1536 (192 vs 256 tiles) 73.9 -> 69.9 us, the same bits
+                // Grids of 512+ tiles: 4 waves of 64 x 64 and 2 stages (64 KB of LDS, two blocks
+                // per CU): prefill 2048 x 1536 -> 8960 85.2 -> 73.7 us, 4096 rows 166 -> 143 us
+                // (with one or two blocks per CU the 3-stage 8-wave form stays ahead)
                 if (!kInt8 && a.K % kTK == 0 && blocks(128, 128) < 256 && blocks(96, 128) <= 256)
                     linearDirect<T, 96, 128, 1, 4, 4><<<blocks(96, 128), 256, 0, s>>>(a);
+                else if (!kInt8 && a.K % kTK == 0 && blocks(128, 128) >= 512)
+                    linearDirect<T, 128, 128, 2, 2, 2><<<blocks(128, 128), 256, 0, s>>>(a);
                 else if (!kInt8 && a.K % kTK == 0)
                     linearDirect<T, 128, 128, 4, 2, 3><<<blocks(128, 128), 512, 0, s>>>(a);
                 else

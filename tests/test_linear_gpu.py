@@ -59,6 +59,8 @@ SHAPES = [
     (1, 1024, 33), (1, 3000, 77), (1, 16384, 3),
     # 192..255 tiles of 128 x 128: the 96 x 128 tile (full and ragged last channel tile)
     (2048, 64, 1536), (2048, 128, 1530),
+    # 512+ tiles of 128 x 128: 4-wave blocks, two stages (ragged row and channel tiles)
+    (1100, 64, 8200),
 ]
 
 
