@@ -924,24 +924,24 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
 }
 
 // ---- decode on MFMA (bf16 q / out, head_dim 128, cache in bf16 or INT8) ---------------
-// Few queries, long cache.  Block = (query, kv head, key chunk), 4 waves; each wave takes
+// Few queries, long cache.  Block = (query, kv head, key chunk), NW waves; each wave takes
 // 32-key steps of the chunk on its own.  The MFMA columns are the G (<= 16) q heads of the
 // kv head (columns past G hold zero queries and are never written): S^T = K Q^T over 2
 // tiles of 16 keys (row m of tile t is key 8(m / 4) + 4t + m % 4, so lane group g holds keys
 // 8g .. 8g + 7 and P^T is the B operand of one 32-key P V product as the lanes hold it),
-// then O^T += V^T P^T with V^T staged through the wave's own LDS slice (no block barrier
-// inside the loop).  K enters the A operand straight from memory: bf16 rows, or INT8 codes
-// turned into bf16(code * scale) (codesToBf16) with the step's scales shared by shuffles.  The waves merge in LDS; a split launch writes chunk partials in
-// the layout attnCombine merges (max in scaled units).
+// then O^T += V^T P^T with the V rows staged through the wave's own LDS slice and read
+// back transposed (no block barrier inside the loop).  K enters the A operand straight
+// from memory: bf16 rows, or INT8 codes turned into bf16(code * scale) (codesToBf16) with
+// the step's scales shared by shuffles.  The waves merge in LDS; a split launch writes
+// chunk partials in the layout attnCombine merges (max in scaled units).
 constexpr int kDecWaves = 4;
 constexpr int kDecKT = 32;   // keys per wave step
-constexpr int kDecVtLd = 40; // V^T row stride (bf16): 16-byte reads of rows 16 apart hit distinct banks
 
 template <bool kInt8, int NW>
 __global__ void __launch_bounds__(kWave * NW)
     attnDecodeMfma(AttnArgs a) {
     constexpr int D = 128, KB = D / 32, DT = D / 16;
-    __shared__ uint16_t vt[NW][D][kDecVtLd];
+    __shared__ __align__(16) char vrow[NW][kDecKT * 2 * D]; // the wave's V rows, chunks swizzled (swzV)
     __shared__ float st[NW][16][D + 2];
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
@@ -979,16 +979,14 @@ __global__ void __launch_bounds__(kWave * NW)
         // Loads are unconditional: a key past the step reads the step's first key and is
         // zeroed after the load (partial steps only).  Loads under per-lane branches were
         // issued one round trip at a time.
-        // V pieces: lane takes pairs (2kp, 2kp + 1) x 8 columns dc .. dc + 7, 4 per lane
-        v4u vr[4][2];
+        // V pieces: piece r of a lane is key 4r + lane / 16, columns 8 (lane % 16) .. + 7, so
+        // 16 lanes read one row contiguously
+        v4u vr[8];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int idx = lane + kWave * r, kp = idx % 16, dc = 8 * (idx / 16);
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const int key = 2 * kp + e < nk ? 2 * kp + e : 0;
-                vr[r][e] = loadRow8<kInt8>(a.v, (kt0 + key) * rstride + g, dc);
-            }
+        for (int r = 0; r < 8; ++r) {
+            const int kr = 4 * r + lane / 16;
+            const int key = kr < nk ? kr : 0;
+            vr[r] = loadRow8<kInt8>(a.v, (kt0 + key) * rstride + g, 8 * (lane % 16));
         }
         // K operands: tile t, row n -> key 8(n / 4) + 4t + n % 4
         v4u ka[2][KB];
@@ -1002,12 +1000,8 @@ __global__ void __launch_bounds__(kWave * NW)
         }
         if (part) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int kp = (lane + kWave * r) % 16;
-#pragma unroll
-                for (int e = 0; e < 2; ++e)
-                    if (2 * kp + e >= nk) vr[r][e] = v4u{0u, 0u, 0u, 0u};
-            }
+            for (int r = 0; r < 8; ++r)
+                if (4 * r + lane / 16 >= nk) vr[r] = v4u{0u, 0u, 0u, 0u};
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -1027,11 +1021,7 @@ __global__ void __launch_bounds__(kWave * NW)
                 for (int kb = 0; kb < KB; ++kb) ka[t][kb] = codesToBf16(ka[t][kb], sc);
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int kp = (lane + kWave * r) % 16;
-#pragma unroll
-                for (int e = 0; e < 2; ++e) vr[r][e] = codesToBf16(vr[r][e], __shfl(sreg, kDecKT + 2 * kp + e, kWave));
-            }
+            for (int r = 0; r < 8; ++r) vr[r] = codesToBf16(vr[r], __shfl(sreg, kDecKT + 4 * r + lane / 16, kWave));
         }
         float p[2][4];
         float mx = m;
@@ -1076,21 +1066,16 @@ __global__ void __launch_bounds__(kWave * NW)
         }
         m = mx;
         lsum += ps;
-        // V^T into this wave's slice (the previous step's reads of it are done: one wave,
-        // in order; the fences keep the compiler from moving accesses across)
+        // V rows into this wave's slice as loaded (the previous step's reads of it are done:
+        // one wave, in order; the fences keep the compiler from moving accesses across); 16
+        // lanes write one row's 16 chunks, whatever the swizzle: no bank conflicts
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int idx = lane + kWave * r, kp = idx % 16, dc = 8 * (idx / 16);
-            const uint32_t w0[4] = {vr[r][0].x, vr[r][0].y, vr[r][0].z, vr[r][0].w};
-            const uint32_t w1[4] = {vr[r][1].x, vr[r][1].y, vr[r][1].z, vr[r][1].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                *reinterpret_cast<uint32_t *>(&vt[wave][dc + 2 * e][2 * kp]) = __builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u);
-                *reinterpret_cast<uint32_t *>(&vt[wave][dc + 2 * e + 1][2 * kp]) = __builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u);
-            }
+        for (int r = 0; r < 8; ++r) {
+            const int kr = 4 * r + lane / 16;
+            *reinterpret_cast<v4u *>(&vrow[wave][kr * 2 * D + 16 * ((lane % 16) ^ swzV(kr))]) = vr[r];
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -1105,9 +1090,16 @@ __global__ void __launch_bounds__(kWave * NW)
         }
         const bf16x8 bhi = asBf16x8(v4u{hw[0], hw[1], hw[2], hw[3]});
         const bf16x8 blo = asBf16x8(v4u{lw[0], lw[1], lw[2], lw[3]});
+        // V^T operands by transposing reads: lane n of group g gets keys 8g .. 8g + 7 of column
+        // 16 dt + n from lanes reading key rows 8g + n / 4 (and + 4), columns 16 dt + 4 (n % 4) ..
+        const int r0 = 8 * g4 + n / 4;
+        const char *v0 = &vrow[wave][r0 * 2 * D + 8 * (n % 2)], *v1 = v0 + 4 * 2 * D;
+        const int vsw = swzV(r0); // rows r0 and r0 + 4 share it
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
-            const v4u vv = *reinterpret_cast<const v4u *>(&vt[wave][16 * dt + n][8 * g4]);
+            const int cofs = 16 * ((2 * dt + (n % 4) / 2) ^ vsw);
+            const uint64_t e0 = ldsReadTr16(v0 + cofs), e1 = ldsReadTr16(v1 + cofs);
+            const v4u vv = v4u{uint32_t(e0), uint32_t(e0 >> 32), uint32_t(e1), uint32_t(e1 >> 32)};
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vv), bhi, o[dt], 0, 0, 0);
             o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(asBf16x8(vv), blo, o[dt], 0, 0, 0);
         }
