@@ -934,7 +934,7 @@ __global__ void __launch_bounds__(kWave * W * (kSplit ? 2 : 1))
 // from memory: bf16 rows, or INT8 codes turned into bf16(code * scale) (codesToBf16) with
 // the step's scales shared by shuffles.  The waves merge in LDS; a split launch writes
 // chunk partials in the layout attnCombine merges (max in scaled units).
-constexpr int kDecWaves = 4;
+constexpr int kDecWaves = 2;
 constexpr int kDecKT = 32;   // keys per wave step
 
 template <bool kInt8, int NW>
@@ -1253,8 +1253,9 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
         if (d == 128 && a.total > 0 && a.seq < size_t(kMfmaQ) && a.group <= 16 && a.scale > 0.0f &&
             std::isfinite(a.scale)) {
             // waves per block: 8 for caches of 16K+ keys (half the partials to merge: 32K
-            // decode 14.6 -> 13.3 us INT8 KV, 14.4 -> 13.8 us bf16 KV), 4 below (more blocks for the
-            // shorter chains: the 4096-key decode step lost with 8)
+            // decode 14.6 -> 13.3 us INT8 KV, 14.4 -> 13.8 us bf16 KV), 2 below (more blocks
+            // for the shorter chains: the 4096-key decode step took 1.157 ms with 4, 1.122 ms
+            // with 2, 1.144 ms with 1; it lost with 8)
             const int nw = a.total >= 16384 ? 8 : kDecWaves;
             const size_t bk = size_t(nw) * kDecKT; // keys per block step
             const size_t pairs = a.seq * size_t(a.nh);
