@@ -2,35 +2,34 @@
 //
 // Semantics: reference src/ops/rope/cpu/rope_cpu.cpp:28-44.  For token i, head h and
 // j < d/2: freq_j = 1 / pow((double)theta, (double)(2.0f * j / d)), angle = (double)p_i *
-// freq_j, and the pair (x_j, x_{j+d/2}) is rotated in double precision; the result is
-// rounded double -> float -> element type.  freq_j is computed on the host with the same
-// libm pow the reference calls, so the angles are bit-identical; cos/sin come from
-// sincos.hpp (within an ulp of glibc's, which the final float rounding absorbs).  The
-// wave kernel of several instructions per token forms x*c +- p*s as one f64 product and
-// one f64 fma (the reference rounds both products); the double results differ by at most
-// an ulp, which the rounding to float absorbs except within 2^-29 of a float tie.  The
-// one-instruction wave kernel (kExact) and ropeVec round both products as the reference.
+// freq_j, and the pair (a, b) = (x_j, x_{j+d/2}) becomes (a*c - b*s, b*c + a*s) with both
+// products rounded in f64, then their sum, then the rounding double -> float -> element
+// type, in every kernel below.  freq_j is computed on the host with the same libm pow the
+// reference calls, so the angles are bit-identical; cos/sin come from sincos.hpp (within
+// an ulp of glibc's, which the final float rounding absorbs).
 //
-// Design: HBM-bound, no MFMA (no contraction).  Two kernels:
-//  * ropeWave (most shapes): 2^split_log2 wavefronts per token (each a contiguous share
-//    of the token's head-row instructions), no block barrier.  A wave issues the 16-byte
-//    loads of its rows, computes the token's d/2 (cos, sin) pairs (one per lane) into its
-//    own LDS slice while they are in flight, and each lane then keeps the pairs of its
-//    column in registers for every head row it rotates.
-//  * ropeVec (at most 1/8 of a wave's lanes per token, e.g. one 64-wide head): a 256-thread block owns a run of tokens,
-//    computes their pairs into LDS behind a block barrier and rotates items that read
-//    their pairs from LDS; it packs several tokens into a block, so lanes stay busy.
+// Design: HBM-bound, no MFMA (no contraction).  Three kernels:
+//  * ropeHalves (most shapes): each lane holds E consecutive elements of the first half
+//    of a head row and the same E of the second half -- whole rotation pairs, so no lane
+//    needs another lane's values.  A wave takes a contiguous share of one token's head
+//    rows, computes the token's d/2 (cos, sin) pairs (one per lane) into its own LDS slice
+//    while its loads are in flight, and keeps its lanes' E pairs in registers.
+//  * ropeVec (under a quarter of a wave's lanes per token, e.g. one 64-wide head): a
+//    256-thread block packs a run of tokens, computes their pairs into LDS behind a block
+//    barrier and rotates 16-byte items that fetch their partner with a cross-lane move.
+//  * ropeScalar: any other head_dim or alignment.
 // The trig is the ~40-instruction routine of sincos.hpp, the device library only on an
 // out-of-line rare path.  Loads and stores are non-temporal (read once, written once).
-// q and k of the same tokens go through one launch.
 //
-// Measured on MI355X (median of batched launches over >= 1 GiB of rotating sets): q+k of
-// Qwen2 at 8192 tokens 12.1 us with 2 waves per token (13.2 with one, 13.5 with ropeVec);
-// q alone 10.3 us; Llama-8B q+k at 16384 tokens 54.0 us with 4 waves per token (57.0
-// with one).  A copy kernel moving the same bytes takes 10.4 us (q+k); the rest is the
-// f64 rotation (two f32 -> f64 conversions, a multiply, an fma and the conversion back
-// per element) issuing behind the loads.  Tried and slower: a persistent double-buffered
-// block loop (18.7-25.8 us), 8 waves/SIMD by register cap (spills, 40 us).
+// Measured on MI355X (bf16, medians of graph-replayed launches over >= 1 GiB of rotating
+// sets, one box): Qwen2 q+k at 8192 tokens 11.38 us, against 11.36-11.47 us for a copy
+// kernel with the same access pattern and no arithmetic, and 11.77 us for the previous
+// layout (16-byte vectors, partner fetched by DPP: every element widened twice, 560 VALU
+// instructions per token against 370 here); q alone 10.26 us (copy 9.69-9.90); k alone
+// 4.17 us (copy 3.06; the token's sincos dominates a one-instruction token); Llama-8B q+k
+// at 16384 tokens 53.39 us.  f64 fma / mul / add and the f32 <-> f64 conversions issue at
+// the f32 fma rate on gfx950 (4.6-5.2 cycles per wave64 instruction, measured), so an
+// f32 rotation with an error-bound test would issue more, not fewer, instructions.
 #include "common.hpp"
 #include "launch.hpp"
 #include "rope_common.hpp"
@@ -144,85 +143,77 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// One wavefront per token, no block barrier.  Each lane computes one (cos, sin) pair (two
-// or more when d/2 > 64) of its token into the wave's own LDS slice, then reads
-// back the N (cos, sin) pairs of its vector column into registers and uses them for every
-// head row of the token: a row is kRowVec consecutive lanes, so a wave instruction covers
-// 64 / kRowVec rows (q rows first, then k rows) and the lane's column is the same in all
-// of them.  Rows are taken in passes of IPT wave instructions (kOnePass: one pass, laid
-// out as straight-line code).  Waves past the last token
-// redo the last token and store nothing, so no wave leaves before the loads (a branch
-// there would serialise the kernel-argument loads ahead of the first global load).
-template <typename T, int IPT, int VPH, bool kOnePass, bool kExact>
+// Half-pair layout.  Lane l of a group of RL = d / (2E) consecutive lanes holds elements
+// E*l .. E*l + E-1 of the first half of a head row and the same E of the second half
+// (chunks of E * element size bytes: 8 or 16 for bf16 / f16, 16 for f32).  Each of a row
+// instruction's two loads covers 64 / RL half-rows, RL * E elements contiguous per group
+// (128 B for bf16 at head_dim 128, the cache line).  One wavefront takes a token's rows
+// (tensor 0's, then tensor 1's) in 2^split_log2 contiguous shares, passes of IPT row
+// instructions each.  Waves past the last token redo the last token and store nothing, so
+// no wave leaves before the loads (a branch there would serialise the kernel-argument
+// loads ahead of the first global load).
+template <typename T, int IPT, int RL, bool kOnePass, int E>
 __global__ void __launch_bounds__(256)
-    ropeWave(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int passes, int split_log2,
-             FreqTable ft) {
-    using F = Fmt<T>;
-    constexpr int N = F::kVec;
-    constexpr int kRowVec = 2 * VPH;          // lanes per head row
-    constexpr int kRows = kWave / kRowVec;    // rows per wave instruction
-    constexpr int kHalf = VPH * N;
-    constexpr int kRowBytes = kRowVec * 16;
-    // (cos, sin) of angle j = jv * N + e sits in slot e * VPH + jv, and lane l computes the
-    // angle of slot l: both the write and every read instruction (same e, consecutive jv)
-    // touch consecutive 16-byte slots, with no LDS bank conflicts (slots N * 16 bytes apart
-    // had shown 4 % of the kernel's time in bank conflicts)
+    ropeHalves(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int passes, int split_log2,
+               FreqTable ft) {
+    using C = Chunk4<T, E>;
+    using V = typename C::V;
+    constexpr int kRows = kWave / RL;          // rows per wave instruction
+    constexpr int kHalf = RL * E;              // elements per half row
+    constexpr int kHalfBytes = kHalf * Fmt<T>::kBytes;
+    constexpr int kRowBytes = 2 * kHalfBytes;
     __shared__ double2 cs[256 / kWave][kHalf];
-    const auto angleOf = [](int slot) { return (slot % VPH) * N + slot / VPH; };
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
     const uint32_t gw = blockIdx.x * (256 / kWave) + uint32_t(wave);
     const uint32_t t0 = gw >> split_log2;
     const int first_instr = int(gw & ((1u << split_log2) - 1)) * passes * IPT;
-    const bool live = t0 < seq;                // waves past the end redo the last token
-    const size_t t = live ? t0 : seq - 1;      // and store nothing
+    const bool live = t0 < seq;
+    const size_t t = live ? t0 : seq - 1;
     const int nh0 = tp.n_heads0, rows = nh0 + tp.n_heads1;
-    const int rlane = lane / kRowVec, v_lane = lane % kRowVec;
-    const int jv = v_lane & (VPH - 1);
-    const bool lower = v_lane < VPH;
-    const char *in0 = static_cast<const char *>(tp.in0) + t * size_t(nh0) * kRowBytes + v_lane * 16;
-    const char *in1 = static_cast<const char *>(tp.in1) + t * size_t(tp.n_heads1) * kRowBytes + v_lane * 16 -
+    const int rlane = lane / RL, l = lane % RL;
+    const char *in0 = static_cast<const char *>(tp.in0) + t * size_t(nh0) * kRowBytes + l * C::kBytes;
+    const char *in1 = static_cast<const char *>(tp.in1) + t * size_t(tp.n_heads1) * kRowBytes + l * C::kBytes -
                       size_t(nh0) * kRowBytes;
-    char *out0 = static_cast<char *>(tp.out0) + t * size_t(nh0) * kRowBytes + v_lane * 16;
-    char *out1 = static_cast<char *>(tp.out1) + t * size_t(tp.n_heads1) * kRowBytes + v_lane * 16 -
+    char *out0 = static_cast<char *>(tp.out0) + t * size_t(nh0) * kRowBytes + l * C::kBytes;
+    char *out1 = static_cast<char *>(tp.out1) + t * size_t(tp.n_heads1) * kRowBytes + l * C::kBytes -
                  size_t(nh0) * kRowBytes;
 
-    // the lane's first frequency before the row loads: the vector memory counter drains in
-    // issue order, so a frequency read issued after them would hold the angle work until all
-    // the rows had landed
-    const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
+    // the lane's first frequency before the row loads (vector loads complete in issue order)
+    const double f_first = ft.f[lane < kHalf ? lane : 0];
     __builtin_amdgcn_sched_barrier(0);
-    double c[N], sn[N];
+    double c[E], sn[E];
     const int npass = kOnePass ? 1 : passes;
     for (int pass = 0; pass < npass; ++pass) {
-        v4u raw[IPT];
+        V xa[IPT], xb[IPT];
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
             const int r = (first_instr + pass * IPT + k) * kRows + rlane;
+            // rows past the token's last read its first q row (and store nothing)
             const char *src = (r < nh0 ? in0 : (r < rows ? in1 : in0 - size_t(r) * kRowBytes)) + size_t(r) * kRowBytes;
-            raw[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
+            xa[k] = C::load(src);
+            xb[k] = C::load(src + kHalfBytes);
         }
         if (pass == 0) {
             const int64_t p = pos[t];
             bool far = false;
-            for (int sl = lane; sl < kHalf; sl += kWave) {
-                const int j = angleOf(sl);
-                const double ang = double(p) * (sl == lane ? f_first : ft.f[j]);
+            for (int j = lane; j < kHalf; j += kWave) {
+                const double ang = double(p) * (j == lane ? f_first : ft.f[j]);
                 double s0 = 0.0, c0 = 0.0;
                 if (fabs(ang) <= kSincosFastLimit)
                     sincosReduced(ang, &s0, &c0);
                 else
                     far = true; // also NaN
-                cs[wave][sl] = make_double2(c0, s0);
+                cs[wave][j] = make_double2(c0, s0);
             }
             if (__builtin_expect(__any(far), 0)) {
-                for (int sl = lane; sl < kHalf; sl += kWave) {
-                    const double ang = double(p) * ft.f[angleOf(sl)];
+                for (int j = lane; j < kHalf; j += kWave) {
+                    const double ang = double(p) * ft.f[j];
                     if (!(fabs(ang) <= kSincosFastLimit)) {
                         double s0, c0;
                         librarySinCos(ang, &s0, &c0);
-                        cs[wave][sl] = make_double2(c0, s0);
+                        cs[wave][j] = make_double2(c0, s0);
                     }
                 }
             }
@@ -230,32 +221,26 @@ __global__ void __launch_bounds__(256)
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-            for (int e = 0; e < N; ++e) {
-                const double2 v = cs[wave][e * VPH + jv];
+            for (int e = 0; e < E; ++e) {
+                const double2 v = cs[wave][l * E + e];
                 c[e] = v.x;
-                sn[e] = lower ? -v.y : v.y; // first half: x*c - partner*s
+                sn[e] = v.y;
             }
         }
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
-            v4u other;
-            other.x = partnerOf<VPH>(raw[k].x);
-            other.y = partnerOf<VPH>(raw[k].y);
-            other.z = partnerOf<VPH>(raw[k].z);
-            other.w = partnerOf<VPH>(raw[k].w);
             const int r = (first_instr + pass * IPT + k) * kRows + rlane;
             if (live && r < rows) {
-                float x[N], q[N], y[N];
-                F::unpack(raw[k], x);
-                F::unpack(other, q);
-                if constexpr (kExact) { // the reference's two rounded products and their sum
+                char *dst = (r < nh0 ? out0 : out1) + size_t(r) * kRowBytes;
+                float a[E], b[E], ya[E], yb[E];
+                C::unpack(xa[k], a);
+                C::unpack(xb[k], b);
 #pragma unroll
-                    for (int e = 0; e < N; ++e) y[e] = float(double(x[e]) * c[e] + double(q[e]) * sn[e]);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < N; ++e) y[e] = float(fma(double(q[e]), sn[e], double(x[e]) * c[e]));
-                }
-                __builtin_nontemporal_store(F::packQ(y), reinterpret_cast<v4u *>((r < nh0 ? out0 : out1) + size_t(r) * kRowBytes));
+                for (int e = 0; e < E; ++e) rotatePair(a[e], b[e], c[e], sn[e], ya[e], yb[e]);
+                // packQ: arithmetic on the inputs and the host frequencies, no foreign NaN
+                // payload (a NaN theta takes the scalar kernel)
+                C::store(dst, C::packQ(ya));
+                C::store(dst + kHalfBytes, C::packQ(yb));
             }
         }
     }
@@ -284,51 +269,83 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-template <typename T, int IPT, bool kOnePass, bool kExact>
-void launchWaveVph(int vph, int passes, int split_log2, const RopePair &tp, const int64_t *pos,
-                   size_t seq, const FreqTable &ft, hipStream_t s) {
+template <typename T, int IPT, bool kOnePass, int E>
+void launchHalvesRl(int rl, int passes, int split_log2, const RopePair &tp, const int64_t *pos,
+                    size_t seq, const FreqTable &ft, hipStream_t s) {
     const unsigned grid = blocksFor(seq << split_log2, 256 / kWave);
-    switch (vph) {
-    case 2: ropeWave<T, IPT, 2, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 4: ropeWave<T, IPT, 4, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 8: ropeWave<T, IPT, 8, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 16: ropeWave<T, IPT, 16, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 32: ropeWave<T, IPT, 32, kOnePass, kExact><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    switch (rl) {
+    case 1: ropeHalves<T, IPT, 1, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 2: ropeHalves<T, IPT, 2, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 4: ropeHalves<T, IPT, 4, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 8: ropeHalves<T, IPT, 8, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 16: ropeHalves<T, IPT, 16, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 32: ropeHalves<T, IPT, 32, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
     default: break;
     }
 }
 
-template <typename T, int IPT>
-void launchWaveIpt(int vph, int passes, int split_log2, const RopePair &tp, const int64_t *pos,
+template <typename T, int E>
+void launchHalvesE(int rl, int instr, int split_log2, const RopePair &tp, const int64_t *pos,
                    size_t seq, const FreqTable &ft, hipStream_t s) {
-    if (passes == 1)
-        launchWaveVph<T, IPT, true, false>(vph, passes, split_log2, tp, pos, seq, ft, s);
-    else
-        launchWaveVph<T, IPT, false, false>(vph, passes, split_log2, tp, pos, seq, ft, s);
-}
-
-// `instr` wave instructions per token, taken in passes of at most 4 (registers).
-template <typename T>
-void launchWave(int vph, int instr, const RopePair &tp, const int64_t *pos, size_t seq,
-                const FreqTable &ft, hipStream_t s) {
-    // Waves per token: the fewest (a power of two, at least 2 from 3 instructions on) that
-    // leave each wave <= 3 row instructions.  Measured on MI355X, 16-byte items: q+k of
-    // Qwen2 at 8192 tokens (4 instructions) 12.1 us with 2 waves vs 13.2 with 1 and 13.3
-    // with 4; q alone (3) 10.3 vs 11.1 with 1; Llama-8B q+k at 16384 tokens (10) 54.0 with
-    // 4 vs 55.5 with 2 and 57.0 with 1.  More waves overlap one token's loads with
-    // another's rotation; each repeats the token's (cos, sin) work.
-    int split_log2 = instr >= 3 ? 1 : 0;
-    while ((instr + (1 << split_log2) - 1) >> split_log2 > 3) ++split_log2;
-    while (split_log2 > 0 && (seq << split_log2) >= (size_t(1) << 31)) --split_log2;
     const int split = 1 << split_log2;
     const int per_wave = (instr + split - 1) / split;
     const int passes = (per_wave + 3) / 4, ipt = (per_wave + passes - 1) / passes;
+    const auto go = [&](auto ipt_c) {
+        constexpr int I = decltype(ipt_c)::value;
+        if (passes == 1)
+            launchHalvesRl<T, I, true, E>(rl, passes, split_log2, tp, pos, seq, ft, s);
+        else
+            launchHalvesRl<T, I, false, E>(rl, passes, split_log2, tp, pos, seq, ft, s);
+    };
     switch (ipt) {
-    case 1: launchWaveIpt<T, 1>(vph, passes, split_log2, tp, pos, seq, ft, s); break;
-    case 2: launchWaveIpt<T, 2>(vph, passes, split_log2, tp, pos, seq, ft, s); break;
-    case 3: launchWaveIpt<T, 3>(vph, passes, split_log2, tp, pos, seq, ft, s); break;
-    default: launchWaveIpt<T, 4>(vph, passes, split_log2, tp, pos, seq, ft, s); break;
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    default: go(std::integral_constant<int, 4>{}); break;
     }
+}
+
+// The half-pair kernel when the shape fits it: head_dim / 2 <= 128 and a power-of-two
+// lane group of at most 32, chunk-aligned pointers, and at least a quarter of a wave's
+// lanes busy per token (fewer: ropeVec packs several tokens per block).  E = 8 (16-byte
+// chunks) for 16-bit types once the rows fill a row instruction, else E = 4.  Waves per
+// token: one for a single row instruction, else the fewest (at least two) that leave each
+// wave <= 2 instructions.  Measured on MI355X, bf16, 8192 tokens: q+k of Qwen2 (2
+// instructions at E = 8) 11.38 us with 2 waves against 12.05 with 1 and 14.07 with 4; q
+// alone 10.38 with 2 (10.26 at E = 4 with 1); k alone (1 instruction at E = 4) 4.17 with
+// 1 against 5.66 with 2; Llama-8B q+k at 16384 tokens (5 instructions) 53.39 with 4
+// against 54.17 with 2 and 56.65 with 1.
+template <typename T>
+bool launchHalves(const RopePair &tp, const int64_t *pos, size_t seq, size_t half,
+                  const FreqTable &ft, hipStream_t s) {
+    constexpr bool k16 = Fmt<T>::kBytes == 2;
+    const size_t rows = size_t(tp.n_heads0) + size_t(tp.n_heads1);
+    if (half % 4 != 0 || half > size_t(kMaxHalf) || rows == 0) return false;
+    const auto fits = [&](size_t e) {
+        const size_t rl = half / e;
+        if (rl == 0 || rl > 32 || (rl & (rl - 1)) != 0) return false;
+        const uintptr_t chunk = e * size_t(Fmt<T>::kBytes);
+        for (const void *p : {static_cast<const void *>(tp.out0), tp.in0, static_cast<const void *>(tp.out1), tp.in1})
+            if (p && (reinterpret_cast<uintptr_t>(p) % chunk) != 0) return false;
+        return true;
+    };
+    int e = 4;
+    if (k16 && half % 8 == 0 && fits(8) && rows >= size_t(kWave) / (half / 8)) e = 8;
+    if (e == 4 && !fits(4)) return false;
+    const int rl = int(half / size_t(e)), rpi = kWave / rl;
+    if (rows * size_t(rl) * 4 < size_t(kWave)) return false;
+    const size_t instr = (rows + size_t(rpi) - 1) / size_t(rpi);
+    if (instr > size_t(INT32_MAX / 2)) return false;
+    int split_log2 = instr >= 2 ? 1 : 0;
+    while ((instr + (size_t(1) << split_log2) - 1) >> split_log2 > 2) ++split_log2;
+    if (seq >= (size_t(1) << 31)) return false; // wave index is 32-bit
+    while (split_log2 > 0 && (seq << split_log2) >= (size_t(1) << 31)) --split_log2;
+    if (e == 8) {
+        if constexpr (k16) launchHalvesE<T, 8>(rl, int(instr), split_log2, tp, pos, seq, ft, s);
+    } else {
+        launchHalvesE<T, 4>(rl, int(instr), split_log2, tp, pos, seq, ft, s);
+    }
+    return true;
 }
 
 template <typename T, int IPT>
@@ -336,6 +353,7 @@ void launchIpt(int vph, const RopePair &tp, const int64_t *pos, size_t seq, size
                uint32_t magic0, uint32_t magic1, const FreqTable &ft, hipStream_t s) {
     const unsigned grid = blocksFor(seq, tpb);
     switch (vph) {
+    case 1: ropeVec<T, IPT, 1><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
     case 2: ropeVec<T, IPT, 2><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
     case 4: ropeVec<T, IPT, 4><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
     case 8: ropeVec<T, IPT, 8><<<grid, 256, 0, s>>>(tp, pos, seq, int(tpb), magic0, magic1, ft); break;
@@ -365,24 +383,6 @@ bool launchVec(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, con
         return heads ? uint32_t((uint64_t(1) << 32) / (size_t(heads) * 2 * vph) + 1) : 0u;
     };
     const uint32_t magic0 = magicOf(tp.n_heads0), magic1 = magicOf(tp.n_heads1);
-    // One wave per token when its instructions keep >= 3/4 of the lanes busy (q+k of Qwen2:
-    // 14 of 16 rows, q alone and Llama-8B q+k: all).  One token of one instruction with at
-    // least 1/4 of the lanes busy (k alone) also takes one wave, with the reference's two
-    // rounded products (the exact form of ropeVec); measured on MI355X, bf16, 8192 tokens:
-    // k [2 heads, 128] 6.02 -> 4.56 us, [1, 128] 4.68 -> 4.39 us, [2, 64] 5.20 -> 4.89 us,
-    // [4, 64] 4.96 -> 4.91 us; at 1/8 ([1, 64]) ropeVec's packed tokens win, 3.96 against
-    // 5.06 us.  Fewer rows per token pack several tokens per block with ropeVec.
-    const int rpi = int(kWave / (2 * vph));
-    const size_t rows = size_t(tp.n_heads0 + tp.n_heads1);
-    const int instr = int((rows + rpi - 1) / rpi);
-    if (rows * 4 >= size_t(instr) * rpi * 3) {
-        launchWave<T>(int(vph), instr, tp, pos, seq, ft, s);
-        return true;
-    }
-    if (instr == 1 && rows * 4 >= size_t(rpi)) {
-        launchWaveVph<T, 1, true, true>(int(vph), 1, 0, tp, pos, seq, ft, s);
-        return true;
-    }
     switch (ipt) {
     case 1: launchIpt<T, 1>(int(vph), tp, pos, seq, tpb, magic0, magic1, ft, s); break;
     case 2: launchIpt<T, 2>(int(vph), tp, pos, seq, tpb, magic0, magic1, ft, s); break;
@@ -408,7 +408,8 @@ void launch(const RopePair &tp, const int64_t *pos, size_t seq, size_t d, float 
     const FreqTable ft = hostFreqs(d, theta);
     // A NaN theta gives NaN frequencies carrying its payload, which the vector kernel's
     // packQ would not round like the reference; the scalar kernel rounds exactly.
-    if (!std::isnan(theta) && launchVec<T>(tp, pos, seq, d, ft, s)) return;
+    if (!std::isnan(theta) && (launchHalves<T>(tp, pos, seq, d / 2, ft, s) || launchVec<T>(tp, pos, seq, d, ft, s)))
+        return;
     launchScalar<T>(tp.out0, tp.in0, pos, seq, size_t(tp.n_heads0), d, theta, ft, s);
     if (tp.n_heads1) launchScalar<T>(tp.out1, tp.in1, pos, seq, size_t(tp.n_heads1), d, theta, ft, s);
 }

@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstddef>
+#include <type_traits>
 
 namespace llaisys::kernels::rope_detail {
 
@@ -125,6 +126,51 @@ __device__ __forceinline__ uint32_t partnerOf(uint32_t v) {
         return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
     else
         return uint32_t(__shfl_xor(int(v), VPH, kWave));
+}
+
+// A chunk: 4 consecutive elements of one half of a head row, the unit of the half-pair
+// layout (rope.hip's ropeHalves, rope_kv.hip): 8 bytes of bf16 / f16, 16 bytes of f32.
+template <typename T, int E = 4>
+struct Chunk4 {
+    using F = Fmt<T>;
+    static constexpr int kElems = E;
+    static constexpr int kBytes = E * F::kBytes;
+    static constexpr int kWords = kBytes / 4;
+    typedef uint32_t V __attribute__((ext_vector_type(kWords)));
+    __device__ static V load(const char *p) { return __builtin_nontemporal_load(reinterpret_cast<const V *>(p)); }
+    __device__ static void store(char *p, const V &v) { __builtin_nontemporal_store(v, reinterpret_cast<V *>(p)); }
+    __device__ static void unpack(const V &v, float *f) {
+        if constexpr (std::is_same_v<T, F32>) {
+#pragma unroll
+            for (int w = 0; w < kWords; ++w) f[w] = __uint_as_float(v[w]);
+        } else {
+            using Cvt = std::conditional_t<std::is_same_v<T, BF16>, Bf16Cvt, F16Cvt>;
+#pragma unroll
+            for (int w = 0; w < kWords; ++w) f[2 * w] = Cvt::widen(v[w] & 0xFFFFu), f[2 * w + 1] = Cvt::widen(v[w] >> 16);
+        }
+    }
+    __device__ static V packQ(const float *f) {
+        V v;
+        if constexpr (std::is_same_v<T, F32>) {
+#pragma unroll
+            for (int w = 0; w < kWords; ++w) v[w] = __float_as_uint(f[w]);
+        } else {
+            using Cvt = std::conditional_t<std::is_same_v<T, BF16>, Bf16Cvt, F16Cvt>;
+#pragma unroll
+            for (int w = 0; w < kWords; ++w) v[w] = Cvt::narrow2Q(f[2 * w], f[2 * w + 1]);
+        }
+        return v;
+    }
+};
+
+// The reference's rotation of one pair (rope_cpu.cpp:38-41): both products rounded in f64,
+// then their sum, then the rounding to float.  Compiled with -ffp-contract=off, so no
+// product is fused into the sum.
+__device__ __forceinline__ void rotatePair(float a, float b, double c, double s, float &out_a,
+                                           float &out_b) {
+    const double A = double(a), B = double(b);
+    out_a = float(A * c - B * s);
+    out_b = float(B * c + A * s);
 }
 
 inline FreqTable hostFreqs(size_t d, float theta) {

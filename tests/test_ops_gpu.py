@@ -186,6 +186,13 @@ ROPE = [
     ((33, 1, 128), 70, 1e4),
     ((40, 2, 64), 0, 1e6),
     ((41, 1, 64), 5, 1e4),
+    # half-pair layout at other widths: head_dim 256 (the widest), 16 (two-lane groups,
+    # eight rows fill a quarter wave), and 8 rows of 128 (16-byte chunks over one wave
+    # instruction); two 16-wide heads fall back to ropeVec
+    ((9, 3, 256), 11, 1e4),
+    ((13, 8, 16), 0, 1e4),
+    ((13, 2, 16), 0, 1e4),
+    ((19, 8, 128), 3, 1e4),
 ]
 
 
