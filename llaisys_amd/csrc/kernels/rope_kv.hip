@@ -8,23 +8,19 @@
 // quantize.hpp.  The codes therefore equal llaisysROPE followed by llaisysKVAppendInt8 bit
 // for bit; the rope'd k never goes to HBM in bf16.
 //
-// Design: one launch covers the q, k and v head rows of the tokens; one wavefront per token
-// (rope.hip's ropeWave layout: a head row on 2*VPH consecutive lanes, 16 bytes each, so
-// every wave instruction moves 1 KB of contiguous rows).  The wave computes its token's
-// f64 (cos, sin) pairs into its own LDS slice while the row loads are in flight; no block
-// barrier.  A k or v row's absmax is reduced across its lanes with DPP, then each lane
-// writes its 8 (bf16 / f16) or 4 (f32) codes, so the group stores the whole code row
-// contiguously.
+// Design: one launch covers the q, k and v head rows of the tokens in rope.hip's half-pair
+// layout: each lane holds E whole rotation pairs (E elements of each half of a head row),
+// so the rotation needs no cross-lane exchange and is the reference's two rounded f64
+// products and their sum for q and k alike -- q equals llaisysROPE's output and k's codes
+// are those of the reference's rope.  Each wave computes its token's f64 (cos, sin) pairs
+// into its own LDS slice while the row loads are in flight; no block barrier.  A k or v
+// row's absmax is reduced across its lanes with DPP / permlane butterflies, then each lane
+// writes the E codes of each half it holds.
 //
-// Bound (MI355X, Qwen2 shapes, 2048 tokens, 15.8 MB): 5.06 us against 3.92 us for a copy
-// kernel with the same traffic.  At 2048 tokens the launch has two waves per SIMD, and
-// the VALU issue of the exact f64 rotation (two f32 -> f64 conversions, two products, a
-// sum and the conversion back per element, which the bit-exact k codes need), the f64
-// sincos and the quantizer is only partly hidden behind the loads: rocprofv3 counted 600
-// VALU instructions per token-wave before the pure-q fast path and the one-pass layout
-// (5.43 -> 5.06 us).  Tried and slower: 2 or 4 waves per token (5.73 / 6.30 us; each
-// wave repeats the token's sincos), a block-per-2-tokens layout with block-wide
-// (cos, sin) staging (5.3-5.45 us).
+// Bound (MI355X, Qwen2 shapes, 2048 tokens, 15.8 MB): 4.58 us against 3.93 us for a copy
+// kernel with the same traffic.  At 2048 tokens the launch has four waves per SIMD and
+// every wave waits one HBM round trip before its VALU work (the f64 rotation, the f64
+// sincos, the quantizer) and then its stores.
 #include "common.hpp"
 #include "launch.hpp"
 #include "quantize.hpp"
@@ -54,54 +50,71 @@ struct RopeKvArgs {
     int nk; // k and v heads
 };
 
-// One wavefront per token (the layout of rope.hip's ropeWave): the token's head rows --
-// q rows, then k rows, then v rows, kRowVec lanes each -- are taken in passes of IPT wave
-// instructions.  Each lane computes one (cos, sin) pair of the token into the wave's own
-// LDS slice (no block barrier) while the row loads are in flight, then keeps its column's
-// pairs in registers.  Waves past the last token redo the last token and store nothing.
-// An instruction whose rows are all q rows (wave-uniform) takes a rotate-and-store path
-// with no quantizer work; kOnePass (all rows in one pass, e.g. Qwen2's 16 rows) lets the
-// compiler lay the whole token out as straight-line code.
-template <typename T, int IPT, int VPH, bool kOnePass>
+// Packed-magnitude maximum over one chunk (AbsBits's rule on 8 or 16 bytes).
+template <typename T, typename V>
+__device__ __forceinline__ uint32_t foldChunk(uint32_t m, const V &v) {
+    constexpr int W = sizeof(V) / 4;
+    if constexpr (std::is_same_v<T, F32>) {
+#pragma unroll
+        for (int w = 0; w < W; ++w) m = max(m, v[w] & 0x7FFFFFFFu);
+    } else {
+        v2u16 acc = __builtin_bit_cast(v2u16, m);
+#pragma unroll
+        for (int w = 0; w < W; ++w) acc = __builtin_elementwise_max(acc, __builtin_bit_cast(v2u16, v[w] & 0x7FFF7FFFu));
+        m = __builtin_bit_cast(uint32_t, acc);
+    }
+    return m;
+}
+
+// Half-pair layout (rope.hip's ropeHalves): lane l of a group of RL = d / (2E) lanes holds
+// elements E*l .. E*l + E-1 of both halves of a head row, i.e. E whole rotation pairs.  A
+// wavefront takes one token's rows -- q rows, then k rows, then v rows, 64 / RL per row
+// instruction -- in passes of IPT instructions, computes the token's (cos, sin) pairs (one
+// per lane) into its own LDS slice while the loads are in flight, and keeps its lanes' E
+// pairs in registers.  k and v rows: the row's absmax is a max over the RL lanes' packed
+// magnitudes (DPP / permlane butterflies), then each lane writes the E codes of each half
+// it holds.  An instruction whose rows are all q rows (wave-uniform) rotates and stores
+// only.  Waves past the last token redo the last token and store nothing.
+template <typename T, int IPT, int RL, bool kOnePass, int E>
 __global__ void __launch_bounds__(256)
-    ropeKvWave(RopeKvArgs a, const int64_t *__restrict__ pos, size_t seq, int passes, FreqTable ft) {
-    using F = Fmt<T>;
-    constexpr int N = F::kVec;
-    constexpr int kRowVec = 2 * VPH;       // lanes per head row
-    constexpr int kRows = kWave / kRowVec; // rows per wave instruction
-    constexpr int kHalf = VPH * N;
-    constexpr int kRowBytes = kRowVec * 16;
-    constexpr int kRowCodes = kRowVec * N; // head_dim
+    ropeKvHalves(RopeKvArgs a, const int64_t *__restrict__ pos, size_t seq, int passes, int split_log2,
+                 FreqTable ft) {
+    using C = Chunk4<T, E>;
+    using Vc = typename C::V;
+    constexpr int kRows = kWave / RL;          // rows per wave instruction
+    constexpr int kHalf = RL * E;              // elements per half row
+    constexpr int kHalfBytes = kHalf * Fmt<T>::kBytes;
+    constexpr int kRowBytes = 2 * kHalfBytes;
+    constexpr int kRowCodes = 2 * kHalf;       // head_dim
     __shared__ double2 cs[256 / kWave][kHalf];
-    const auto angleOf = [](int slot) { return (slot % VPH) * N + slot / VPH; };
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
-    const size_t t0 = size_t(blockIdx.x) * (256 / kWave) + size_t(wave);
+    const uint32_t gw = blockIdx.x * (256 / kWave) + uint32_t(wave);
+    const size_t t0 = gw >> split_log2;
+    const int first_instr = int(gw & ((1u << split_log2) - 1)) * passes * IPT;
     const bool live = t0 < seq;
     const size_t t = live ? t0 : seq - 1;
     const int nq = a.nq, nk = a.nk, rows = nq + 2 * nk;
-    const int rlane = lane / kRowVec, v_lane = lane % kRowVec;
-    const int jv = v_lane & (VPH - 1);
-    const bool lower = v_lane < VPH;
-    const char *q_in = static_cast<const char *>(a.q_in) + t * size_t(nq) * kRowBytes + v_lane * 16;
-    const char *k_in = static_cast<const char *>(a.k_in) + t * size_t(nk) * kRowBytes + v_lane * 16;
-    const char *v_in = static_cast<const char *>(a.v_in) + t * size_t(nk) * kRowBytes + v_lane * 16;
-    char *q_out = static_cast<char *>(a.q_out) + t * size_t(nq) * kRowBytes + v_lane * 16;
-    int8_t *k_codes = a.k_codes + t * size_t(nk) * kRowCodes + v_lane * N;
-    int8_t *v_codes = a.v_codes + t * size_t(nk) * kRowCodes + v_lane * N;
+    const int rlane = lane / RL, l = lane % RL;
+    const char *q_in = static_cast<const char *>(a.q_in) + t * size_t(nq) * kRowBytes + l * C::kBytes;
+    const char *k_in = static_cast<const char *>(a.k_in) + t * size_t(nk) * kRowBytes + l * C::kBytes;
+    const char *v_in = static_cast<const char *>(a.v_in) + t * size_t(nk) * kRowBytes + l * C::kBytes;
+    char *q_out = static_cast<char *>(a.q_out) + t * size_t(nq) * kRowBytes + l * C::kBytes;
+    int8_t *k_codes = a.k_codes + t * size_t(nk) * kRowCodes + l * E;
+    int8_t *v_codes = a.v_codes + t * size_t(nk) * kRowCodes + l * E;
     float *k_scale = a.k_scale + t * size_t(nk), *v_scale = a.v_scale + t * size_t(nk);
 
-    // the first frequency before the row loads (vector loads complete in issue order)
-    const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
+    // the lane's first frequency before the row loads (vector loads complete in issue order)
+    const double f_first = ft.f[lane < kHalf ? lane : 0];
     __builtin_amdgcn_sched_barrier(0);
-    double c[N], sn[N];
+    double c[E], sn[E];
     const int npass = kOnePass ? 1 : passes;
     for (int pass = 0; pass < npass; ++pass) {
-        v4u raw[IPT];
+        Vc xa[IPT], xb[IPT];
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
-            const int ins = pass * IPT + k; // wave-uniform
+            const int ins = first_instr + pass * IPT + k; // wave-uniform
             const int r = ins * kRows + rlane;
             const char *src;
             if ((ins + 1) * kRows <= nq) {
@@ -113,28 +126,28 @@ __global__ void __launch_bounds__(256)
                       : r < rows ? v_in + size_t(r - nq - nk) * kRowBytes
                                  : q_in;
             }
-            raw[k] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(src));
+            xa[k] = C::load(src);
+            xb[k] = C::load(src + kHalfBytes);
         }
         if (pass == 0) {
             const int64_t p = pos[t];
             bool far = false;
-            for (int sl = lane; sl < kHalf; sl += kWave) {
-                const int j = angleOf(sl);
-                const double ang = double(p) * (sl == lane ? f_first : ft.f[j]);
+            for (int j = lane; j < kHalf; j += kWave) {
+                const double ang = double(p) * (j == lane ? f_first : ft.f[j]);
                 double s0 = 0.0, c0 = 0.0;
                 if (fabs(ang) <= kSincosFastLimit)
                     sincosReduced(ang, &s0, &c0);
                 else
                     far = true; // also NaN
-                cs[wave][sl] = make_double2(c0, s0);
+                cs[wave][j] = make_double2(c0, s0);
             }
             if (__builtin_expect(__any(far), 0)) {
-                for (int sl = lane; sl < kHalf; sl += kWave) {
-                    const double ang = double(p) * ft.f[angleOf(sl)];
+                for (int j = lane; j < kHalf; j += kWave) {
+                    const double ang = double(p) * ft.f[j];
                     if (!(fabs(ang) <= kSincosFastLimit)) {
                         double s0, c0;
                         librarySinCos(ang, &s0, &c0);
-                        cs[wave][sl] = make_double2(c0, s0);
+                        cs[wave][j] = make_double2(c0, s0);
                     }
                 }
             }
@@ -142,127 +155,152 @@ __global__ void __launch_bounds__(256)
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-            for (int e = 0; e < N; ++e) {
-                const double2 v = cs[wave][e * VPH + jv];
+            for (int e = 0; e < E; ++e) {
+                const double2 v = cs[wave][l * E + e];
                 c[e] = v.x;
-                sn[e] = lower ? -v.y : v.y; // first half: x*c - partner*s
+                sn[e] = v.y;
             }
         }
 #pragma unroll
         for (int k = 0; k < IPT; ++k) {
-            v4u other;
-            other.x = partnerOf<VPH>(raw[k].x);
-            other.y = partnerOf<VPH>(raw[k].y);
-            other.z = partnerOf<VPH>(raw[k].z);
-            other.w = partnerOf<VPH>(raw[k].w);
-            const int ins = pass * IPT + k; // wave-uniform
+            const int ins = first_instr + pass * IPT + k; // wave-uniform
             const int r = ins * kRows + rlane;
             if ((ins + 1) * kRows <= nq) {
-                // every row of this instruction is a q row: rotation and store only, in
-                // ropeWave's form (rope.hip), so q equals llaisysROPE's
+                // every row of this instruction is a q row: rotate and store
                 if (!live) continue;
-                float x[N], q[N], y[N];
-                F::unpack(raw[k], x);
-                F::unpack(other, q);
+                float x0[E], x1[E], y0[E], y1[E];
+                C::unpack(xa[k], x0);
+                C::unpack(xb[k], x1);
 #pragma unroll
-                for (int e = 0; e < N; ++e) y[e] = float(fma(double(q[e]), sn[e], double(x[e]) * c[e]));
-                __builtin_nontemporal_store(F::packQ(y), reinterpret_cast<v4u *>(q_out + size_t(r) * kRowBytes));
+                for (int e = 0; e < E; ++e) rotatePair(x0[e], x1[e], c[e], sn[e], y0[e], y1[e]);
+                char *dst = q_out + size_t(r) * kRowBytes;
+                C::store(dst, C::packQ(y0));
+                C::store(dst + kHalfBytes, C::packQ(y1));
                 continue;
             }
             const int kind = r < nq ? 0 : (r < nq + nk ? 1 : (r < rows ? 2 : 3)); // 3: none
-            v4u out = raw[k];
+            Vc o0 = xa[k], o1 = xb[k];
             if (kind <= 1) {
-                float x[N], q[N], y[N];
-                F::unpack(raw[k], x);
-                F::unpack(other, q);
+                float x0[E], x1[E], y0[E], y1[E];
+                C::unpack(xa[k], x0);
+                C::unpack(xb[k], x1);
 #pragma unroll
-                // the reference's two rounded f64 products and their rounded sum
-                // (rope_cpu.cpp:40-41), so k's codes are those of the reference's rope
-                for (int e = 0; e < N; ++e) y[e] = float(double(x[e]) * c[e] + double(q[e]) * sn[e]);
-                out = F::packQ(y); // the element-type value llaisysROPE would store
+                for (int e = 0; e < E; ++e) rotatePair(x0[e], x1[e], c[e], sn[e], y0[e], y1[e]);
+                o0 = C::packQ(y0); // the element-type values llaisysROPE would store
+                o1 = C::packQ(y1);
             }
-            // k / v rows: quantizer input is the stored element values of the row; amax as
-            // in quant.hip (integer max of magnitude bits, float rule for a row with a NaN)
+            // k / v rows: the quantizer's input is the row's stored element values; amax as
+            // in quant.hip (integer max of magnitude bits, the float rule for a row with a NaN)
             using A = AbsBits<T>;
-            uint32_t bits = kind == 1 || kind == 2 ? A::finish(A::fold(0u, out)) : 0u;
-            bits = waveGroupReduce<kRowVec, MaxU32Op>(bits);
-            float val[N];
-            F::unpack(out, val);
+            uint32_t bits = kind == 1 || kind == 2 ? A::finish(foldChunk<T>(foldChunk<T>(0u, o0), o1)) : 0u;
+            bits = waveGroupReduce<RL, MaxU32Op>(bits);
+            float v0[E], v1[E];
+            C::unpack(o0, v0);
+            C::unpack(o1, v1);
             float amax = A::value(bits);
             if (__builtin_expect(bits > A::kInf, 0)) { // uniform over the row's lanes
                 amax = 0.0f;
 #pragma unroll
-                for (int e = 0; e < N; ++e) amax = MaxOp::apply(amax, fabsf(val[e]));
-#pragma unroll
-                for (int m = kRowVec / 2; m > 0; m >>= 1) amax = MaxOp::apply(amax, __shfl_xor(amax, m, kWave));
+                for (int e = 0; e < E; ++e) amax = MaxOp::apply(MaxOp::apply(amax, fabsf(v0[e])), fabsf(v1[e]));
+                amax = waveGroupReduce<RL, MaxOp>(amax);
             }
             if (!live || kind == 3) continue;
             if (kind == 0) {
-                __builtin_nontemporal_store(out, reinterpret_cast<v4u *>(q_out + size_t(r) * kRowBytes));
+                char *dst = q_out + size_t(r) * kRowBytes;
+                C::store(dst, o0);
+                C::store(dst + kHalfBytes, o1);
             } else {
                 const int hr = kind == 1 ? r - nq : r - nq - nk; // head row within k / v
                 const RowQuantizer qz(amax);
-                uint32_t cd[N];
-                qz.codes<N, std::is_same_v<T, F32>>(val, cd);
-                storeCodes<N>(kind == 1 ? k_codes : v_codes, size_t(hr) * kRowCodes, cd);
-                if (v_lane == 0) (kind == 1 ? k_scale : v_scale)[hr] = qz.scale;
+                uint32_t cd0[E], cd1[E];
+                qz.codes<E, std::is_same_v<T, F32>>(v0, cd0);
+                qz.codes<E, std::is_same_v<T, F32>>(v1, cd1);
+                int8_t *dst = (kind == 1 ? k_codes : v_codes) + size_t(hr) * kRowCodes;
+                storeCodes<E>(dst, 0, cd0);
+                storeCodes<E>(dst, kHalf, cd1);
+                if (l == 0) (kind == 1 ? k_scale : v_scale)[hr] = qz.scale;
             }
         }
     }
 }
 
-template <typename T, int IPT, bool kOnePass>
-void launchKvWaveIpt(int vph, int passes, const RopeKvArgs &a, const int64_t *pos, size_t seq,
-                     const FreqTable &ft, hipStream_t s) {
-    const unsigned grid = blocksFor(seq, 256 / kWave);
-    switch (vph) {
-    case 2: ropeKvWave<T, IPT, 2, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
-    case 4: ropeKvWave<T, IPT, 4, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
-    case 8: ropeKvWave<T, IPT, 8, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
-    case 16: ropeKvWave<T, IPT, 16, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
-    case 32: ropeKvWave<T, IPT, 32, kOnePass><<<grid, 256, 0, s>>>(a, pos, seq, passes, ft); break;
+template <typename T, int IPT, bool kOnePass, int E>
+void launchKvHalvesRl(int rl, int passes, int split_log2, const RopeKvArgs &a, const int64_t *pos, size_t seq,
+                      const FreqTable &ft, hipStream_t s) {
+    const unsigned grid = blocksFor(seq << split_log2, 256 / kWave);
+    switch (rl) {
+    case 1: ropeKvHalves<T, IPT, 1, kOnePass, E><<<grid, 256, 0, s>>>(a, pos, seq, passes, split_log2, ft); break;
+    case 2: ropeKvHalves<T, IPT, 2, kOnePass, E><<<grid, 256, 0, s>>>(a, pos, seq, passes, split_log2, ft); break;
+    case 4: ropeKvHalves<T, IPT, 4, kOnePass, E><<<grid, 256, 0, s>>>(a, pos, seq, passes, split_log2, ft); break;
+    case 8: ropeKvHalves<T, IPT, 8, kOnePass, E><<<grid, 256, 0, s>>>(a, pos, seq, passes, split_log2, ft); break;
+    case 16: ropeKvHalves<T, IPT, 16, kOnePass, E><<<grid, 256, 0, s>>>(a, pos, seq, passes, split_log2, ft); break;
+    case 32: ropeKvHalves<T, IPT, 32, kOnePass, E><<<grid, 256, 0, s>>>(a, pos, seq, passes, split_log2, ft); break;
     default: break;
     }
 }
 
-template <typename T>
-void launchKvWave(int vph, const RopeKvArgs &a, const int64_t *pos, size_t seq, const FreqTable &ft,
-                  hipStream_t s) {
-    const int rows_per_instr = kWave / (2 * vph);
-    const int instr = (a.nq + 2 * a.nk + rows_per_instr - 1) / rows_per_instr;
-    const int passes = (instr + 3) / 4, ipt = (instr + passes - 1) / passes;
-    if (passes == 1) {
-        switch (ipt) {
-        case 1: launchKvWaveIpt<T, 1, true>(vph, passes, a, pos, seq, ft, s); break;
-        case 2: launchKvWaveIpt<T, 2, true>(vph, passes, a, pos, seq, ft, s); break;
-        case 3: launchKvWaveIpt<T, 3, true>(vph, passes, a, pos, seq, ft, s); break;
-        default: launchKvWaveIpt<T, 4, true>(vph, passes, a, pos, seq, ft, s); break;
-        }
-        return;
-    }
+template <typename T, int E>
+void launchKvHalvesE(int rl, int instr, int split_log2, const RopeKvArgs &a, const int64_t *pos, size_t seq,
+                     const FreqTable &ft, hipStream_t s) {
+    const int per_wave = (instr + (1 << split_log2) - 1) >> split_log2;
+    const int passes = (per_wave + 3) / 4, ipt = (per_wave + passes - 1) / passes;
+    const auto go = [&](auto ipt_c) {
+        constexpr int I = decltype(ipt_c)::value;
+        if (passes == 1)
+            launchKvHalvesRl<T, I, true, E>(rl, passes, split_log2, a, pos, seq, ft, s);
+        else
+            launchKvHalvesRl<T, I, false, E>(rl, passes, split_log2, a, pos, seq, ft, s);
+    };
     switch (ipt) {
-    case 1: launchKvWaveIpt<T, 1, false>(vph, passes, a, pos, seq, ft, s); break;
-    case 2: launchKvWaveIpt<T, 2, false>(vph, passes, a, pos, seq, ft, s); break;
-    case 3: launchKvWaveIpt<T, 3, false>(vph, passes, a, pos, seq, ft, s); break;
-    default: launchKvWaveIpt<T, 4, false>(vph, passes, a, pos, seq, ft, s); break;
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    default: go(std::integral_constant<int, 4>{}); break;
     }
+}
+
+// The half-pair kernel when the shape fits it (head_dim / 2 <= 128, a power-of-two lane
+// group of at most 32, chunk-aligned pointers); E = 8 for 16-bit types once the rows fill
+// a row instruction, else E = 4; two waves per token from two row instructions on, each
+// with half of them.  Measured on MI355X (bf16, graph-replayed medians over >= 1 GiB of
+// rotating sets): the config-4 layer, 2048 tokens of Qwen2 q / k / v (2 instructions at
+// E = 8), 4.58 us with 2 waves per token against 4.79 with 1, 4.68 at E = 4 with 1 and
+// 4.83 for the previous layout (16-byte vectors, partner by DPP); a variant whose first
+// wave per token computes the pairs for both, behind an LDS barrier, 5.09 us.  Llama-8B
+// heads at 2048 tokens 10.65 us against 11.42 with 1 and 12.27 before; one decode token
+// 2.34 against 2.80 and 2.89.
+template <typename T>
+bool launchKvHalves(const RopeKvArgs &a, const int64_t *pos, size_t seq, size_t half,
+                    const FreqTable &ft, hipStream_t s) {
+    constexpr bool k16 = Fmt<T>::kBytes == 2;
+    const size_t rows = size_t(a.nq) + 2 * size_t(a.nk);
+    if (half % 4 != 0 || half > size_t(kMaxHalf) || rows == 0 || seq >= (size_t(1) << 31)) return false;
+    const auto fits = [&](size_t e) {
+        const size_t rl = half / e;
+        if (rl == 0 || rl > 32 || (rl & (rl - 1)) != 0) return false;
+        const uintptr_t chunk = e * size_t(Fmt<T>::kBytes);
+        for (const void *p : {static_cast<const void *>(a.q_out), a.q_in, a.k_in, a.v_in})
+            if (reinterpret_cast<uintptr_t>(p) % chunk != 0) return false;
+        return reinterpret_cast<uintptr_t>(a.k_codes) % e == 0 && reinterpret_cast<uintptr_t>(a.v_codes) % e == 0;
+    };
+    int e = 4;
+    if (k16 && half % 8 == 0 && fits(8) && rows >= size_t(kWave) / (half / 8)) e = 8;
+    if (e == 4 && !fits(4)) return false;
+    const int rl = int(half / size_t(e)), rpi = kWave / rl;
+    const int instr = int((rows + size_t(rpi) - 1) / size_t(rpi));
+    const int split_log2 = instr >= 2 && seq < (size_t(1) << 30) ? 1 : 0;
+    if (e == 8) {
+        if constexpr (k16) launchKvHalvesE<T, 8>(rl, instr, split_log2, a, pos, seq, ft, s);
+    } else {
+        launchKvHalvesE<T, 4>(rl, instr, split_log2, a, pos, seq, ft, s);
+    }
+    return true;
 }
 
 template <typename T>
 bool launchKv(const RopeKvArgs &a, const int64_t *pos, size_t seq, size_t d, float theta,
               hipStream_t s) {
-    constexpr int N = Fmt<T>::kVec;
-    const size_t half = d / 2;
-    if (half % N != 0 || half > size_t(kMaxHalf)) return false;
-    const size_t vph = half / N;
-    if ((vph & (vph - 1)) || vph > 32) return false;
-    for (const void *p : {static_cast<const void *>(a.q_out), a.q_in, a.k_in, a.v_in})
-        if (!aligned16(p)) return false;
-    if (reinterpret_cast<uintptr_t>(a.k_codes) % N || reinterpret_cast<uintptr_t>(a.v_codes) % N)
-        return false;
-    if (a.nq + 2 * a.nk == 0) return false;
-    launchKvWave<T>(int(vph), a, pos, seq, hostFreqs(d, theta), s);
-    return true;
+    return launchKvHalves<T>(a, pos, seq, d / 2, hostFreqs(d, theta), s);
 }
 
 } // namespace
