@@ -864,6 +864,18 @@ def _cpu_model():
     return "unknown"
 
 
+def summary_of(per_op, chain, configs):
+    """Per-op fraction of peak (config 1), chain ms and tokens/s (config 4), config-3 fractions."""
+    out = {"config1_frac_peak": {k: v["frac_peak"] for k, v in per_op.items()},
+           "config1_us": {k: v["us"] for k, v in per_op.items()}}
+    if chain is not None:
+        out["chain_ms"] = chain["ms"]
+        out["chain_tokens_per_s"] = chain["tokens_per_s"]
+    if configs is not None and "config3" in configs:
+        out["config3_frac_peak"] = {k: v["frac_peak"] for k, v in configs["config3"].items()}
+    return out
+
+
 def copy_floors():
     """Copy-kernel floors of the ops' traffic (llaisys_amd/csrc/floors/floors.cpp, built next
     to libllaisys.so): us per launch of a plain streaming kernel moving each op's bytes, and
@@ -909,7 +921,9 @@ def main():
                     help="only the self-attention lines (profiling); prints their JSON")
     ap.add_argument("--chain-only", action="store_true", help="only the config-4 chain: --steps graph replays (profiling), then its timing as JSON")
     ap.add_argument("--no-linear", action="store_true", help="skip the linear and rearrange lines")
-    ap.add_argument("--no-decode", action="store_true", help="skip the decode-step chain")
+    ap.add_argument("--decode", action="store_true",
+                    help="also time the decode-step chain (model orchestration, off by default)")
+    ap.add_argument("--no-decode", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--decode-only", action="store_true",
                     help="only the decode-step chain; prints its JSON")
     ap.add_argument("--decode-eager", action="store_true",
@@ -1078,7 +1092,7 @@ def main():
     if not args.no_attention:
         attention = measure_attention(L, hip, stream, e0, e1, args.steps)
     decode = None
-    if not args.no_decode:
+    if args.decode and not args.no_decode:
         decode = measure_decode(L, hip, stream, e0, e1)
     linear = None
     if not args.no_linear:
@@ -1122,9 +1136,13 @@ def main():
         "frac_peak": round(value / PEAK_GBS, 4),
         "tokens_per_s": round(T / (ms_step * 1e-3)),
         "wall_s_timed": round(wall, 3),
-        "per_op": per_op, "chain": chain, "configs": configs, "attention": attention,
-        "linear": linear, "decode": decode, "roofline": roof,
-        "cpu_baseline": cpu,
+        "roofline": roof, "cpu_baseline": cpu,
+        "attention": attention, "linear": linear, "decode": decode,
+        "configs": configs,
+        # the detailed hot-path figures last, and a compact summary at the very end, so that
+        # a reader that keeps only the tail of the line still sees every per-op fraction
+        "per_op": per_op, "chain": chain,
+        "summary": summary_of(per_op, chain, configs),
     }
     print(json.dumps(line), flush=True)
 
