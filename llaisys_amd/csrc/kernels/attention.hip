@@ -1168,13 +1168,26 @@ void launchD(const AttnArgs &a, int G, size_t blocks, hipStream_t s) {
     }
 }
 
+// The vector kernels' shape and alignment condition.
+bool vecShape(const AttnArgs &a, int d, int dv, bool int8) {
+    const auto aligned = [](const void *p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; };
+    return d == dv && (d == 64 || d == 128) && aligned(a.q, 16) && aligned(a.out, 16) &&
+           (int8 ? aligned(a.k, 8) && aligned(a.v, 8) : aligned(a.k, 16) && aligned(a.v, 16));
+}
+
+// The bf16 prefill on MFMA: head_dim 128, 16 or more queries, a non-empty cache and a
+// positive finite scale (the kernel tracks the max of the raw dot products).
+bool prefillMfma(const AttnArgs &a, int d, int dv, bool int8, bool bf16) {
+    if (!bf16 || !vecShape(a, d, dv, int8)) return false;
+    const size_t mblocks = (a.seq + kMfmaQ - 1) / kMfmaQ * size_t(a.nkvh) * size_t(a.group / sliceOf(a.group));
+    return d == 128 && a.total > 0 && a.seq >= size_t(kMfmaQ) && mblocks < (size_t(1) << 31) &&
+           a.scale > 0.0f && std::isfinite(a.scale);
+}
+
 template <typename T, bool kInt8>
 void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s) {
     if (a.seq == 0 || a.nh == 0) return;
-    const auto aligned = [](const void *p, size_t n) { return (reinterpret_cast<uintptr_t>(p) % n) == 0; };
-    const bool vec = d == dv && (d == 64 || d == 128) &&
-                     aligned(a.q, 16) && aligned(a.out, 16) &&
-                     (kInt8 ? aligned(a.k, 8) && aligned(a.v, 8) : aligned(a.k, 16) && aligned(a.v, 16));
+    const bool vec = vecShape(a, d, dv, kInt8);
     if (!vec) {
         a.nchunks = 1;
         attnScalar<T, kInt8><<<unsigned(a.seq * size_t(a.nh)), kWave, size_t(dv) * sizeof(float), s>>>(a, d, dv);
@@ -1186,9 +1199,7 @@ void launch(AttnArgs a, int d, int dv, void *ws, size_t ws_bytes, hipStream_t s)
     // decode and the other types stay on the vector kernel
     if constexpr (std::is_same_v<T, BF16>) {
         const size_t mblocks = (a.seq + kMfmaQ - 1) / kMfmaQ * size_t(a.nkvh) * size_t(a.slices);
-        // (the MFMA kernel tracks the max of the raw dot products: valid for a positive scale)
-        if (d == 128 && a.total > 0 && a.seq >= size_t(kMfmaQ) && mblocks < (size_t(1) << 31) &&
-            a.scale > 0.0f && std::isfinite(a.scale)) {
+        if (prefillMfma(a, d, dv, kInt8, true)) {
             a.nchunks = 1;
             if constexpr (kInt8) {
                 // An INT8 cache whose bf16 form fits the workspace is dequantized once (both
@@ -1342,6 +1353,27 @@ void *noAllocScratch(int device, char *err, size_t err_len) {
         g_scratch_ptr[device] = ptr;
     }
     return g_scratch_ptr[device];
+}
+
+size_t selfAttentionInt8KVScratchBytes(const void *out, const void *q, const void *k, const void *v,
+                                       size_t seq, size_t total, size_t nh, size_t nkvh, size_t d,
+                                       size_t dv, float scale, llaisysDataType_t dt, size_t cap) {
+    AttnArgs a{};
+    a.out = const_cast<void *>(out);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.seq = seq;
+    a.total = total;
+    a.nh = int(nh);
+    a.nkvh = int(nkvh);
+    a.group = int(nh / nkvh);
+    a.scale = scale;
+    if (seq > 0 && nh > 0 && prefillMfma(a, int(d), int(dv), true, dt == LLAISYS_DTYPE_BF16)) {
+        const size_t cache = 2 * total * nkvh * d * sizeof(uint16_t);
+        return cache <= cap ? cache : 0;
+    }
+    return selfAttentionWorkspaceBytes(seq, nh, d);
 }
 
 size_t selfAttentionWorkspaceBytes(size_t seq, size_t nh, size_t head_dim) {

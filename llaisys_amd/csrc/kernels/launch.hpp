@@ -107,6 +107,13 @@ size_t selfAttentionWorkspaceBytes(size_t seq, size_t nh, size_t head_dim);
 // returns null and writes the reason to err.
 constexpr size_t kNoAllocScratchBytes = size_t(24) << 20;
 void *noAllocScratch(int device, char *err, size_t err_len);
+// Workspace bytes selfAttention over an INT8 cache uses for these arguments: the bf16
+// prefill (MFMA) path only needs room for the dequantized caches, 2 * total * nkvh * d bf16
+// (0 if that exceeds `cap`: the kernel then converts the codes itself, with the same bits);
+// every other path the split partials, selfAttentionWorkspaceBytes(seq, nh, d).
+size_t selfAttentionInt8KVScratchBytes(const void *out, const void *q, const void *k, const void *v,
+                                       size_t seq, size_t total, size_t nh, size_t nkvh, size_t d,
+                                       size_t dv, float scale, llaisysDataType_t dt, size_t cap);
 void selfAttention(void *out, const void *q, const void *k, const void *v, const float *k_scale,
                    const float *v_scale, size_t seq, size_t total, size_t nh, size_t nkvh,
                    size_t d, size_t dv, float scale, llaisysDataType_t dt, void *ws,

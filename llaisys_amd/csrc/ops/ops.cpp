@@ -416,16 +416,21 @@ void selfAttentionInt8KV(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor
                     reinterpret_cast<const float *>(v_scale->data()), scale);
 }
 
-// The same op with its split partials in the library's file-scope device scratch
-// (kernels::kNoAllocScratchBytes per GPU) instead of the workspace: nothing is allocated.
-// It launches exactly the kernels selfAttentionInt8KV launches (same chunking, so the same
-// bits), and rejects calls whose partials would not fit.  Calls on one GPU share the
-// scratch: overlapping calls (several threads or streams) race.
+// The same op with its workspace in the library's file-scope device scratch
+// (kernels::kNoAllocScratchBytes per GPU): nothing is allocated.  Decode and the vector
+// kernels put their split partials there with the chunking selfAttentionInt8KV uses (the
+// same bits), and calls whose partials would not fit are rejected.  A bf16 prefill on the
+// MFMA kernel dequantizes the caches into the scratch when they fit, else the kernel
+// converts the codes itself; either way the same operands in the same MFMA order, so the
+// same bits.  Calls on one GPU share the scratch: overlapping calls (several threads or
+// streams) race.
 void selfAttentionInt8KVNoAlloc(tensor_t attn_val, tensor_t q, tensor_t k_codes, tensor_t k_scale,
                                 tensor_t v_codes, tensor_t v_scale, float scale) {
     checkAttentionInt8KV(attn_val, q, k_codes, k_scale, v_codes, v_scale);
     const size_t seq = q->shape()[0], nh = q->shape()[1], d = q->shape()[2];
-    const size_t need = kernels::selfAttentionWorkspaceBytes(seq, nh, d);
+    const size_t need = kernels::selfAttentionInt8KVScratchBytes(
+        attn_val->data(), q->data(), k_codes->data(), v_codes->data(), seq, k_codes->shape()[0], nh,
+        k_codes->shape()[1], d, v_codes->shape()[2], scale, q->dtype(), kernels::kNoAllocScratchBytes);
     if (need > kernels::kNoAllocScratchBytes)
         LLAISYS_FAIL(std::invalid_argument,
                      "SelfAttentionInt8KVNoAlloc: the call needs " << need << " bytes of scratch, more than the "

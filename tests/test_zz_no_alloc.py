@@ -1,5 +1,6 @@
 """llaisysSelfAttentionInt8KVNoAlloc (the attention over the INT8 KV cache that allocates
-nothing: its split partials live in a fixed device scratch) against
+nothing: its split partials, or a prefill's dequantized caches, live in a fixed device
+scratch) against
 llaisysSelfAttentionInt8KV, the allocating entry point it mirrors: the same launches with the
 same chunking, so equal bit for bit.  Two calls in a row share the scratch; the second is
 smaller, so a stale partial of the first call would show.  Both outputs are also checked
@@ -41,6 +42,10 @@ def cache(rng, total, nkvh, d):
     # a speculative 3-token step (36 query-heads), then one token over 700 keys
     ((1, 32768, 12, 2, 128), (1, 5000, 12, 2, 128)),
     ((3, 4096, 12, 2, 128), (1, 700, 12, 2, 128)),
+    # bf16 prefills on the MFMA kernel: caches dequantized into the scratch (2048 tokens of
+    # Qwen2-1.5B, 2 MB), then a cache whose bf16 form exceeds the 24 MB scratch (the kernel
+    # converts the codes itself)
+    ((2048, 2048, 12, 2, 128), (16, 52000, 2, 2, 128)),
 ])
 def test_no_alloc_attention_equals_allocating_entry(first, second):
     rng = np.random.default_rng(41)
@@ -56,3 +61,4 @@ def test_no_alloc_attention_equals_allocating_entry(first, second):
         exp = oracle.self_attention(q, kd, vd, scale)
         assert_attention_close(out.numpy(), exp, vd, f"{(seq, total)} vs the oracle")
     assert L.take_device_error() == 0
+
