@@ -162,7 +162,11 @@ __global__ void __launch_bounds__(256)
     constexpr int kHalf = RL * E;              // elements per half row
     constexpr int kHalfBytes = kHalf * Fmt<T>::kBytes;
     constexpr int kRowBytes = 2 * kHalfBytes;
+    // (cos, sin) of angle j = E l + e sits in slot e * RL + l: lane l's read of its element e
+    // and the lanes' writes (slot = lane) both touch consecutive 16-byte slots, free of LDS
+    // bank conflicts (slots E * 16 bytes apart conflicted E-fold)
     __shared__ double2 cs[256 / kWave][kHalf];
+    const auto angleOf = [](int slot) { return (slot % RL) * E + slot / RL; };
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
@@ -181,7 +185,7 @@ __global__ void __launch_bounds__(256)
                  size_t(nh0) * kRowBytes;
 
     // the lane's first frequency before the row loads (vector loads complete in issue order)
-    const double f_first = ft.f[lane < kHalf ? lane : 0];
+    const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
     __builtin_amdgcn_sched_barrier(0);
     double c[E], sn[E];
     const int npass = kOnePass ? 1 : passes;
@@ -198,22 +202,22 @@ __global__ void __launch_bounds__(256)
         if (pass == 0) {
             const int64_t p = pos[t];
             bool far = false;
-            for (int j = lane; j < kHalf; j += kWave) {
-                const double ang = double(p) * (j == lane ? f_first : ft.f[j]);
+            for (int sl = lane; sl < kHalf; sl += kWave) {
+                const double ang = double(p) * (sl == lane ? f_first : ft.f[angleOf(sl)]);
                 double s0 = 0.0, c0 = 0.0;
                 if (fabs(ang) <= kSincosFastLimit)
                     sincosReduced(ang, &s0, &c0);
                 else
                     far = true; // also NaN
-                cs[wave][j] = make_double2(c0, s0);
+                cs[wave][sl] = make_double2(c0, s0);
             }
             if (__builtin_expect(__any(far), 0)) {
-                for (int j = lane; j < kHalf; j += kWave) {
-                    const double ang = double(p) * ft.f[j];
+                for (int sl = lane; sl < kHalf; sl += kWave) {
+                    const double ang = double(p) * ft.f[angleOf(sl)];
                     if (!(fabs(ang) <= kSincosFastLimit)) {
                         double s0, c0;
                         librarySinCos(ang, &s0, &c0);
-                        cs[wave][j] = make_double2(c0, s0);
+                        cs[wave][sl] = make_double2(c0, s0);
                     }
                 }
             }
@@ -222,7 +226,7 @@ __global__ void __launch_bounds__(256)
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                const double2 v = cs[wave][l * E + e];
+                const double2 v = cs[wave][e * RL + l];
                 c[e] = v.x;
                 sn[e] = v.y;
             }
