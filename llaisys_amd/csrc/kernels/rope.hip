@@ -152,10 +152,11 @@ __global__ void __launch_bounds__(256)
 // instructions each.  Waves past the last token redo the last token and store nothing, so
 // no wave leaves before the loads (a branch there would serialise the kernel-argument
 // loads ahead of the first global load).
-template <typename T, int IPT, int RL, bool kOnePass, int E>
+template <typename T, int IPT, int RL, bool kOnePass, int E, int TPW>
 __global__ void __launch_bounds__(256)
     ropeHalves(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int passes, int split_log2,
                FreqTable ft) {
+    static_assert(TPW == 1 || kOnePass, "several tokens per wave take their rows in one pass");
     using C = Chunk4<T, E>;
     using V = typename C::V;
     constexpr int kRows = kWave / RL;          // rows per wave instruction
@@ -165,86 +166,104 @@ __global__ void __launch_bounds__(256)
     // (cos, sin) of angle j = E l + e sits in slot e * RL + l: lane l's read of its element e
     // and the lanes' writes (slot = lane) both touch consecutive 16-byte slots, free of LDS
     // bank conflicts (slots E * 16 bytes apart conflicted E-fold)
-    __shared__ double2 cs[256 / kWave][kHalf];
+    __shared__ double2 cs[256 / kWave][TPW][kHalf];
     const auto angleOf = [](int slot) { return (slot % RL) * E + slot / RL; };
 
     const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
     const int lane = int(threadIdx.x) % kWave;
     const uint32_t gw = blockIdx.x * (256 / kWave) + uint32_t(wave);
-    const uint32_t t0 = gw >> split_log2;
+    const size_t tbase = size_t(gw >> split_log2) * TPW; // the wave's first token
     const int first_instr = int(gw & ((1u << split_log2) - 1)) * passes * IPT;
-    const bool live = t0 < seq;
-    const size_t t = live ? t0 : seq - 1;
     const int nh0 = tp.n_heads0, rows = nh0 + tp.n_heads1;
     const int rlane = lane / RL, l = lane % RL;
-    const char *in0 = static_cast<const char *>(tp.in0) + t * size_t(nh0) * kRowBytes + l * C::kBytes;
-    const char *in1 = static_cast<const char *>(tp.in1) + t * size_t(tp.n_heads1) * kRowBytes + l * C::kBytes -
-                      size_t(nh0) * kRowBytes;
-    char *out0 = static_cast<char *>(tp.out0) + t * size_t(nh0) * kRowBytes + l * C::kBytes;
-    char *out1 = static_cast<char *>(tp.out1) + t * size_t(tp.n_heads1) * kRowBytes + l * C::kBytes -
-                 size_t(nh0) * kRowBytes;
+    const size_t tok0 = size_t(nh0) * kRowBytes, tok1 = size_t(tp.n_heads1) * kRowBytes; // token strides
+    const char *in0 = static_cast<const char *>(tp.in0) + l * C::kBytes;
+    const char *in1 = static_cast<const char *>(tp.in1) + l * C::kBytes - size_t(nh0) * kRowBytes;
+    char *out0 = static_cast<char *>(tp.out0) + l * C::kBytes;
+    char *out1 = static_cast<char *>(tp.out1) + l * C::kBytes - size_t(nh0) * kRowBytes;
+    // tokens past the last redo the last token and store nothing
+    const auto tokenOf = [&](int tk) { return min(tbase + size_t(tk), seq - 1); };
 
-    // the lane's first frequency before the row loads (vector loads complete in issue order)
+    // the lane's first frequency before the row loads (vector loads complete in issue order);
+    // the wave's tokens share the frequencies
     const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
     __builtin_amdgcn_sched_barrier(0);
     double c[E], sn[E];
     const int npass = kOnePass ? 1 : passes;
     for (int pass = 0; pass < npass; ++pass) {
-        V xa[IPT], xb[IPT];
+        V xa[TPW][IPT], xb[TPW][IPT];
 #pragma unroll
-        for (int k = 0; k < IPT; ++k) {
-            const int r = (first_instr + pass * IPT + k) * kRows + rlane;
-            // rows past the token's last read its first q row (and store nothing)
-            const char *src = (r < nh0 ? in0 : (r < rows ? in1 : in0 - size_t(r) * kRowBytes)) + size_t(r) * kRowBytes;
-            xa[k] = C::load(src);
-            xb[k] = C::load(src + kHalfBytes);
+        for (int tk = 0; tk < TPW; ++tk) {
+            const size_t t = tokenOf(tk);
+#pragma unroll
+            for (int k = 0; k < IPT; ++k) {
+                const int r = (first_instr + pass * IPT + k) * kRows + rlane;
+                // rows past the token's last read its first q row (and store nothing)
+                const char *src = (r < nh0 ? in0 + t * tok0 : (r < rows ? in1 + t * tok1 : in0 + t * tok0 - size_t(r) * kRowBytes)) +
+                                  size_t(r) * kRowBytes;
+                xa[tk][k] = C::load(src);
+                xb[tk][k] = C::load(src + kHalfBytes);
+            }
         }
         if (pass == 0) {
-            const int64_t p = pos[t];
             bool far = false;
-            for (int sl = lane; sl < kHalf; sl += kWave) {
-                const double ang = double(p) * (sl == lane ? f_first : ft.f[angleOf(sl)]);
-                double s0 = 0.0, c0 = 0.0;
-                if (fabs(ang) <= kSincosFastLimit)
-                    sincosReduced(ang, &s0, &c0);
-                else
-                    far = true; // also NaN
-                cs[wave][sl] = make_double2(c0, s0);
+#pragma unroll
+            for (int tk = 0; tk < TPW; ++tk) {
+                const int64_t p = pos[tokenOf(tk)];
+                for (int sl = lane; sl < kHalf; sl += kWave) {
+                    const double ang = double(p) * (sl == lane ? f_first : ft.f[angleOf(sl)]);
+                    double s0 = 0.0, c0 = 0.0;
+                    if (fabs(ang) <= kSincosFastLimit)
+                        sincosReduced(ang, &s0, &c0);
+                    else
+                        far = true; // also NaN
+                    cs[wave][tk][sl] = make_double2(c0, s0);
+                }
             }
             if (__builtin_expect(__any(far), 0)) {
-                for (int sl = lane; sl < kHalf; sl += kWave) {
-                    const double ang = double(p) * ft.f[angleOf(sl)];
-                    if (!(fabs(ang) <= kSincosFastLimit)) {
-                        double s0, c0;
-                        librarySinCos(ang, &s0, &c0);
-                        cs[wave][sl] = make_double2(c0, s0);
+                for (int tk = 0; tk < TPW; ++tk) {
+                    const int64_t p = pos[tokenOf(tk)];
+                    for (int sl = lane; sl < kHalf; sl += kWave) {
+                        const double ang = double(p) * ft.f[angleOf(sl)];
+                        if (!(fabs(ang) <= kSincosFastLimit)) {
+                            double s0, c0;
+                            librarySinCos(ang, &s0, &c0);
+                            cs[wave][tk][sl] = make_double2(c0, s0);
+                        }
                     }
                 }
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const double2 v = cs[wave][e * RL + l];
-                c[e] = v.x;
-                sn[e] = v.y;
-            }
         }
 #pragma unroll
-        for (int k = 0; k < IPT; ++k) {
-            const int r = (first_instr + pass * IPT + k) * kRows + rlane;
-            if (live && r < rows) {
-                char *dst = (r < nh0 ? out0 : out1) + size_t(r) * kRowBytes;
-                float a[E], b[E], ya[E], yb[E];
-                C::unpack(xa[k], a);
-                C::unpack(xb[k], b);
+        for (int tk = 0; tk < TPW; ++tk) {
+            if (TPW > 1 || pass == 0) {
 #pragma unroll
-                for (int e = 0; e < E; ++e) rotatePair(a[e], b[e], c[e], sn[e], ya[e], yb[e]);
-                // packQ: arithmetic on the inputs and the host frequencies, no foreign NaN
-                // payload (a NaN theta takes the scalar kernel)
-                C::store(dst, C::packQ(ya));
-                C::store(dst + kHalfBytes, C::packQ(yb));
+                for (int e = 0; e < E; ++e) {
+                    const double2 v = cs[wave][tk][e * RL + l];
+                    c[e] = v.x;
+                    sn[e] = v.y;
+                }
+            }
+            const size_t t = tokenOf(tk);
+            const bool live = tbase + size_t(tk) < seq;
+#pragma unroll
+            for (int k = 0; k < IPT; ++k) {
+                const int r = (first_instr + pass * IPT + k) * kRows + rlane;
+                if (live && r < rows) {
+                    char *dst = (r < nh0 ? out0 + t * tok0 : out1 + t * tok1) + size_t(r) * kRowBytes;
+                    float a[E], b[E], ya[E], yb[E];
+                    C::unpack(xa[tk][k], a);
+                    C::unpack(xb[tk][k], b);
+#pragma unroll
+                    for (int e = 0; e < E; ++e) rotatePair(a[e], b[e], c[e], sn[e], ya[e], yb[e]);
+                    // packQ: arithmetic on the inputs and the host frequencies, no foreign NaN
+                    // payload (a NaN theta takes the scalar kernel)
+                    C::store(dst, C::packQ(ya));
+                    C::store(dst + kHalfBytes, C::packQ(yb));
+                }
             }
         }
     }
@@ -273,33 +292,37 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-template <typename T, int IPT, bool kOnePass, int E>
+template <typename T, int IPT, bool kOnePass, int E, int TPW>
 void launchHalvesRl(int rl, int passes, int split_log2, const RopePair &tp, const int64_t *pos,
                     size_t seq, const FreqTable &ft, hipStream_t s) {
-    const unsigned grid = blocksFor(seq << split_log2, 256 / kWave);
+    const unsigned grid = blocksFor(((seq + TPW - 1) / TPW) << split_log2, 256 / kWave);
     switch (rl) {
-    case 1: ropeHalves<T, IPT, 1, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 2: ropeHalves<T, IPT, 2, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 4: ropeHalves<T, IPT, 4, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 8: ropeHalves<T, IPT, 8, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 16: ropeHalves<T, IPT, 16, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
-    case 32: ropeHalves<T, IPT, 32, kOnePass, E><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 1: ropeHalves<T, IPT, 1, kOnePass, E, TPW><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 2: ropeHalves<T, IPT, 2, kOnePass, E, TPW><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 4: ropeHalves<T, IPT, 4, kOnePass, E, TPW><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 8: ropeHalves<T, IPT, 8, kOnePass, E, TPW><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 16: ropeHalves<T, IPT, 16, kOnePass, E, TPW><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
+    case 32: ropeHalves<T, IPT, 32, kOnePass, E, TPW><<<grid, 256, 0, s>>>(tp, pos, seq, passes, split_log2, ft); break;
     default: break;
     }
 }
 
 template <typename T, int E>
-void launchHalvesE(int rl, int instr, int split_log2, const RopePair &tp, const int64_t *pos,
+void launchHalvesE(int rl, int instr, int split_log2, int tpw, const RopePair &tp, const int64_t *pos,
                    size_t seq, const FreqTable &ft, hipStream_t s) {
     const int split = 1 << split_log2;
     const int per_wave = (instr + split - 1) / split;
     const int passes = (per_wave + 3) / 4, ipt = (per_wave + passes - 1) / passes;
     const auto go = [&](auto ipt_c) {
         constexpr int I = decltype(ipt_c)::value;
-        if (passes == 1)
-            launchHalvesRl<T, I, true, E>(rl, passes, split_log2, tp, pos, seq, ft, s);
-        else
-            launchHalvesRl<T, I, false, E>(rl, passes, split_log2, tp, pos, seq, ft, s);
+        if (passes == 1) {
+            if (tpw == 4)
+                launchHalvesRl<T, I, true, E, 4>(rl, passes, split_log2, tp, pos, seq, ft, s);
+            else
+                launchHalvesRl<T, I, true, E, 1>(rl, passes, split_log2, tp, pos, seq, ft, s);
+        } else {
+            launchHalvesRl<T, I, false, E, 1>(rl, passes, split_log2, tp, pos, seq, ft, s);
+        }
     };
     switch (ipt) {
     case 1: go(std::integral_constant<int, 1>{}); break;
@@ -312,13 +335,19 @@ void launchHalvesE(int rl, int instr, int split_log2, const RopePair &tp, const 
 // The half-pair kernel when the shape fits it: head_dim / 2 <= 128 and a power-of-two
 // lane group of at most 32, chunk-aligned pointers, and at least a quarter of a wave's
 // lanes busy per token (fewer: ropeVec packs several tokens per block).  E = 8 (16-byte
-// chunks) for 16-bit types once the rows fill a row instruction, else E = 4.  Waves per
-// token: one for a single row instruction, else the fewest (at least two) that leave each
-// wave <= 2 instructions.  Measured on MI355X, bf16, 8192 tokens: q+k of Qwen2 (2
-// instructions at E = 8) 11.38 us with 2 waves against 12.05 with 1 and 14.07 with 4; q
-// alone 10.38 with 2 (10.26 at E = 4 with 1); k alone (1 instruction at E = 4) 4.17 with
-// 1 against 5.66 with 2; Llama-8B q+k at 16384 tokens (5 instructions) 53.39 with 4
-// against 54.17 with 2 and 56.65 with 1.
+// chunks) for 16-bit types once the rows fill a row instruction, else E = 4.  Tokens of 2
+// row instructions with >= 8192 tokens: 4 tokens per wave, one wave each; otherwise waves
+// per token: one for a single row instruction, else the fewest (at least two) that leave
+// each wave <= 2 instructions.  Measured on MI355X, bf16, graph-replayed medians over >= 1
+// GiB of rotating sets: q+k of Qwen2 at 8192 tokens (2 instructions at E = 8) 10.77 us
+// with 4 tokens per wave, against 11.38 with 2 waves per token, 12.05 with 1, 11.30 with
+// 8 tokens per wave and 11.47-11.57 for copy kernels of the same access pattern with 1-2
+// tokens per wave (10.50 with 4, 10.70 for the best plain copy); q alone 9.51-9.78 with 4
+// tokens per wave against 9.97-10.02; k alone (1 instruction at E = 4) 3.99 with one wave
+// per token against 4.54 with 4 tokens per wave and 5.66 with 2 waves per token; Llama-8B
+// q+k at 16384 tokens (5 instructions) 53.3-53.7 with 4 waves per token against 54.17 with
+// 2, 56.65 with 1 and 56.7 with 4 tokens per wave; the chain's 2048-token q+k 3.86 with 2
+// waves per token against 5.90 with 4 tokens per wave.
 template <typename T>
 bool launchHalves(const RopePair &tp, const int64_t *pos, size_t seq, size_t half,
                   const FreqTable &ft, hipStream_t s) {
@@ -340,14 +369,22 @@ bool launchHalves(const RopePair &tp, const int64_t *pos, size_t seq, size_t hal
     if (rows * size_t(rl) * 4 < size_t(kWave)) return false;
     const size_t instr = (rows + size_t(rpi) - 1) / size_t(rpi);
     if (instr > size_t(INT32_MAX / 2)) return false;
-    int split_log2 = instr >= 2 ? 1 : 0;
-    while ((instr + (size_t(1) << split_log2) - 1) >> split_log2 > 2) ++split_log2;
     if (seq >= (size_t(1) << 31)) return false; // wave index is 32-bit
-    while (split_log2 > 0 && (seq << split_log2) >= (size_t(1) << 31)) --split_log2;
-    if (e == 8) {
-        if constexpr (k16) launchHalvesE<T, 8>(rl, int(instr), split_log2, tp, pos, seq, ft, s);
+    // Four tokens per wave (16 loads of 16 bytes in flight per lane) when a token takes 2
+    // row instructions and that still leaves >= 2048 waves; else one token per wave in
+    // 2^split_log2 shares.
+    int tpw = 1, split_log2 = 0;
+    if (instr == 2 && (seq + 3) / 4 >= 2048) {
+        tpw = 4;
     } else {
-        launchHalvesE<T, 4>(rl, int(instr), split_log2, tp, pos, seq, ft, s);
+        split_log2 = instr >= 2 ? 1 : 0;
+        while ((instr + (size_t(1) << split_log2) - 1) >> split_log2 > 2) ++split_log2;
+        while (split_log2 > 0 && (seq << split_log2) >= (size_t(1) << 31)) --split_log2;
+    }
+    if (e == 8) {
+        if constexpr (k16) launchHalvesE<T, 8>(rl, int(instr), split_log2, tpw, tp, pos, seq, ft, s);
+    } else {
+        launchHalvesE<T, 4>(rl, int(instr), split_log2, tpw, tp, pos, seq, ft, s);
     }
     return true;
 }

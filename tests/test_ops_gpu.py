@@ -568,6 +568,7 @@ def test_config2_rope_qk_full():
     (300, 32, 8, 128, 16000, 5e5),    # config 2 heads
     (5, 3, 1, 6, 2, 1e4),             # odd half-dim: scalar kernels
     (17, 64, 64, 128, 7, 1e4),        # more items per token than the register plan holds
+    (8195, 12, 2, 128, 5, 1e4),       # four tokens per wave, the last wave's group ragged
 ])
 def test_rope_qk_equals_two_ropes(dt, seq, nhq, nhk, d, p0, theta):
     rng = np.random.default_rng(seed_of(seq, nhq, dt))
