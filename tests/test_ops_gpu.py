@@ -193,6 +193,9 @@ ROPE = [
     ((13, 8, 16), 0, 1e4),
     ((13, 2, 16), 0, 1e4),
     ((19, 8, 128), 3, 1e4),
+    # tokens packed per row instruction (one tensor filling 1/2 or 1/4 of it), ragged counts
+    ((8193, 2, 128), 7, 1e4),
+    ((8191, 1, 128), 0, 1e4),
 ]
 
 
