@@ -127,12 +127,14 @@ __C {
     /* No counterpart in the reference: llaisysSelfAttentionInt8KV for callers that cannot
      * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
      * that forbid hipMalloc).  Same arguments, checks and result bits as
-     * llaisysSelfAttentionInt8KV, but its split partials go to a file-scope device scratch
-     * of 24 MiB per GPU (held until the process ends) instead of the library workspace, and
-     * it calls no allocator.  A call whose partials exceed the scratch -- queries x q heads x
-     * (head_dim + 2) x 4 KiB, e.g. more than 47 query-heads at head_dim 128 -- fails with a
-     * message.  Calls on one GPU share the scratch: calls that overlap (other threads or
-     * streams) race. */
+     * llaisysSelfAttentionInt8KV, but its workspace is a file-scope device scratch of 24 MiB
+     * per GPU (held until the process ends) instead of the library workspace, and it calls
+     * no allocator.  Decode-shaped calls put their split partials there; one whose partials
+     * exceed the scratch -- queries x q heads x (head_dim + 2) x 4 KiB, e.g. more than 47
+     * query-heads at head_dim 128 -- fails with a message.  A bf16 prefill (16 or more
+     * queries, head_dim 128) dequantizes the caches into the scratch when they fit and
+     * otherwise converts the codes inside its kernel.  Calls on one GPU share the scratch:
+     * calls that overlap (other threads or streams) race. */
     __export void llaisysSelfAttentionInt8KVNoAlloc(llaisysTensor_t attn_val, llaisysTensor_t q,
                                                     llaisysTensor_t k_codes, llaisysTensor_t k_scale,
                                                     llaisysTensor_t v_codes, llaisysTensor_t v_scale,
