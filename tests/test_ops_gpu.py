@@ -221,6 +221,31 @@ def test_rope_shuffled_positions():
     assert_close(y.numpy(), oracle.rope(x, pos, 1e4))
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("seq,nhq,nhk", [
+    (8192, 12, 2),   # q + k, four tokens per wave
+    (8192, 2, 0),    # k alone, two tokens per row instruction
+    (64, 12, 2),     # two waves per token
+])
+def test_rope_far_angles(dt, seq, nhq, nhk):
+    """Positions up to 2^40: angles beyond the reduced-argument range (|angle| > 2^30) take
+    the device library's sincos inside each kernel layout; every fourth position is small,
+    so waves mix both paths."""
+    rng = np.random.default_rng(seed_of(seq, nhq, nhk, dt))
+    pos = rng.integers(0, 2 ** 40, size=seq).astype(np.int64)
+    pos[::4] = rng.integers(0, 4096, size=len(pos[::4]))
+    q = sample(rng, (seq, nhq, 128), dt)
+    qo = empty(q.shape, DTS[dt])
+    if nhk:
+        k = sample(rng, (seq, nhk, 128), dt)
+        ko = empty(k.shape, DTS[dt])
+        L.Ops.rope_qk(qo, dev(q, DTS[dt]), ko, dev(k, DTS[dt]), dev(pos), 1e4)
+        assert_close(ko.numpy(), oracle.rope(k, pos, 1e4), "k")
+    else:
+        L.Ops.rope(qo, dev(q, DTS[dt]), dev(pos), 1e4)
+    assert_close(qo.numpy(), oracle.rope(q, pos, 1e4), "q")
+
+
 # ---- swiglu / add ------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
@@ -885,6 +910,33 @@ def test_rms_norm_nan_eps_matches_oracle_nan_pattern():
     got = bf16_to_f32(out.numpy())
     ref = bf16_to_f32(oracle.rms_norm(x, w, float("nan")))
     assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.isnan(ref).all()
+
+
+def test_rope_kv_append_far_positions():
+    """The fused RoPE + INT8 KV append with positions up to 2^40 (the device library's sincos
+    beside the reduced-argument routine) equals llaisysROPEQK followed by the pair append."""
+    rng = np.random.default_rng(31)
+    seq, nq, nk, d = 2048, 12, 2, 128
+    q, k, v = (sample(rng, (seq, h, d), "bf16") for h in (nq, nk, nk))
+    pos = rng.integers(0, 2 ** 40, size=seq).astype(np.int64)
+    pos[::3] = np.arange(len(pos[::3]))
+    T = L.DataType.BF16
+    tq, tk, tv, tp = dev(q, T), dev(k, T), dev(v, T), dev(pos)
+    def caches():
+        return (dev(np.zeros((seq, nk, d), np.int8)), dev(np.zeros((seq, nk), np.float32)),
+                dev(np.zeros((seq, nk, d), np.int8)), dev(np.zeros((seq, nk), np.float32)))
+    kc, ks, vc, vs = caches()
+    qo = empty(q.shape, T)
+    L.Ops.rope_kv_append_int8(qo, tq, tk, tv, tp, 1e6, kc, ks, vc, vs, 0)
+    kc2, ks2, vc2, vs2 = caches()
+    qo2, ko2 = empty(q.shape, T), empty(k.shape, T)
+    L.Ops.rope_qk(qo2, tq, ko2, tk, tp, 1e6)
+    L.Ops.kv_append_int8(kc2, ks2, ko2, 0)
+    L.Ops.kv_append_int8(vc2, vs2, tv, 0)
+    for a, b, what in ((qo, qo2, "q"), (kc, kc2, "k codes"), (ks, ks2, "k scales"),
+                       (vc, vc2, "v codes"), (vs, vs2, "v scales")):
+        assert_exact(a.numpy(), b.numpy(), what)
+    assert_close(qo.numpy(), oracle.rope(q, pos, 1e6), "q vs the oracle")
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f32", "f16"])
