@@ -9,8 +9,11 @@
 // Design: pure copy, HBM-bound.  Rows of 16-byte units up to 8 KB (every config shape):
 // one wavefront gathers R rows.  Lanes 0..R-1 load the R ids in one vector load, the ids are
 // broadcast with v_readlane, and the wave issues the loads of all R rows (PL units per lane
-// per row) before any store; when every id is in range (the normal case) the stores are one
-// straight run, so each row's stores wait only for that row's loads.  R rows per wave keep
+// per row) before any store; for 3 KB rows (8 per wave) the stores start once all of them
+// have landed, so a wave's reads and writes reach HBM as two phases rather than interleaved
+// (same-box A/B, 4 runs each: 9.24-9.29 -> 9.14-9.17 us, against holding each row's stores
+// only for that row's loads), and when every id is in range (the normal case) they are one
+// straight run.  R rows per wave keep
 // R * 3 KB in flight per wave behind a single id round trip: measured on MI355X (8192
 // random ids into [151936, 1536] bf16, >= 1 GiB of rotating sets) 9.14 us with R = 8 (1024
 // waves, one per SIMD), against 9.87 / 10.15 / 9.96 / 9.33 / 9.18 us with R = 4 / 6 / 10
@@ -79,6 +82,16 @@ __global__ void __launch_bounds__(kWave)
 #pragma unroll
         for (int k = 0; k < PL; ++k)
             if (kFull || lane + k * kWave < units_per_row) r[j][k] = src[lane + k * kWave];
+    }
+    if constexpr (PL == 3) {
+        // 3 KB rows, 8 per wave: every row's loads land before the first store (the read and
+        // write phases of the wave apart); the scheduling barriers keep the compiler from
+        // moving loads below the wait.  Other plans measured slower with it: 8 KB rows, one
+        // per wave, 42.4 -> 43.6 us ([128256, 4096] x 16384); 128 f32 rows of 6 KB, 4 per
+        // wave, 2.87 -> 3.02 us.
+        __builtin_amdgcn_sched_barrier(0);
+        waitVmcnt<0>();
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (bad == 0 && row0 + R <= n_index) {
 #pragma unroll

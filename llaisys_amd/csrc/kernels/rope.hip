@@ -237,6 +237,14 @@ __global__ void __launch_bounds__(256)
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
+        // All of the pass's row loads land before the first rotation and store: the wave's
+        // reads and writes then reach HBM as two phases.  Rotating token 0 as soon as its
+        // rows arrive, its stores interleaved with the later tokens' loads, was slower:
+        // q + k at 8192 tokens 10.78-10.85 -> 10.46-10.52 us (same-box A/B, 4 runs each; on
+        // another box 10.71-10.76 -> 10.12-10.19 us).
+        __builtin_amdgcn_sched_barrier(0);
+        waitVmcnt<0>();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int tk = 0; tk < TPW; ++tk) {
             if (TPW > 1 || pass == 0) {
