@@ -277,6 +277,115 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// TPW tokens per wave with each tensor's rows of those tokens taken as one flat run: a
+// token's nh rows of one tensor sit next to the next token's in memory, so row instruction
+// k of the wave covers flat rows k * kRows .. + kRows - 1 of the run, whichever tokens they
+// belong to, and no lane of an instruction idles when a token's rows do not fill whole
+// instructions (Qwen2 q: 12 rows of 8 per instruction, 6 instructions per 4 tokens instead
+// of 8).  Instructions 0 .. i0 - 1 take tensor 0's run, the rest tensor 1's (the launcher
+// uses one tensor).  Each lane reads the (cos, sin) pairs of its own row's token.  Otherwise as
+// ropeHalves: the same rotation, the tokens' pairs computed while the loads are in flight,
+// every load landed before the first rotation and store.
+template <typename T, int RL, int E, int TPW, int I>
+__global__ void __launch_bounds__(256)
+    ropeFlat(RopePair tp, const int64_t *__restrict__ pos, size_t seq, int i0, FreqTable ft) {
+    using C = Chunk4<T, E>;
+    using V = typename C::V;
+    constexpr int kRows = kWave / RL;          // rows per wave instruction
+    constexpr int kHalf = RL * E;              // elements per half row
+    constexpr int kHalfBytes = kHalf * Fmt<T>::kBytes;
+    constexpr int kRowBytes = 2 * kHalfBytes;
+    __shared__ double2 cs[256 / kWave][TPW][kHalf]; // slot e * RL + l holds angle E l + e
+    const auto angleOf = [](int slot) { return (slot % RL) * E + slot / RL; };
+
+    const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+    const int lane = int(threadIdx.x) % kWave;
+    const size_t tbase = (size_t(blockIdx.x) * (256 / kWave) + size_t(wave)) * TPW;
+    const int rlane = lane / RL, l = lane % RL;
+    const auto tokenOf = [&](int tk) { return min(tbase + size_t(tk), seq - 1); };
+
+    // instruction k: the lane's token within the wave and its row in the tensor; a slot past
+    // the run or past the last token reads row 0 and stores nothing
+    int tkOf[I];
+    size_t rowOf[I];
+    bool ok[I];
+#pragma unroll
+    for (int k = 0; k < I; ++k) {
+        const bool t1 = k >= i0; // wave-uniform
+        const int nh = t1 ? tp.n_heads1 : tp.n_heads0;
+        const int fr = (t1 ? k - i0 : k) * kRows + rlane; // flat row within the wave's run
+        int tk = 0;
+#pragma unroll
+        for (int q = 1; q < TPW; ++q) tk += fr >= q * nh ? 1 : 0;
+        const int rr = fr - tk * nh;
+        ok[k] = rr < nh && tbase + size_t(tk) < seq;
+        tkOf[k] = tk;
+        rowOf[k] = ok[k] ? (tbase + size_t(tk)) * size_t(nh) + size_t(rr) : 0;
+    }
+    const double f_first = ft.f[angleOf(lane < kHalf ? lane : 0)];
+    __builtin_amdgcn_sched_barrier(0);
+    V xa[I], xb[I];
+#pragma unroll
+    for (int k = 0; k < I; ++k) {
+        const char *src = static_cast<const char *>(k >= i0 ? tp.in1 : tp.in0) + rowOf[k] * kRowBytes + l * C::kBytes;
+        xa[k] = C::load(src);
+        xb[k] = C::load(src + kHalfBytes);
+    }
+    bool far = false;
+#pragma unroll
+    for (int tk = 0; tk < TPW; ++tk) {
+        const int64_t p = pos[tokenOf(tk)];
+        for (int sl = lane; sl < kHalf; sl += kWave) {
+            const double ang = double(p) * (sl == lane ? f_first : ft.f[angleOf(sl)]);
+            double s0 = 0.0, c0 = 0.0;
+            if (fabs(ang) <= kSincosFastLimit)
+                sincosReduced(ang, &s0, &c0);
+            else
+                far = true; // also NaN
+            cs[wave][tk][sl] = make_double2(c0, s0);
+        }
+    }
+    if (__builtin_expect(__any(far), 0)) {
+        for (int tk = 0; tk < TPW; ++tk) {
+            const int64_t p = pos[tokenOf(tk)];
+            for (int sl = lane; sl < kHalf; sl += kWave) {
+                const double ang = double(p) * ft.f[angleOf(sl)];
+                if (!(fabs(ang) <= kSincosFastLimit)) {
+                    double s0, c0;
+                    librarySinCos(ang, &s0, &c0);
+                    cs[wave][tk][sl] = make_double2(c0, s0);
+                }
+            }
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // every row load lands before the first rotation and store (as in ropeHalves)
+    __builtin_amdgcn_sched_barrier(0);
+    waitVmcnt<0>();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < I; ++k) {
+        if (!ok[k]) continue;
+        double c[E], sn[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const double2 v = cs[wave][tkOf[k]][e * RL + l];
+            c[e] = v.x;
+            sn[e] = v.y;
+        }
+        char *dst = static_cast<char *>(k >= i0 ? tp.out1 : tp.out0) + rowOf[k] * kRowBytes + l * C::kBytes;
+        float a[E], b[E], ya[E], yb[E];
+        C::unpack(xa[k], a);
+        C::unpack(xb[k], b);
+#pragma unroll
+        for (int e = 0; e < E; ++e) rotatePair(a[e], b[e], c[e], sn[e], ya[e], yb[e]);
+        C::store(dst, C::packQ(ya));
+        C::store(dst + kHalfBytes, C::packQ(yb));
+    }
+}
+
 // One tensor whose head rows fill 1/TPI of a row instruction (k alone: 2 heads of 128 at
 // E = 4 fill half): one wave instruction covers TPI consecutive tokens, the half-pair
 // layout otherwise.  The wave computes the TPI tokens' (cos, sin) pairs, one per lane and
@@ -407,6 +516,12 @@ void launchPackedRl(int rl, const RopePair &tp, const int64_t *pos, size_t seq, 
     }
 }
 
+template <typename T, int TPW, int I>
+void launchFlat(int i0, const RopePair &tp, const int64_t *pos, size_t seq, const FreqTable &ft, hipStream_t s) {
+    const unsigned grid = blocksFor((seq + TPW - 1) / TPW, 256 / kWave);
+    ropeFlat<T, 8, 8, TPW, I><<<grid, 256, 0, s>>>(tp, pos, seq, i0, ft);
+}
+
 template <typename T, int E>
 void launchHalvesE(int rl, int instr, int split_log2, int tpw, const RopePair &tp, const int64_t *pos,
                    size_t seq, const FreqTable &ft, hipStream_t s) {
@@ -484,6 +599,24 @@ bool launchHalves(const RopePair &tp, const int64_t *pos, size_t seq, size_t hal
     // Four tokens per wave (16 loads of 16 bytes in flight per lane) when a token takes 2
     // row instructions and that still leaves >= 2048 waves; else one token per wave in
     // 2^split_log2 shares.
+    // One tensor of 9-15 rows per token in 8-row instructions of 16-byte chunks (Qwen2 q
+    // alone, as the reference's separate rope calls issue it): 4 tokens per wave as flat row
+    // runs, every row slot busy (ropeFlat).  Measured on MI355X (graph-replayed medians over
+    // >= 1 GiB of rotating sets, same-box A/B, 3 runs each): q [8192, 12, 128] 9.29-9.33 ->
+    // 9.17-9.18 us (9.35 -> 9.09-9.12 on another box); 2 tokens per wave 10.35-10.39 us, 8
+    // tokens 11.32-11.35 us.  With k in the same launch (7 instructions instead of 8) it
+    // measured slower, 10.21-10.28 -> 11.06-11.08 us, so q + k keeps ropeHalves.
+    if constexpr (k16) {
+        if (tp.n_heads1 == 0 && instr == 2 && (seq + 3) / 4 >= 2048 && e == 8 && rl == 8) {
+            const int i0 = (4 * tp.n_heads0 + 7) / 8;
+            switch (i0) {
+            case 5: launchFlat<T, 4, 5>(i0, tp, pos, seq, ft, s); return true;
+            case 6: launchFlat<T, 4, 6>(i0, tp, pos, seq, ft, s); return true;
+            case 7: launchFlat<T, 4, 7>(i0, tp, pos, seq, ft, s); return true;
+            default: break; // 8: every slot already busy
+            }
+        }
+    }
     int tpw = 1, split_log2 = 0;
     if (instr == 2 && (seq + 3) / 4 >= 2048) {
         tpw = 4;

@@ -196,6 +196,11 @@ ROPE = [
     # tokens packed per row instruction (one tensor filling 1/2 or 1/4 of it), ragged counts
     ((8193, 2, 128), 7, 1e4),
     ((8191, 1, 128), 0, 1e4),
+    # one tensor of 9-15 rows per token, 4 tokens per wave as flat row runs (16-bit types):
+    # the last wave's group ragged, 5 and 7 row instructions per wave
+    ((8195, 12, 128), 5, 1e4),
+    ((8190, 9, 128), 3, 1e4),
+    ((8189, 14, 128), 0, 1e6),
 ]
 
 
@@ -212,10 +217,13 @@ def test_rope(dt, shape, p0, theta):
     assert_close(y.numpy(), oracle.rope(x, pos, theta), f"rope {dt} {shape}")
 
 
-def test_rope_shuffled_positions():
+@pytest.mark.parametrize("shape", [(300, 2, 128), (8194, 12, 128)])
+def test_rope_shuffled_positions(shape):
+    """Random positions: a lane that took a neighbouring token's (cos, sin) pairs would
+    show (the flat row runs of the second shape put several tokens in one row instruction)."""
     rng = np.random.default_rng(14)
-    x = sample(rng, (300, 2, 128), "bf16")
-    pos = rng.integers(0, 32768, size=300).astype(np.int64)
+    x = sample(rng, shape, "bf16")
+    pos = rng.integers(0, 32768, size=shape[0]).astype(np.int64)
     y = empty(x.shape, L.DataType.BF16)
     L.Ops.rope(y, dev(x, L.DataType.BF16), dev(pos), 1e4)
     assert_close(y.numpy(), oracle.rope(x, pos, 1e4))
