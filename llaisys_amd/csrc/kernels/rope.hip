@@ -8,12 +8,17 @@
 // reference calls, so the angles are bit-identical; cos/sin come from sincos.hpp (within
 // an ulp of glibc's, which the final float rounding absorbs).
 //
-// Design: HBM-bound, no MFMA (no contraction).  Three kernels:
+// Design: HBM-bound, no MFMA (no contraction).  The kernels:
 //  * ropeHalves (most shapes): each lane holds E consecutive elements of the first half
 //    of a head row and the same E of the second half -- whole rotation pairs, so no lane
 //    needs another lane's values.  A wave takes a contiguous share of one token's head
-//    rows, computes the token's d/2 (cos, sin) pairs (one per lane) into its own LDS slice
-//    while its loads are in flight, and keeps its lanes' E pairs in registers.
+//    rows (or four tokens' rows), computes the tokens' d/2 (cos, sin) pairs (one per lane)
+//    into its own LDS slice while its loads are in flight, and keeps its lanes' E pairs in
+//    registers; every load lands before the first store.
+//  * ropeFlat (one tensor of 9-15 heads, e.g. Qwen2 q alone): the same, with four tokens'
+//    rows taken as one flat run so that no row slot of an instruction idles.
+//  * ropeHalvesPacked (one tensor filling 1/2 or 1/4 of a row instruction, e.g. k alone):
+//    several tokens per row instruction.
 //  * ropeVec (under a quarter of a wave's lanes per token, e.g. one 64-wide head): a
 //    256-thread block packs a run of tokens, computes their pairs into LDS behind a block
 //    barrier and rotates 16-byte items that fetch their partner with a cross-lane move.
@@ -22,7 +27,8 @@
 // out-of-line rare path.  Loads and stores are non-temporal (read once, written once).
 //
 // Measured on MI355X (bf16, medians of graph-replayed launches over >= 1 GiB of rotating
-// sets, one box): Qwen2 q+k at 8192 tokens 11.38 us, against 11.36-11.47 us for a copy
+// sets, one box) when the half-pair layout replaced the DPP one, before the four-token
+// waves, the two-phase order and ropeFlat: Qwen2 q+k at 8192 tokens 11.38 us, against 11.36-11.47 us for a copy
 // kernel with the same access pattern and no arithmetic, and 11.77 us for the previous
 // layout (16-byte vectors, partner fetched by DPP: every element widened twice, 560 VALU
 // instructions per token against 370 here); q alone 10.26 us (copy 9.69-9.90); k alone
