@@ -233,6 +233,7 @@ def test_rope_shuffled_positions(shape):
 @pytest.mark.parametrize("seq,nhq,nhk", [
     (8192, 12, 2),   # q + k, four tokens per wave
     (8192, 2, 0),    # k alone, two tokens per row instruction
+    (8192, 12, 0),   # q alone, four tokens per wave as flat row runs (16-bit types)
     (64, 12, 2),     # two waves per token
 ])
 def test_rope_far_angles(dt, seq, nhq, nhk):
