@@ -125,14 +125,19 @@ __global__ void __launch_bounds__(blockFor<G>())
 // vectors lane + 64 v in registers; amax by wave butterflies only (no LDS, no block
 // barrier).  Same results as quantRows.  Measured on MI355X (W[8960, 1536] bf16, graph-
 // replayed medians over >= 1 GiB of rotating sets): 8.64 us against 9.0 us for quantRows
-// with the same lane plan; V = 4 ran faster than V = 3 (8.94 us) on these 192-vector rows,
-// so the launcher uses V = 4 for rows of 65..256 vectors.  Rows of 257..1152 vectors take
+// with the same lane plan; V = 4 ran faster than V = 3 (8.94 us) on these 192-vector rows
+// while both masked the slots past the row end.  kFull (rows of exactly V * 64 vectors,
+// the wave index wave-uniform): no masks, no dead slot; the launcher takes it at V = 3 for
+// 192-vector rows, 8.70-8.82 -> 8.57-8.73 us (same-box A/B, 3 runs each; the uniform wave
+// index alone, at V = 4, measured slower: 9.26-9.44 us), V = 4 for other rows of 65..256
+// vectors.  Rows of 257..1152 vectors take
 // V = 8 / 12 / 18 in one-wavefront blocks: W[1536, 8960] 8.74 us against 9.15 us for
 // quantRows (256 lanes per row) and 9.01 / 10.18 us for 2 / 4 rows per block (at
 // W[8960, 1536] one-wavefront blocks made no difference: 8.63 against 8.67 us).
-template <typename T, int V, int B>
+template <typename T, int V, int B, bool kFull = false>
 __global__ void __launch_bounds__(B)
-    quantWave(QuantJobs jobs, int nvec) {
+    quantWave(QuantJobs jobs, int nvec_arg) {
+    const int nvec = kFull ? V * kWave : nvec_arg;
     using F = Fmt<T>;
     constexpr int N = F::kVec;
     const bool second = blockIdx.x >= jobs.nb0; // block-uniform
@@ -142,7 +147,9 @@ __global__ void __launch_bounds__(B)
     const size_t rows = second ? jobs.job[1].rows : jobs.job[0].rows;
     const unsigned blk = second ? blockIdx.x - jobs.nb0 : blockIdx.x;
     const int lane = int(threadIdx.x) % kWave;
-    const size_t row = size_t(blk) * (B / kWave) + threadIdx.x / kWave;
+    // kFull: the wave index as a wave-uniform value (with the masked slots it measured slower)
+    const int wv = kFull ? __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave) : int(threadIdx.x) / kWave;
+    const size_t row = size_t(blk) * (B / kWave) + size_t(wv);
     const bool live = row < rows;
     const size_t base = (live ? row : 0) * size_t(nvec); // in vectors
     v4u raw[V];
@@ -285,7 +292,10 @@ void launch(const QuantJob &j0, const QuantJob &j1, size_t cols, hipStream_t s) 
     if (vec && cols / N > 64 && cols / N <= 256) {
         const unsigned nb0 = blocksFor(j0.rows, 256 / kWave), nb1 = blocksFor(j1.rows, 256 / kWave);
         if (nb0 + nb1 == 0) return;
-        quantWave<T, 4, 256><<<nb0 + nb1, 256, 0, s>>>(QuantJobs{{j0, j1}, nb0}, int(cols / N));
+        if (cols / N == 192)
+            quantWave<T, 3, 256, true><<<nb0 + nb1, 256, 0, s>>>(QuantJobs{{j0, j1}, nb0}, int(cols / N));
+        else
+            quantWave<T, 4, 256><<<nb0 + nb1, 256, 0, s>>>(QuantJobs{{j0, j1}, nb0}, int(cols / N));
         return;
     }
     if (vec && cols / N > 256 && cols / N <= 18 * 64) {
