@@ -873,8 +873,9 @@ def quant_edge_rows(dt, cols=256, seed=5):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
-# one-wavefront lane groups (128, 200), lane-group plan, one wave per row (full / partial)
-@pytest.mark.parametrize("cols", [128, 200, 256, 1536, 1000, 8960])
+# one-wavefront lane groups (128, 200), lane-group plan, one wave per row (full / partial);
+# rows of exactly 192 16-byte vectors (bf16 / f16 1536, f32 768) take the exact-fit form
+@pytest.mark.parametrize("cols", [128, 200, 256, 768, 1536, 1000, 8960])
 def test_quantize_boundary_rows(dt, cols):
     x = quant_edge_rows(dt, cols=cols)
     q, s = empty(x.shape, L.DataType.I8), empty(x.shape[:-1], L.DataType.F32)
