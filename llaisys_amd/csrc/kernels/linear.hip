@@ -529,7 +529,9 @@ __global__ void __launch_bounds__(256)
 //    (larger N loses: [18944, 3584] 14.4 -> 15.3 us; bf16 [1536, 8960] 8.1 -> 8.7 us);
 //  - 4 channels per wave for INT8 rows of at most 2 chunks per lane over 65536+ channels (the
 //    lm_head), which spreads the block's x staging over 16 rows: [151936, 1536] 46.0 -> 40.0 us
-//    (at [8960, 1536] it loses, 5.45 -> 6.57 us: too few blocks);
+//    (at [8960, 1536] it loses, 5.45 -> 6.57 us: too few blocks); 2 channels per wave in
+//    4-wave blocks for such rows over 4097..65535 channels: [8960, 1536] 5.28-5.31 ->
+//    4.99-5.03 us, [17920, 1536] 7.73-7.82 -> 7.66-7.68 us (same-box A/B, 3 runs each);
 //  - waves per block: 8 where x is staged (the staging shared by more rows: bf16 [1536, 8960]
 //    8.19 -> 7.70 us, [1536, 1536] 3.10 -> 2.95 us, [8960, 1536] 6.17 -> 6.09 us; 16 waves
 //    10.5 us), 2 where it is read from L1 / L2 (INT8 [1536, 8960] 5.88 -> 5.68 us), 4 for
@@ -556,6 +558,7 @@ bool launchGemv1(const LinearArgs &a, hipStream_t s) {
     if constexpr (kInt8) {
         if (a.N <= 4096) return launchRowJ<T, true, 1, false, 2, 24>(a, j, s);
         if (a.N >= 65536 && j <= 2) return launchRowJ<T, true, 4, true, 4, 2>(a, j, s);
+        if (j <= 2) return launchRowJ<T, true, 2, true, 4, 2>(a, j, s);
     }
     return launchRowJ<T, kInt8, 1, true, 8, 24>(a, j, s);
 }
